@@ -1,0 +1,274 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused attention hot path on one MI355X.
+
+One step = one call of the Laya drop-in op (tfd_laya_attention_block_f32:
+keep packing + fused split/RoPE/attention kernel) on the ModernBERT-base
+global configuration ("C2": batch 8, seq 512,
+hidden 768, 12 heads x 64, right-padded rows), inputs resident in HBM.
+
+Prints ONE JSON line: the metric (algorithmic fused-attention TFLOP/s), its
+fraction of the f32 MFMA peak, prefill tokens/s, the dominant kernel's
+roofline (its launches timed with HIP events on the stream it runs on) and
+the CPU baseline (the oracle's restatement of the reference rayon path, timed
+on this host). The other configurations run once each under "also".
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "tenferro-decision-rs_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+F32_MFMA_PEAK = 157.3   # TFLOP/s, MI355X dense f32 matrix
+BF16_MFMA_PEAK = 2500.0  # TFLOP/s, MI355X dense bf16 matrix
+HBM_PEAK = 8000.0        # GB/s
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def time_gpu(fn, steps, warmup, ctx):
+    """(ms per step by torch events on the shared stream, avg attention-kernel ms)."""
+    import torch
+    import tenferro_ext as te
+
+    with te.asynchronous():
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        ctx.take_kernel_time()
+        ctx.set_timing(True)
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(steps):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
+        ctx.set_timing(False)
+    total, launches = ctx.take_kernel_time()
+    return start.elapsed_time(end) / steps, total / max(1, launches)
+
+
+def laya_bytes(w):
+    """Minimal I/O: q, k, v of the valid tokens' rows once, out once, keep once."""
+    return 4 * (3 * w.hidden * w.length * w.batch) + 4 * w.hidden * w.length * w.batch
+
+
+def cpu_laya(w, threads, reps=15, warmup=5):
+    import oracle
+
+    oracle.set_threads(threads)
+    times = []
+    for i in range(warmup + reps):
+        t = time.perf_counter()
+        oracle.laya_attention_block(w.qkv, w.keep, w.hidden, w.heads, w.length, w.batch, w.rope_base)
+        if i >= warmup:
+            times.append(time.perf_counter() - t)
+    return statistics.median(times)
+
+
+def cpu_jeff_rows(w, rows, threads, reps=3):
+    import oracle
+
+    oracle.set_threads(threads)
+    L, W, KW = w.length, w.heads * w.head_dim, w.kv_heads * w.head_dim
+    sl = lambda x, n: x[: rows * L * n]
+    times = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        oracle.jeff_rows(sl(w.q, W), sl(w.k, KW), sl(w.v, KW), sl(w.gate, W), w.q_norm, w.k_norm,
+                         w.mask[: rows * L], rows, L, w.heads, w.kv_heads, w.head_dim, w.rotary_dim,
+                         w.theta, w.eps)
+        times.append(time.perf_counter() - t)
+    return statistics.median(times)
+
+
+def run(args):
+    import numpy as np
+    import torch
+
+    import tenferro_ext as te
+    from tenferro_ext.workloads import jeff_config, laya_config
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    ctx = te.Context(0, stream=torch.cuda.current_stream().cuda_stream)
+    gpu_name = torch.cuda.get_device_name(0)
+
+    # ------------------------------------------------------------ C2 headline
+    w = laya_config(2)
+    pairs = w.kept_pairs()
+    flops = 4 * w.head_dim * pairs * w.heads
+    qkv = torch.from_numpy(w.qkv).to(dev)
+    keep = torch.from_numpy(w.keep).to(dev)
+    out = torch.empty(w.hidden * w.length * w.batch, dtype=torch.float32, device=dev)
+    shape = (3 * w.hidden, w.length, w.batch)
+
+    def step():
+        te.laya_attention_block(qkv, keep, w.hidden, w.heads, w.rope_base, qkv_shape=shape,
+                                ctx=ctx, out=out)
+
+    log(f"[bench] C2 drop-in: {args.warmup} warmup + {args.steps} timed steps")
+    ms, kern_ms = time_gpu(step, args.steps, args.warmup, ctx)
+    value = flops / (ms * 1e-3) / 1e12
+    achieved = flops / (kern_ms * 1e-3) / 1e12
+    tokens = w.valid_tokens()
+    result = {
+        "metric": "fused-attention TFLOP/s",
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded LCG + Box-Muller, BASELINE configs[1])",
+        "config": {"workload": "C2 ModernBERT-base global attention layer, Laya drop-in op",
+                   "batch": w.batch, "seq_len": w.length, "hidden": w.hidden, "heads": w.heads,
+                   "head_dim": w.head_dim, "rope_base": w.rope_base,
+                   "mask": "right padding, valid lengths U{64..512}, keep (L,L,B) tensor",
+                   "parallelism": "single GPU"},
+        "pct_of_f32_mfma_peak": round(100.0 * value / F32_MFMA_PEAK, 2),
+        "prefill_tokens_per_s": round(tokens / (ms * 1e-3), 1),
+        "algorithmic_flops_per_step": flops,
+        "roofline": {"bound": "mfma", "kernel": "laya_attention_kernel<64, keep bits>",
+                     "achieved": round(achieved, 3), "peak": F32_MFMA_PEAK, "unit": "TFLOP/s",
+                     "frac": round(achieved / F32_MFMA_PEAK, 4), "kernel_ms": round(kern_ms, 5),
+                     "traffic": None},
+        "gpu": gpu_name,
+    }
+
+    # ------------------------------------------------------------ other configs
+    also = {}
+    if not args.no_extra:
+        # C2 through the structured entry (no keep tensor: one kernel per step)
+        valid = torch.from_numpy(w.valid).to(dev)
+
+        def step_s():
+            te.laya_attention_structured(qkv, valid, w.hidden, w.heads, w.length, w.batch,
+                                         w.window, w.rope_base, ctx=ctx, out=out)
+
+        ms_s, k_s = time_gpu(step_s, args.steps, args.warmup, ctx)
+        also["C2_structured"] = {"ms_per_step": round(ms_s, 5), "kernel_ms": round(k_s, 5),
+                                 "tflops": round(flops / (ms_s * 1e-3) / 1e12, 3),
+                                 "kernel_tflops": round(flops / (k_s * 1e-3) / 1e12, 3)}
+        del valid
+
+        w3 = laya_config(3)
+        f3 = 4 * w3.head_dim * w3.kept_pairs() * w3.heads
+        q3 = torch.from_numpy(w3.qkv).to(dev)
+        k3 = torch.from_numpy(w3.keep).to(dev)
+        v3 = torch.from_numpy(w3.valid).to(dev)
+        o3 = torch.empty(w3.hidden * w3.length * w3.batch, dtype=torch.float32, device=dev)
+        sh3 = (3 * w3.hidden, w3.length, w3.batch)
+        ms3, k3ms = time_gpu(lambda: te.laya_attention_block(q3, k3, w3.hidden, w3.heads, w3.rope_base,
+                                                             qkv_shape=sh3, ctx=ctx, out=o3),
+                             args.steps, args.warmup, ctx)
+        ms3s, k3s = time_gpu(lambda: te.laya_attention_structured(q3, v3, w3.hidden, w3.heads, w3.length,
+                                                                  w3.batch, w3.window, w3.rope_base,
+                                                                  ctx=ctx, out=o3),
+                             args.steps, args.warmup, ctx)
+        also["C3"] = {"ms_per_step": round(ms3, 5), "kernel_ms": round(k3ms, 5),
+                      "tflops": round(f3 / (ms3 * 1e-3) / 1e12, 3),
+                      "kernel_tflops": round(f3 / (k3ms * 1e-3) / 1e12, 3),
+                      "structured_ms_per_step": round(ms3s, 5),
+                      "structured_kernel_tflops": round(f3 / (k3s * 1e-3) / 1e12, 3),
+                      "tokens_per_s": round(w3.valid_tokens() / (ms3 * 1e-3), 1),
+                      "algorithmic_flops": f3}
+        del q3, k3, v3, o3
+
+        for cfg in (4, 5):
+            wj = jeff_config(cfg)
+            fj = 4 * wj.head_dim * wj.kept_pairs() * wj.heads
+            bf = wj.bf16
+            conv = (lambda x: torch.from_numpy(te.to_bf16_bits(x).view(np.int16)).to(dev)) if bf else \
+                (lambda x: torch.from_numpy(x).to(dev))
+            tq, tk, tv, tg = (conv(getattr(wj, n)) for n in ("q", "k", "v", "gate"))
+            tqn, tkn, tm = (torch.from_numpy(getattr(wj, n)).to(dev) for n in ("q_norm", "k_norm", "mask"))
+            oj = torch.empty(wj.rows * wj.length * wj.heads * wj.head_dim, dtype=torch.float32, device=dev)
+
+            def step_j():
+                te.jeff_full_attention_rows(tq, tk, tv, tg, tqn, tkn, tm, wj.rows, wj.length, wj.heads,
+                                            wj.kv_heads, wj.head_dim, wj.rotary_dim, wj.theta, wj.eps,
+                                            bf16=bf, ctx=ctx, out=oj)
+
+            try:
+                msj, kj = time_gpu(step_j, args.steps, args.warmup, ctx)
+            except te.Unsupported as e:
+                also[f"C{cfg}"] = {"skipped": str(e)}
+                continue
+            peak = BF16_MFMA_PEAK if bf else F32_MFMA_PEAK
+            also[f"C{cfg}"] = {"ms_per_step": round(msj, 5), "kernel_ms": round(kj, 5),
+                               "tflops": round(fj / (msj * 1e-3) / 1e12, 3),
+                               "kernel_tflops": round(fj / (kj * 1e-3) / 1e12, 3),
+                               "pct_of_peak": round(100.0 * fj / (kj * 1e-3) / 1e12 / peak, 2),
+                               "peak": peak, "dtype": "bf16" if bf else "f32",
+                               "tokens_per_s": round(wj.valid_tokens() / (msj * 1e-3), 1),
+                               "algorithmic_flops": fj}
+            if cfg == 4 and not args.no_cpu:
+                cores = min(16, os.cpu_count() or 1)
+                t = cpu_jeff_rows(wj, 2, cores)
+                also["C4"]["cpu_port_tokens_per_s"] = round(
+                    float((wj.mask[: 2 * wj.length] != 0).sum()) / t, 1)
+                also["C4"]["cpu_port_sample"] = f"2 of 16 rows, median of 3, {cores} threads"
+            del tq, tk, tv, tg, tqn, tkn, tm, oj
+    result["also"] = also
+
+    # ------------------------------------------------------------ CPU baseline
+    if not args.no_cpu:
+        cores = min(16, os.cpu_count() or 1)
+        log(f"[bench] CPU baseline: oracle port of the rayon path, {cores} threads")
+        t_all = cpu_laya(w, cores)
+        t_8 = cpu_laya(w, 8) if cores != 8 else t_all
+        result["cpu_baseline"] = {
+            "value": round(flops / t_all / 1e12, 5), "unit": "TFLOP/s", "cores": cores,
+            "kind": "port",
+            "sample": "full C2 workload per call, median of 15 after 5 warmups",
+            "ms": round(t_all * 1e3, 3),
+            "tokens_per_s": round(tokens / t_all, 1),
+            "ms_8_threads": round(t_8 * 1e3, 3),
+            "cpu": _cpu_model(),
+        }
+        result["gpu_over_cpu"] = round(value / (flops / t_all / 1e12), 1)
+    ctx.close()
+    return result
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-extra", action="store_true", help="only the C2 headline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)",
+              file=sys.stderr)
+        sys.exit(2)
+    print(json.dumps(run(args)), flush=True)
+
+
+if __name__ == "__main__":
+    main()

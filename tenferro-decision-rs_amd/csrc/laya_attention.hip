@@ -1,0 +1,307 @@
+// Laya fused split + RoPE + masked attention on gfx950 f32 matrix cores.
+//
+// Arithmetic follows cpu-kernels laya_attention_block_with_workspace
+// (crates/cpu-kernels/src/lib.rs:843-1156): RoPE on q and k from a host-built
+// f32 table (874-888), s = (q.k) * (1/sqrt(hd)) (1124), masked softmax
+// (1111-1136), out = sum p*v with p == 0 never multiplying a value (1143-1151),
+// NaN for a query that keeps no key (1025-1033, 1143-1151).
+//
+// One workgroup = 4 wavefronts = 128 queries of one (batch, head). Each
+// wavefront owns 32 queries and walks 32-key tiles:
+//   S^T (32 keys x 32 queries) = K_tile * Q^T      (hd/2 MFMA 32x32x2)
+//   O^T (hd x 32 queries)     += V_tile^T * P^T     (hd/32 x 16 MFMA 32x32x2)
+// Computing S^T rather than S puts each lane's 16 probabilities exactly where
+// the B operand of the P.V product wants them, so no shuffles sit between the
+// two products. Q (rotated) stays in registers for the whole walk; K (rotated
+// while staged) and V tiles go through LDS and are shared by the 4 waves.
+// Key tiles outside the workgroup's key span are never visited; a wave whose
+// 32 queries keep nothing in a tile skips its MFMAs.
+#include "tfd_device.hpp"
+#include "tfd_internal.hpp"
+
+namespace tfd {
+
+// ---------------------------------------------------------------- keep bits
+
+// Packs the (L, L, B) byte keep tensor into one 32-bit word per
+// (batch, key tile, query): bit j set when key 32*kt + j is kept.
+__global__ __launch_bounds__(256) void laya_keep_bits_kernel(const uint8_t *__restrict__ keep,
+                                                             uint32_t *__restrict__ bits, int L,
+                                                             int nkt) {
+  const int q = blockIdx.x * blockDim.x + threadIdx.x;
+  const int kt = blockIdx.y, b = blockIdx.z;
+  if (q >= L) return;
+  const uint8_t *base = keep + (size_t)L * L * b + q;
+  const int k0 = kt * kKeyTile;
+  const int n = min(kKeyTile, L - k0);
+  uint32_t w = 0;
+  for (int kk = 0; kk < n; ++kk) w |= (uint32_t)(base[(size_t)L * (k0 + kk)] != 0) << kk;
+  bits[((size_t)b * nkt + kt) * L + q] = w;
+}
+
+// ------------------------------------------------------------------ helpers
+
+// Element dd of the head's RoPE-rotated row (lib.rs:991-1010): pairs
+// (i, i + half) for i < half, x[i]*c - x[i+half]*s and x[i]*s + x[i+half]*c,
+// evaluated without contraction like the reference. dd >= hd pads with 0.
+__device__ __forceinline__ float rope_elem(const float *row, int dd, int hd, int half,
+                                           const float *cr, const float *sr) {
+#pragma clang fp contract(off)
+  if (dd >= hd) return 0.0f;
+  const float x = row[dd];
+  if (cr == nullptr) return x;
+  if (dd < half) return x * cr[dd] - row[dd + half] * sr[dd];
+  if (dd < 2 * half) {
+    const int i = dd - half;
+    return row[i] * sr[i] + x * cr[i];
+  }
+  return x;
+}
+
+// ------------------------------------------------------------------- kernel
+
+template <int HDP, int MODE>
+__global__ __launch_bounds__(256) void laya_attention_kernel(const LayaArgs a) {
+  constexpr int KS = HDP + 4;  // K row stride (floats): 16-byte rows, conflict-free b128 reads
+  constexpr int VS = HDP + 8;  // V row stride: the two lane halves read rows 4 apart
+  constexpr int QS = HDP / 2;  // Q registers per lane
+  constexpr int NB = HDP / 32; // 32-row blocks of O^T
+  __shared__ __attribute__((aligned(16))) float Ks[kKeyTile * KS];
+  __shared__ __attribute__((aligned(16))) float Vs[kKeyTile * VS];
+  __shared__ int s_span[3];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int col = lane & 31, half = lane >> 5;
+  const int head = blockIdx.y, b = blockIdx.z;
+  const int L = a.L, hd = a.hd, hh = a.half, nkt = a.nkt;
+  const int qg0 = blockIdx.x * kLayaGroupQueries;
+  const int q = qg0 + wave * kWaveQueries + col;
+  const bool qin = q < L;
+  const size_t tok = 3 * (size_t)a.d;
+  const float *xb = a.qkv + (size_t)b * L * tok + (size_t)head * hd;
+  const bool rope = a.cos_t != nullptr;
+
+  // -------- key span of the workgroup
+  if (tid == 0) {
+    s_span[0] = 0x7fffffff;
+    s_span[1] = -1;
+    s_span[2] = 0;
+  }
+  __syncthreads();
+  if (MODE == kMaskBits) {
+    int lo = 0x7fffffff, hi = -1;
+    for (int i = tid; i < kLayaGroupQueries * nkt; i += 256) {
+      const int qq = qg0 + (i & (kLayaGroupQueries - 1));
+      const int kt = i / kLayaGroupQueries;
+      if (qq < L && a.bits[((size_t)b * nkt + kt) * L + qq] != 0u) {
+        lo = min(lo, kt);
+        hi = max(hi, kt);
+      }
+    }
+    lo = wave_min(lo);
+    hi = wave_max(hi);
+    if (lane == 0) {
+      atomicMin(&s_span[0], lo);
+      atomicMax(&s_span[1], hi);
+    }
+  } else {
+    const uint8_t *vb = a.valid + (size_t)b * L;
+    int lo = 0x7fffffff, hi = -1, padded = 0;
+    for (int k = tid; k < L; k += 256) {
+      if (vb[k]) {
+        lo = min(lo, k);
+        hi = max(hi, k);
+      }
+    }
+    if (tid < kLayaGroupQueries) {
+      const int qq = qg0 + tid;
+      padded = (qq < L && !vb[qq]) ? 1 : 0;
+    }
+    lo = wave_min(lo);
+    hi = wave_max(hi);
+    padded = wave_max(padded);
+    if (lane == 0) {
+      atomicMin(&s_span[0], lo);
+      atomicMax(&s_span[1], hi);
+      atomicMax(&s_span[2], padded);
+    }
+  }
+  __syncthreads();
+  int kt_begin = 0, kt_end = 0;
+  if (MODE == kMaskBits) {
+    if (s_span[1] >= 0) {
+      kt_begin = s_span[0];
+      kt_end = s_span[1] + 1;
+    }
+  } else {
+    int kf = s_span[0], kl = s_span[1];
+    // A padded query keeps every valid key (build_mask), so only a tile of
+    // valid queries narrows to the window.
+    if (a.window >= 0 && s_span[2] == 0 && kl >= 0) {
+      kf = max(kf, qg0 - a.window);
+      kl = min(kl, min(qg0 + kLayaGroupQueries - 1, L - 1) + a.window);
+    }
+    if (kl >= 0 && kf <= kl) {
+      kt_begin = kf / kKeyTile;
+      kt_end = kl / kKeyTile + 1;
+    }
+  }
+
+  // -------- Q: rotated, in registers. Lane (col, half) holds
+  // Q[q][half*QS + s] for s < QS, the B operand of step s.
+  float qreg[QS];
+  {
+    const int qq = qin ? q : 0;
+    const float *row = xb + (size_t)qq * tok;
+    const float *cr = rope ? a.cos_t + (size_t)qq * hh : nullptr;
+    const float *sr = rope ? a.sin_t + (size_t)qq * hh : nullptr;
+#pragma unroll
+    for (int s = 0; s < QS; ++s) qreg[s] = qin ? rope_elem(row, half * QS + s, hd, hh, cr, sr) : 0.0f;
+  }
+  bool q_valid = false;
+  if (MODE == kMaskStruct) q_valid = qin && a.valid[(size_t)b * L + q] != 0;
+
+  f32x16 O[NB];
+#pragma unroll
+  for (int j = 0; j < NB; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) O[j][r] = 0.0f;
+  float m = -INFINITY, l = 0.0f;
+
+  for (int kt = kt_begin; kt < kt_end; ++kt) {
+    const int k0 = kt * kKeyTile;
+    // -------- stage K (rotated) and V (as is; the MFMA product only runs on
+    // tiles whose V is all finite)
+    int nonfinite = 0;
+    for (int e = tid; e < kKeyTile * HDP; e += 256) {
+      const int kk = e / HDP, dd = e % HDP;
+      const int key = k0 + kk;
+      float kv = 0.0f, vv = 0.0f;
+      if (key < L && dd < hd) {
+        const float *row = xb + (size_t)key * tok;
+        const float *cr = rope ? a.cos_t + (size_t)key * hh : nullptr;
+        const float *sr = rope ? a.sin_t + (size_t)key * hh : nullptr;
+        kv = rope_elem(row + a.d, dd, hd, hh, cr, sr);
+        vv = row[2 * a.d + dd];
+        nonfinite |= !__builtin_isfinite(vv);
+      }
+      Ks[kk * KS + dd] = kv;
+      Vs[kk * VS + dd] = vv;
+    }
+    // -------- this lane's keep word for the tile
+    uint32_t w = 0u;
+    if (MODE == kMaskBits) {
+      if (qin) w = a.bits[((size_t)b * nkt + kt) * L + q];
+    } else {
+      const int key = k0 + col;
+      const bool kv = key < L && a.valid[(size_t)b * L + key] != 0;
+      const uint32_t vbits = (uint32_t)__ballot(kv);  // lanes 0..31 = keys of the tile
+      if (qin) {
+        w = vbits;
+        if (a.window >= 0 && q_valid) w &= range_bits(q - a.window - k0, q + a.window - k0);
+      }
+    }
+    const int nf = __syncthreads_or(nonfinite);
+
+    if (__ballot(w != 0u) != 0) {  // wave-uniform: skip tiles this wave never keeps
+      f32x16 s;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[r] = 0.0f;
+      const f32x4 *krow = reinterpret_cast<const f32x4 *>(&Ks[col * KS + half * QS]);
+#pragma unroll
+      for (int c = 0; c < QS / 4; ++c) {
+        const f32x4 kv = krow[c];
+        s = mfma_32x32x2(kv[0], qreg[4 * c + 0], s);
+        s = mfma_32x32x2(kv[1], qreg[4 * c + 1], s);
+        s = mfma_32x32x2(kv[2], qreg[4 * c + 2], s);
+        s = mfma_32x32x2(kv[3], qreg[4 * c + 3], s);
+      }
+      const float alpha = softmax_tile(s, w, half, a.c1, m, l);
+      if (alpha != 1.0f) {
+#pragma unroll
+        for (int j = 0; j < NB; ++j) O[j] *= alpha;
+      }
+      if (!nf) {
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            O[j] = mfma_32x32x2(Vs[acc_row(r, half) * VS + j * 32 + col], s[r], O[j]);
+      } else {
+        // A value in this tile is NaN or infinite: accumulate key by key and
+        // skip zero probabilities, as the reference's scalar path does
+        // (lib.rs:1143-1151), so a masked non-finite value never leaks.
+        for (int kk = 0; kk < kKeyTile; ++kk) {
+          const float p = tile_prob(s, kk, col);
+          if (p == 0.0f) continue;
+#pragma unroll
+          for (int j = 0; j < NB; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) O[j][r] += p * Vs[kk * VS + j * 32 + acc_row(r, half)];
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  // -------- normalize and store: out[feat + d + hidden*(q + L*b)]
+  const float lt = l + __shfl_xor(l, 32);
+  if (qin) {
+    float *orow = a.out + ((size_t)b * L + q) * a.d + (size_t)head * hd;
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int dd = j * 32 + acc_row(r, half);
+        if (dd < hd) orow[dd] = O[j][r] / lt;
+      }
+  }
+}
+
+// Writes zeros (a kernel rather than a memset, so callers may capture it in a
+// graph).
+__global__ __launch_bounds__(256) void fill_zero_kernel(float *__restrict__ out, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x)
+    out[i] = 0.0f;
+}
+
+// ----------------------------------------------------------------- launchers
+
+hipError_t launch_fill_zero(float *out, size_t n, hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  size_t blocks = (n + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, out, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_laya_keep_bits(const uint8_t *keep, uint32_t *bits, int L, int B, int nkt,
+                                 hipStream_t stream) {
+  dim3 grid((L + 255) / 256, nkt, B);
+  hipLaunchKernelGGL(laya_keep_bits_kernel, grid, dim3(256), 0, stream, keep, bits, L, nkt);
+  return hipGetLastError();
+}
+
+template <int HDP>
+static hipError_t launch_laya_hd(const LayaArgs &a, int heads, int batch, int mode,
+                                 hipStream_t stream) {
+  dim3 grid((a.L + kLayaGroupQueries - 1) / kLayaGroupQueries, heads, batch);
+  if (mode == kMaskBits)
+    hipLaunchKernelGGL((laya_attention_kernel<HDP, kMaskBits>), grid, dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL((laya_attention_kernel<HDP, kMaskStruct>), grid, dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_laya_attention(const LayaArgs &a, int heads, int batch, int hd_pad, int mode,
+                                 hipStream_t stream) {
+  switch (hd_pad) {
+    case 32: return launch_laya_hd<32>(a, heads, batch, mode, stream);
+    case 64: return launch_laya_hd<64>(a, heads, batch, mode, stream);
+    case 128: return launch_laya_hd<128>(a, heads, batch, mode, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace tfd

@@ -1,0 +1,139 @@
+// Device helpers shared by the gfx950 attention kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tfd {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// D(32x32) += A(32x2) * B(2x32) on the f32 matrix cores.
+// Lane l supplies A[l%32][l/32] and B[l/32][l%32]; D row for accumulator r is
+// acc_row(r, l/32), D column is l%32.
+__device__ __forceinline__ f32x16 mfma_32x32x2(float a, float b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// D(16x16) += A(16x4) * B(4x16). Lane l supplies A[l%16][l/16] and
+// B[l/16][l%16]; accumulator r holds D[4*(l/16) + r][l%16].
+__device__ __forceinline__ f32x4 mfma_16x16x4(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ int acc_row(int r, int half) {
+  return 8 * (r >> 2) + 4 * half + (r & 3);
+}
+
+// Bits j of a 32-key word with lo <= j <= hi (clamped to the word).
+__device__ __forceinline__ uint32_t range_bits(int lo, int hi) {
+  lo = lo < 0 ? 0 : lo;
+  hi = hi > 31 ? 31 : hi;
+  if (lo > hi) return 0u;
+  uint32_t upper = hi == 31 ? 0xffffffffu : ((1u << (hi + 1)) - 1u);
+  return upper & ~((1u << lo) - 1u);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ int wave_min(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o));
+  return v;
+}
+
+__device__ __forceinline__ int wave_max(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o));
+  return v;
+}
+
+// Online-softmax step on one 32-key tile held as the S^T accumulators of a
+// lane (its query = lane%32, its 16 keys = acc_row(r, lane/32)). Follows the
+// reference's masked softmax (cpu-kernels lib.rs:1111-1136): masked or
+// non-finite scores contribute 0 and never raise the running max, a +inf
+// score makes the row's sum 0. Scores are kept in the log2 domain
+// (x = acc * c1 with c1 = scale*log2(e)), so exp(score - max) = exp2(x - m).
+// On return s holds the unnormalized probabilities, m/l are updated and
+// alpha is the factor the output accumulators must be scaled by.
+__device__ __forceinline__ float softmax_tile(f32x16 &s, uint32_t keep, int half, float c1,
+                                              float &m, float &l) {
+  float mx = -INFINITY;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    bool kept = (keep >> acc_row(r, half)) & 1u;
+    float x = kept ? s[r] * c1 : -INFINITY;
+    s[r] = x;
+    mx = fmaxf(mx, x);
+  }
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  const float mn = fmaxf(m, mx);
+  const float alpha = (m == mn) ? 1.0f : fast_exp2(m - mn);
+  float rs = 0.0f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    float x = s[r];
+    float e = __builtin_isfinite(x) ? fast_exp2(x - mn) : 0.0f;
+    s[r] = e;
+    rs += e;
+  }
+  l = l * alpha + rs;
+  m = mn;
+  return alpha;
+}
+
+// Probability of key kk (0..31) of the tile for this lane's query, fetched
+// from whichever lane half holds it.
+__device__ __forceinline__ float tile_prob(const f32x16 &s, int kk, int col) {
+  const int r = ((kk >> 3) << 2) | (kk & 3);
+  const int src_half = (kk >> 2) & 1;
+  float sel = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) sel = (i == r) ? s[i] : sel;
+  return __shfl(sel, col + 32 * src_half);
+}
+
+// softmax_tile for the 16x16 layout: a 32-key tile is two S^T blocks,
+// s0 (keys 0..15) and s1 (keys 16..31); lane group g = lane/16 holds keys
+// 16*b + 4*g + r of its query lane%16.
+__device__ __forceinline__ float softmax_tile16(f32x4 &s0, f32x4 &s1, uint32_t keep, int grp,
+                                                float c1, float &m, float &l) {
+  float mx = -INFINITY;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int k = 4 * grp + r;
+    const float x0 = ((keep >> k) & 1u) ? s0[r] * c1 : -INFINITY;
+    const float x1 = ((keep >> (16 + k)) & 1u) ? s1[r] * c1 : -INFINITY;
+    s0[r] = x0;
+    s1[r] = x1;
+    mx = fmaxf(mx, fmaxf(x0, x1));
+  }
+  mx = fmaxf(mx, __shfl_xor(mx, 16));
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  const float mn = fmaxf(m, mx);
+  const float alpha = (m == mn) ? 1.0f : fast_exp2(m - mn);
+  float rs = 0.0f;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float e0 = __builtin_isfinite(s0[r]) ? fast_exp2(s0[r] - mn) : 0.0f;
+    const float e1 = __builtin_isfinite(s1[r]) ? fast_exp2(s1[r] - mn) : 0.0f;
+    s0[r] = e0;
+    s1[r] = e1;
+    rs += e0 + e1;
+  }
+  l = l * alpha + rs;
+  m = mn;
+  return alpha;
+}
+
+// Probability of key kx (0..31) for this lane's query in the 16x16 layout.
+__device__ __forceinline__ float tile_prob16(const f32x4 &s0, const f32x4 &s1, int kx, int col) {
+  const int kl = kx & 15, r = kl & 3, g = kl >> 2;
+  float sel = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) sel = (i == r) ? ((kx >> 4) ? s1[i] : s0[i]) : sel;
+  return __shfl(sel, col + 16 * g);
+}
+
+}  // namespace tfd

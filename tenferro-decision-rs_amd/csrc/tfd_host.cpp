@@ -1,0 +1,625 @@
+// Host side of the C ABI declared in include/tfd_attention.h.
+//
+// Mirrors the reference extension ops' execute_in_session:
+//   Laya: crates/tenferro-ext/src/laya_attention.rs:99-176
+//   Jeff: crates/tenferro-ext/src/jeff_attention.rs:103-184
+// including their validation order and messages, then runs the gfx950
+// kernels on the context's stream. No CPU fallback exists: every failure to
+// reach the GPU is reported as TFD_EHIP.
+#include "tfd_attention.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "tfd_internal.hpp"
+
+namespace {
+
+constexpr const char *kLayaFamily = "tenferro-decision.laya_attention_block.v1";
+constexpr const char *kJeffFamily = "tenferro-decision.jeff_full_attention.v1";
+constexpr const char *kLayaOp = "tenferro-ext::laya_attention_block";
+constexpr const char *kJeffOp = "tenferro-ext::jeff_full_attention";
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr size_t kRopeCacheEntries = 8;
+
+struct DevBuf {
+  void *ptr = nullptr;
+  size_t cap = 0;
+};
+
+struct RopeEntry {
+  int kind = 0;  // 0 = Laya (L, hd/2), 1 = Jeff (L, rot/2)
+  size_t length = 0, dim = 0;
+  uint32_t bits = 0;
+  float *cos_d = nullptr, *sin_d = nullptr;
+  size_t bytes = 0;
+  uint64_t stamp = 0;
+};
+
+}  // namespace
+
+struct tfd_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  bool own_stream = false;
+  bool ready = false;
+  std::string err;
+  DevBuf staging[8];  // uploads of host-pointer operands
+  DevBuf bits;        // Laya packed keep words
+  std::vector<RopeEntry> rope;
+  uint64_t clock = 0;
+  bool timing = false;
+  std::vector<hipEvent_t> events;  // pairs: [2i] before, [2i+1] after launch i
+  size_t events_used = 0;
+};
+
+namespace {
+
+int fail(tfd_ctx *c, int code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  c->err = buf;
+  return code;
+}
+
+// invalid_argument(op, field, message) of the reference.
+int invalid(tfd_ctx *c, const char *op, const char *field, const char *msg) {
+  return fail(c, TFD_EINVAL, "%s: invalid argument `%s`: %s", op, field, msg);
+}
+
+int hip_fail(tfd_ctx *c, hipError_t e, const char *what) {
+  return fail(c, TFD_EHIP, "%s: %s (%s)", what, hipGetErrorString(e), hipGetErrorName(e));
+}
+
+#define TFD_HIP(c, expr, what)                \
+  do {                                        \
+    hipError_t e_ = (expr);                   \
+    if (e_ != hipSuccess) return hip_fail((c), e_, (what)); \
+  } while (0)
+
+bool mul_ok(size_t a, size_t b, size_t *out) {
+  if (a != 0 && b > SIZE_MAX / a) return false;
+  *out = a * b;
+  return true;
+}
+
+int ensure_ready(tfd_ctx *c) {
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess || count == 0)
+    return fail(c, TFD_EHIP, "no HIP device available (%s); tfd has no CPU fallback",
+                e == hipSuccess ? "0 devices" : hipGetErrorString(e));
+  if (c->device < 0 || c->device >= count)
+    return fail(c, TFD_EHIP, "device %d out of range (%d devices)", c->device, count);
+  TFD_HIP(c, hipSetDevice(c->device), "hipSetDevice");
+  if (!c->ready) {
+    if (c->stream == nullptr) {
+      TFD_HIP(c, hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreate");
+      c->own_stream = true;
+    }
+    c->ready = true;
+  }
+  return TFD_OK;
+}
+
+int reserve(tfd_ctx *c, DevBuf &b, size_t bytes) {
+  if (bytes <= b.cap) return TFD_OK;
+  if (b.ptr) {
+    TFD_HIP(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    TFD_HIP(c, hipFree(b.ptr), "hipFree");
+    b.ptr = nullptr;
+    b.cap = 0;
+  }
+  size_t cap = bytes < 256 ? 256 : bytes;
+  TFD_HIP(c, hipMalloc(&b.ptr, cap), "hipMalloc");
+  b.cap = cap;
+  return TFD_OK;
+}
+
+// Device operand: the caller's pointer, or an upload of the host buffer into
+// staging slot `slot`.
+int operand(tfd_ctx *c, unsigned flags, int slot, const void *host_or_dev, size_t bytes,
+            const void **dev) {
+  if (flags & TFD_DEVICE_PTRS) {
+    *dev = host_or_dev;
+    return TFD_OK;
+  }
+  int rc = reserve(c, c->staging[slot], bytes);
+  if (rc) return rc;
+  if (bytes)
+    TFD_HIP(c, hipMemcpyAsync(c->staging[slot].ptr, host_or_dev, bytes, hipMemcpyHostToDevice,
+                              c->stream),
+            "hipMemcpyAsync H2D");
+  *dev = c->staging[slot].ptr;
+  return TFD_OK;
+}
+
+int output(tfd_ctx *c, unsigned flags, int slot, void *host_or_dev, size_t bytes, void **dev) {
+  if (flags & TFD_DEVICE_PTRS) {
+    *dev = host_or_dev;
+    return TFD_OK;
+  }
+  int rc = reserve(c, c->staging[slot], bytes);
+  if (rc) return rc;
+  *dev = c->staging[slot].ptr;
+  return TFD_OK;
+}
+
+int finish(tfd_ctx *c, unsigned flags, void *host_out, const void *dev_out, size_t bytes) {
+  if (!(flags & TFD_DEVICE_PTRS)) {
+    if (bytes)
+      TFD_HIP(c, hipMemcpyAsync(host_out, dev_out, bytes, hipMemcpyDeviceToHost, c->stream),
+              "hipMemcpyAsync D2H");
+    TFD_HIP(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return TFD_OK;
+  }
+  if (!(flags & TFD_ASYNC)) TFD_HIP(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  return TFD_OK;
+}
+
+// RoPE tables. Laya (cpu-kernels lib.rs:874-888): theta = (l as f32) *
+// base.powf(-2 i / hd) for i < hd/2. Jeff (lib.rs:692-709): angle = (t as
+// f32) * theta.powf(-2 i / rot) for i < rot/2. Both in f32 with the C
+// library's powf/cosf/sinf, which is what Rust's f32 methods call on
+// linux-gnu.
+int rope_table(tfd_ctx *c, int kind, size_t length, size_t dim, float base, uint32_t bits,
+               const float **cos_d, const float **sin_d) {
+  const size_t half = dim / 2;
+  for (auto &e : c->rope) {
+    if (e.kind == kind && e.length == length && e.dim == dim && e.bits == bits) {
+      e.stamp = ++c->clock;
+      *cos_d = e.cos_d;
+      *sin_d = e.sin_d;
+      return TFD_OK;
+    }
+  }
+  std::vector<float> ct(length * half + 1), st(length * half + 1);
+  for (size_t l = 0; l < length; ++l) {
+    for (size_t i = 0; i < half; ++i) {
+      volatile float expo = -2.0f * (float)i / (float)dim;
+      volatile float angle = (float)l * powf(base, expo);
+      ct[l * half + i] = cosf(angle);
+      st[l * half + i] = sinf(angle);
+    }
+  }
+  RopeEntry ent;
+  if (c->rope.size() >= kRopeCacheEntries) {
+    size_t victim = 0;
+    for (size_t i = 1; i < c->rope.size(); ++i)
+      if (c->rope[i].stamp < c->rope[victim].stamp) victim = i;
+    TFD_HIP(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    TFD_HIP(c, hipFree(c->rope[victim].cos_d), "hipFree");
+    TFD_HIP(c, hipFree(c->rope[victim].sin_d), "hipFree");
+    c->rope.erase(c->rope.begin() + victim);
+  }
+  ent.kind = kind;
+  ent.length = length;
+  ent.dim = dim;
+  ent.bits = bits;
+  ent.bytes = 2 * sizeof(float) * ct.size();
+  TFD_HIP(c, hipMalloc((void **)&ent.cos_d, sizeof(float) * ct.size()), "hipMalloc");
+  TFD_HIP(c, hipMalloc((void **)&ent.sin_d, sizeof(float) * st.size()), "hipMalloc");
+  TFD_HIP(c, hipMemcpy(ent.cos_d, ct.data(), sizeof(float) * ct.size(), hipMemcpyHostToDevice),
+          "hipMemcpy rope");
+  TFD_HIP(c, hipMemcpy(ent.sin_d, st.data(), sizeof(float) * st.size(), hipMemcpyHostToDevice),
+          "hipMemcpy rope");
+  ent.stamp = ++c->clock;
+  c->rope.push_back(ent);
+  *cos_d = ent.cos_d;
+  *sin_d = ent.sin_d;
+  return TFD_OK;
+}
+
+// Event pair around the next attention-kernel launch (timing enabled only).
+int timing_begin(tfd_ctx *c, hipEvent_t *after) {
+  *after = nullptr;
+  if (!c->timing) return TFD_OK;
+  while (c->events.size() < 2 * (c->events_used + 1)) {
+    hipEvent_t e;
+    TFD_HIP(c, hipEventCreate(&e), "hipEventCreate");
+    c->events.push_back(e);
+  }
+  TFD_HIP(c, hipEventRecord(c->events[2 * c->events_used], c->stream), "hipEventRecord");
+  *after = c->events[2 * c->events_used + 1];
+  c->events_used++;
+  return TFD_OK;
+}
+
+int timing_end(tfd_ctx *c, hipEvent_t after) {
+  if (after) TFD_HIP(c, hipEventRecord(after, c->stream), "hipEventRecord");
+  return TFD_OK;
+}
+
+int pad_head_dim(size_t hd, size_t max_hd) {
+  if (hd > max_hd) return 0;
+  if (hd <= 32) return 32;
+  if (hd <= 64) return 64;
+  if (hd <= 128) return 128;
+  return 256;
+}
+
+float bits_to_f32(uint32_t b) {
+  float f;
+  std::memcpy(&f, &b, sizeof f);
+  return f;
+}
+
+int check_flags(tfd_ctx *c, const char *op, unsigned flags, unsigned allowed) {
+  if (flags & ~allowed) return invalid(c, op, "flags", "unknown flag bits");
+  if ((flags & TFD_ASYNC) && !(flags & TFD_DEVICE_PTRS))
+    return invalid(c, op, "flags", "TFD_ASYNC requires TFD_DEVICE_PTRS");
+  return TFD_OK;
+}
+
+// ------------------------------------------------------------------ Laya run
+
+int laya_run(tfd_ctx *c, const char *op, const float *qkv, const uint8_t *keep,
+             const uint8_t *valid, int64_t window, size_t hidden, size_t heads, size_t length,
+             size_t batch, uint32_t rope_bits, float *out, unsigned flags) {
+  size_t n = 0, n3 = 0, keep_len = 0, valid_len = 0;
+  if (!mul_ok(hidden, length, &n) || !mul_ok(n, batch, &n) || !mul_ok(n, 3, &n3) ||
+      !mul_ok(length, length, &keep_len) || !mul_ok(keep_len, batch, &keep_len) ||
+      !mul_ok(length, batch, &valid_len))
+    return invalid(c, op, "shape", "attention dimensions overflow");
+  if (n == 0) return TFD_OK;
+  const bool zero_fill = heads == 0 || hidden % heads != 0;
+  const size_t hd = zero_fill ? 0 : hidden / heads;
+  int hd_pad = zero_fill ? 32 : pad_head_dim(hd, 128);
+  if (!hd_pad)
+    return fail(c, TFD_EUNSUPPORTED, "%s: head_dim %zu exceeds the supported 128", op, hd);
+  if (length > (size_t)INT32_MAX / 4 || hidden > (size_t)INT32_MAX / 4)
+    return fail(c, TFD_EUNSUPPORTED, "%s: length/hidden too large for the kernels", op);
+  if (heads > 65535 || batch > 65535 || (length + tfd::kKeyTile - 1) / tfd::kKeyTile > 65535)
+    return fail(c, TFD_EUNSUPPORTED, "%s: heads/batch/length exceed the launch grid", op);
+  int rc = ensure_ready(c);
+  if (rc) return rc;
+  void *out_d = nullptr;
+  if ((rc = output(c, flags, 0, out, sizeof(float) * n, &out_d))) return rc;
+  if (zero_fill) {
+    // laya_attention.rs:141 allocates zeros and the kernel returns early
+    // (lib.rs:870-872) when heads == 0 or d % heads != 0.
+    TFD_HIP(c, tfd::launch_fill_zero(static_cast<float *>(out_d), n, c->stream), "fill launch");
+    return finish(c, flags, out, out_d, sizeof(float) * n);
+  }
+  const void *qkv_d = nullptr, *mask_d = nullptr;
+  if ((rc = operand(c, flags, 1, qkv, sizeof(float) * n3, &qkv_d))) return rc;
+  if (keep) {
+    if ((rc = operand(c, flags, 2, keep, keep_len, &mask_d))) return rc;
+  } else {
+    if ((rc = operand(c, flags, 2, valid, valid_len, &mask_d))) return rc;
+  }
+  tfd::LayaArgs a{};
+  a.qkv = static_cast<const float *>(qkv_d);
+  a.out = static_cast<float *>(out_d);
+  a.d = (int)hidden;
+  a.hd = (int)hd;
+  a.half = (int)(hd / 2);
+  a.L = (int)length;
+  a.nkt = (int)((length + tfd::kKeyTile - 1) / tfd::kKeyTile);
+  a.window = window < 0 ? -1 : (int)(window > (int64_t)length ? (int64_t)length : window);
+  const float scale = 1.0f / sqrtf((float)hd);
+  a.c1 = scale * kLog2e;
+  const float base = bits_to_f32(rope_bits);
+  if (base != 0.0f) {
+    if ((rc = rope_table(c, 0, length, hd, base, rope_bits, &a.cos_t, &a.sin_t))) return rc;
+  }
+  int mode = tfd::kMaskStruct;
+  if (keep) {
+    mode = tfd::kMaskBits;
+    size_t words = 0;
+    if (!mul_ok((size_t)a.nkt * batch, length, &words))
+      return invalid(c, op, "shape", "attention dimensions overflow");
+    if ((rc = reserve(c, c->bits, sizeof(uint32_t) * words))) return rc;
+    a.bits = static_cast<const uint32_t *>(c->bits.ptr);
+    TFD_HIP(c,
+            tfd::launch_laya_keep_bits(static_cast<const uint8_t *>(mask_d),
+                                       static_cast<uint32_t *>(c->bits.ptr), a.L, (int)batch,
+                                       a.nkt, c->stream),
+            "laya_keep_bits launch");
+  } else {
+    a.valid = static_cast<const uint8_t *>(mask_d);
+  }
+  hipEvent_t after;
+  if ((rc = timing_begin(c, &after))) return rc;
+  TFD_HIP(c, tfd::launch_laya_attention(a, (int)heads, (int)batch, hd_pad, mode, c->stream),
+          "laya_attention launch");
+  if ((rc = timing_end(c, after))) return rc;
+  return finish(c, flags, out, out_d, sizeof(float) * n);
+}
+
+// ------------------------------------------------------------------ Jeff run
+
+int jeff_run(tfd_ctx *c, const char *op, bool bf16, size_t rows, size_t length, size_t heads,
+             size_t kv_heads, size_t head_dim, size_t rotary_dim, const void *q, const void *k,
+             const void *v, const void *gate, const float *q_norm, const float *k_norm,
+             const float *mask, uint32_t theta_bits, uint32_t eps_bits, float *out,
+             unsigned flags) {
+  size_t width = 0, kv_width = 0, qn = 0, kvn = 0, mn = 0;
+  if (!mul_ok(heads, head_dim, &width) || !mul_ok(kv_heads, head_dim, &kv_width) ||
+      !mul_ok(width, length, &qn) || !mul_ok(qn, rows, &qn) || !mul_ok(kv_width, length, &kvn) ||
+      !mul_ok(kvn, rows, &kvn) || !mul_ok(rows, length, &mn))
+    return invalid(c, op, "shape", "attention dimensions overflow");
+  // cpu-kernels lib.rs:643-645: nothing to do for an empty problem.
+  if (qn == 0 || head_dim == 0) return TFD_OK;
+  const int hd_pad = pad_head_dim(head_dim, 256);
+  if (!hd_pad)
+    return fail(c, TFD_EUNSUPPORTED, "%s: head_dim %zu exceeds the supported 256", op,
+                head_dim);
+  if (length > (size_t)INT32_MAX / 4 || width > (size_t)INT32_MAX / 4)
+    return fail(c, TFD_EUNSUPPORTED, "%s: length/width too large for the kernels", op);
+  if (heads > 65535 || rows > 65535)
+    return fail(c, TFD_EUNSUPPORTED, "%s: heads/rows exceed the launch grid", op);
+  int rc = ensure_ready(c);
+  if (rc) return rc;
+  const size_t es = bf16 ? 2 : 4;
+  const void *q_d, *k_d, *v_d, *g_d, *qn_d, *kn_d, *m_d;
+  void *out_d;
+  if ((rc = operand(c, flags, 1, q, es * qn, &q_d))) return rc;
+  if ((rc = operand(c, flags, 2, k, es * kvn, &k_d))) return rc;
+  if ((rc = operand(c, flags, 3, v, es * kvn, &v_d))) return rc;
+  if ((rc = operand(c, flags, 4, gate, es * qn, &g_d))) return rc;
+  if ((rc = operand(c, flags, 5, q_norm, sizeof(float) * head_dim, &qn_d))) return rc;
+  if ((rc = operand(c, flags, 6, k_norm, sizeof(float) * head_dim, &kn_d))) return rc;
+  if ((rc = operand(c, flags, 7, mask, sizeof(float) * mn, &m_d))) return rc;
+  if ((rc = output(c, flags, 0, out, sizeof(float) * qn, &out_d))) return rc;
+  tfd::JeffArgs a{};
+  a.q = q_d;
+  a.k = k_d;
+  a.v = v_d;
+  a.gate = g_d;
+  a.q_norm = static_cast<const float *>(qn_d);
+  a.k_norm = static_cast<const float *>(kn_d);
+  a.mask = static_cast<const float *>(m_d);
+  a.out = static_cast<float *>(out_d);
+  a.L = (int)length;
+  a.heads = (int)heads;
+  a.kv_heads = (int)kv_heads;
+  a.hd = (int)head_dim;
+  a.rot_half = (int)(rotary_dim / 2);
+  a.groups = (int)(heads / kv_heads);
+  a.heads_per_group = (a.groups % 4 == 0) ? 4 : (a.groups % 2 == 0) ? 2 : 1;
+  a.trim = (flags & TFD_TRIM_LEADING) ? 1 : 0;
+  a.eps = bits_to_f32(eps_bits);
+  a.c1 = (1.0f / sqrtf((float)head_dim)) * kLog2e;
+  a.q_row = qn / rows;
+  a.kv_row = kvn / rows;
+  if (a.rot_half > 0) {
+    if ((rc = rope_table(c, 1, length, rotary_dim, bits_to_f32(theta_bits), theta_bits, &a.cos_t,
+                         &a.sin_t)))
+      return rc;
+  }
+  hipEvent_t after;
+  if ((rc = timing_begin(c, &after))) return rc;
+  hipError_t e = bf16 ? tfd::launch_jeff_attention_bf16(a, (int)rows, hd_pad, c->stream)
+                      : tfd::launch_jeff_attention_f32(a, (int)rows, hd_pad, c->stream);
+  if ((rc = timing_end(c, after))) return rc;
+  if (e == hipErrorNotSupported)
+    return fail(c, TFD_EUNSUPPORTED, "%s: this variant is not available", op);
+  if (e != hipSuccess) return hip_fail(c, e, "jeff_attention launch");
+  return finish(c, flags, out, out_d, sizeof(float) * qn);
+}
+
+int jeff_rows_common(tfd_ctx *c, bool bf16, size_t rows, size_t length, size_t heads,
+                     size_t kv_heads, size_t head_dim, size_t rotary_dim, const void *q,
+                     const void *k, const void *v, const void *gate, const float *q_norm,
+                     const float *k_norm, const float *mask, uint32_t theta_bits,
+                     uint32_t eps_bits, float *out, unsigned flags) {
+  const char *op = bf16 ? "tfd_jeff_full_attention_rows_bf16" : "tfd_jeff_full_attention_rows_f32";
+  if (!c) return TFD_EINVAL;
+  c->err.clear();
+  int rc = check_flags(c, op, flags, TFD_DEVICE_PTRS | TFD_ASYNC | TFD_TRIM_LEADING);
+  if (rc) return rc;
+  if (kv_heads == 0 || heads % kv_heads != 0)
+    return invalid(c, op, "kv_heads", "heads must be a multiple of kv_heads");
+  if (rotary_dim > head_dim)
+    return invalid(c, op, "rotary_dim", "rotary_dim must not exceed head_dim");
+  if (rows && length && heads && head_dim &&
+      (!q || !k || !v || !gate || !q_norm || !k_norm || !mask || !out))
+    return invalid(c, op, "inputs", "null buffer");
+  return jeff_run(c, op, bf16, rows, length, heads, kv_heads, head_dim, rotary_dim, q, k, v, gate,
+                  q_norm, k_norm, mask, theta_bits, eps_bits, out, flags);
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- C ABI
+
+extern "C" {
+
+int tfd_abi_version(void) { return TFD_ABI_VERSION; }
+
+const char *tfd_laya_attention_block_family_id(void) { return kLayaFamily; }
+const char *tfd_jeff_full_attention_family_id(void) { return kJeffFamily; }
+
+int tfd_ctx_create(int device, tfd_ctx **out) {
+  if (!out) return TFD_EINVAL;
+  *out = new (std::nothrow) tfd_ctx();
+  if (!*out) return TFD_EHIP;
+  (*out)->device = device;
+  return TFD_OK;
+}
+
+int tfd_ctx_create_on_stream(int device, void *stream, tfd_ctx **out) {
+  int rc = tfd_ctx_create(device, out);
+  if (rc) return rc;
+  (*out)->stream = static_cast<hipStream_t>(stream);
+  return TFD_OK;
+}
+
+void tfd_ctx_destroy(tfd_ctx *c) {
+  if (!c) return;
+  if (c->ready) {
+    (void)hipSetDevice(c->device);
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    for (auto &b : c->staging)
+      if (b.ptr) (void)hipFree(b.ptr);
+    if (c->bits.ptr) (void)hipFree(c->bits.ptr);
+    for (auto &e : c->rope) {
+      (void)hipFree(e.cos_d);
+      (void)hipFree(e.sin_d);
+    }
+    for (auto &e : c->events) (void)hipEventDestroy(e);
+    if (c->own_stream) (void)hipStreamDestroy(c->stream);
+  }
+  delete c;
+}
+
+const char *tfd_last_error(const tfd_ctx *c) { return c ? c->err.c_str() : "null context"; }
+
+int tfd_ctx_synchronize(tfd_ctx *c) {
+  if (!c) return TFD_EINVAL;
+  if (!c->ready) return TFD_OK;
+  TFD_HIP(c, hipSetDevice(c->device), "hipSetDevice");
+  TFD_HIP(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  return TFD_OK;
+}
+
+void *tfd_ctx_stream(tfd_ctx *c) {
+  if (!c) return nullptr;
+  if (!c->ready && ensure_ready(c) != TFD_OK) return nullptr;
+  return c->stream;
+}
+
+size_t tfd_ctx_retained_bytes(const tfd_ctx *c) {
+  if (!c) return 0;
+  size_t total = sizeof(tfd_ctx) + c->bits.cap;
+  for (const auto &b : c->staging) total += b.cap;
+  for (const auto &e : c->rope) total += e.bytes;
+  return total;
+}
+
+int tfd_ctx_set_timing(tfd_ctx *c, int enabled) {
+  if (!c) return TFD_EINVAL;
+  c->timing = enabled != 0;
+  return TFD_OK;
+}
+
+int tfd_ctx_take_kernel_time(tfd_ctx *c, double *total_ms, uint64_t *launches) {
+  if (!c) return TFD_EINVAL;
+  double total = 0.0;
+  const uint64_t n = c->events_used;
+  if (n) {
+    TFD_HIP(c, hipSetDevice(c->device), "hipSetDevice");
+    TFD_HIP(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    for (size_t i = 0; i < n; ++i) {
+      float ms = 0.0f;
+      TFD_HIP(c, hipEventElapsedTime(&ms, c->events[2 * i], c->events[2 * i + 1]),
+              "hipEventElapsedTime");
+      total += ms;
+    }
+  }
+  c->events_used = 0;
+  if (total_ms) *total_ms = total;
+  if (launches) *launches = n;
+  return TFD_OK;
+}
+
+int tfd_laya_attention_block_f32(tfd_ctx *c, const float *qkv, const size_t *qkv_shape,
+                                 size_t qkv_rank, const uint8_t *keep, size_t keep_len,
+                                 size_t hidden, size_t heads, uint32_t rope_base_bits,
+                                 float *out, size_t out_len, unsigned flags) {
+  if (!c) return TFD_EINVAL;
+  c->err.clear();
+  int rc = check_flags(c, kLayaOp, flags, TFD_DEVICE_PTRS | TFD_ASYNC);
+  if (rc) return rc;
+  // laya_attention.rs:111-114 (and infer_output_meta 80-83)
+  if (qkv_shape == nullptr || qkv_rank != 3 || hidden > SIZE_MAX / 3 ||
+      qkv_shape[0] != 3 * hidden)
+    return invalid(c, kLayaOp, "shape", "attention block expects (3d, L, B)");
+  const size_t length = qkv_shape[1], batch = qkv_shape[2];
+  size_t expect = 0;
+  // laya_attention.rs:138-140
+  if (!mul_ok(length, length, &expect) || !mul_ok(expect, batch, &expect) || keep_len != expect)
+    return invalid(c, kLayaOp, "keep", "keep must be (L, L, B)");
+  if (!mul_ok(hidden, length, &expect) || !mul_ok(expect, batch, &expect) || out_len != expect)
+    return invalid(c, kLayaOp, "out", "out must be (d, L, B)");
+  if (expect != 0 && (!qkv || !out || (keep_len && !keep)))
+    return invalid(c, kLayaOp, "inputs", "null buffer");
+  return laya_run(c, kLayaOp, qkv, keep, nullptr, -1, hidden, heads, length, batch,
+                  rope_base_bits, out, flags);
+}
+
+int tfd_laya_attention_structured_f32(tfd_ctx *c, const float *qkv, size_t hidden, size_t heads,
+                                      size_t length, size_t batch, const uint8_t *valid,
+                                      int64_t window, uint32_t rope_base_bits, float *out,
+                                      unsigned flags) {
+  const char *op = "tfd_laya_attention_structured_f32";
+  if (!c) return TFD_EINVAL;
+  c->err.clear();
+  int rc = check_flags(c, op, flags, TFD_DEVICE_PTRS | TFD_ASYNC);
+  if (rc) return rc;
+  if (hidden && length && batch && (!qkv || !valid || !out))
+    return invalid(c, op, "inputs", "null buffer");
+  return laya_run(c, op, qkv, nullptr, valid, window, hidden, heads, length, batch,
+                  rope_base_bits, out, flags);
+}
+
+int tfd_jeff_full_attention_f32(tfd_ctx *c, const float *q, const size_t *q_shape,
+                                size_t q_rank, const float *k, size_t k_len, const float *v,
+                                size_t v_len, const float *gate, size_t gate_len,
+                                const float *q_norm, size_t q_norm_len, const float *k_norm,
+                                size_t k_norm_len, const float *mask, size_t mask_len,
+                                size_t heads, size_t head_dim, size_t rotary_dim,
+                                uint32_t theta_bits, uint32_t eps_bits, float *out,
+                                size_t out_len, unsigned flags) {
+  if (!c) return TFD_EINVAL;
+  c->err.clear();
+  int rc = check_flags(c, kJeffOp, flags, TFD_DEVICE_PTRS | TFD_ASYNC);
+  if (rc) return rc;
+  // jeff_attention.rs:116-125
+  if (q_shape == nullptr || q_rank != 2)
+    return invalid(c, kJeffOp, "shape", "full attention expects (length, width)");
+  const size_t length = q_shape[0], width = q_shape[1];
+  size_t hw = 0;
+  if (!mul_ok(heads, head_dim, &hw) || width != hw)
+    return invalid(c, kJeffOp, "shape", "width must equal heads * head_dim");
+  // jeff_attention.rs:159-164
+  if (q_norm_len != head_dim || k_norm_len != head_dim || mask_len != length)
+    return invalid(c, kJeffOp, "shape", "q_norm/k_norm must be (head_dim) and mask (length)");
+  size_t n = 0;
+  if (!mul_ok(length, width, &n))
+    return invalid(c, kJeffOp, "shape", "attention dimensions overflow");
+  // The reference only debug-asserts these (cpu-kernels lib.rs:635-642).
+  if (k_len != n || v_len != n || gate_len != n)
+    return invalid(c, kJeffOp, "shape", "k/v/gate must be (length, width)");
+  if (out_len != n) return invalid(c, kJeffOp, "out", "out must be (length, width)");
+  if (rotary_dim > head_dim)
+    return invalid(c, kJeffOp, "rotary_dim", "rotary_dim must not exceed head_dim");
+  if (n != 0 && (!q || !k || !v || !gate || !q_norm || !k_norm || !mask || !out))
+    return invalid(c, kJeffOp, "inputs", "null buffer");
+  return jeff_run(c, kJeffOp, false, 1, length, heads, heads, head_dim, rotary_dim, q, k, v, gate,
+                  q_norm, k_norm, mask, theta_bits, eps_bits, out, flags);
+}
+
+int tfd_jeff_full_attention_rows_f32(tfd_ctx *c, size_t rows, size_t length, size_t heads,
+                                     size_t kv_heads, size_t head_dim, size_t rotary_dim,
+                                     const float *q, const float *k, const float *v,
+                                     const float *gate, const float *q_norm,
+                                     const float *k_norm, const float *mask,
+                                     uint32_t theta_bits, uint32_t eps_bits, float *out,
+                                     unsigned flags) {
+  return jeff_rows_common(c, false, rows, length, heads, kv_heads, head_dim, rotary_dim, q, k, v,
+                          gate, q_norm, k_norm, mask, theta_bits, eps_bits, out, flags);
+}
+
+int tfd_jeff_full_attention_rows_bf16(tfd_ctx *c, size_t rows, size_t length, size_t heads,
+                                      size_t kv_heads, size_t head_dim, size_t rotary_dim,
+                                      const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                                      const uint16_t *gate, const float *q_norm,
+                                      const float *k_norm, const float *mask,
+                                      uint32_t theta_bits, uint32_t eps_bits, float *out,
+                                      unsigned flags) {
+  return jeff_rows_common(c, true, rows, length, heads, kv_heads, head_dim, rotary_dim, q, k, v,
+                          gate, q_norm, k_norm, mask, theta_bits, eps_bits, out, flags);
+}
+
+}  // extern "C"

@@ -1,0 +1,61 @@
+// Internal declarations shared by the host code (tfd_host.cpp) and the gfx950
+// kernels (laya_attention.hip, jeff_attention.hip). Not part of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace tfd {
+
+// Keys per tile and queries per wave in every attention kernel: one 32x32
+// MFMA output block covers (32 keys) x (32 queries).
+constexpr int kKeyTile = 32;
+constexpr int kWaveQueries = 32;
+constexpr int kWavesPerGroup = 4;   // 256 threads per workgroup
+constexpr int kLayaGroupQueries = kWaveQueries * kWavesPerGroup;
+constexpr int kJeffWaveQueries = 16;  // Jeff waves use the 16x16x4 MFMA
+
+enum LayaMaskMode : int {
+  kMaskBits = 0,    // general (L, L, B) keep tensor, pre-packed into 32-key words
+  kMaskStruct = 1,  // valid (L, B) + window (build_mask semantics)
+};
+
+struct LayaArgs {
+  const float *qkv;      // (3d, L, B)
+  const uint32_t *bits;  // kMaskBits: word (b*nkt + kt)*L + q, bit j = key 32*kt + j kept
+  const uint8_t *valid;  // kMaskStruct: (L, B)
+  const float *cos_t;    // (L, half) or nullptr (no RoPE)
+  const float *sin_t;
+  float *out;            // (d, L, B)
+  int d, hd, half, L, nkt, window;
+  float c1;              // (1/sqrt(hd)) * log2(e)
+};
+
+struct JeffArgs {
+  const void *q, *k, *v, *gate;  // f32 or bf16 per kernel
+  const float *q_norm, *k_norm;  // (hd)
+  const float *mask;             // rows x (L)
+  const float *cos_t, *sin_t;    // (L, rot_half) by RoPE position, or nullptr
+  float *out;
+  int L, heads, kv_heads, hd, rot_half, groups;
+  int heads_per_group;           // query heads sharing one workgroup (1, 2 or 4)
+  int trim;                      // TFD_TRIM_LEADING semantics
+  float c1;                      // (1/sqrt(hd)) * log2(e)
+  float eps;
+  size_t q_row, kv_row;          // elements per row: L*heads*hd and L*kv_heads*hd
+};
+
+// Kernel launchers (return the launch status). hd_pad selects the
+// compile-time padded head dim (32, 64, 128 or 256).
+hipError_t launch_fill_zero(float *out, size_t n, hipStream_t stream);
+hipError_t launch_laya_keep_bits(const uint8_t *keep, uint32_t *bits, int L, int B, int nkt,
+                                 hipStream_t stream);
+hipError_t launch_laya_attention(const LayaArgs &a, int heads, int batch, int hd_pad, int mode,
+                                 hipStream_t stream);
+hipError_t launch_jeff_attention_f32(const JeffArgs &a, int rows, int hd_pad,
+                                     hipStream_t stream);
+hipError_t launch_jeff_attention_bf16(const JeffArgs &a, int rows, int hd_pad,
+                                      hipStream_t stream);
+
+}  // namespace tfd

@@ -1,0 +1,249 @@
+"""GPU parity tests: the HIP kernels, called through the C ABI, against the
+CPU oracle on identical seeded inputs. Tolerances are the north star's:
+max-abs <= 2e-5 for f32, <= 1e-2 for bf16; NaN positions must match exactly.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+import tenferro_ext as te
+from tenferro_ext.workloads import Lcg, jeff_config, laya_config
+
+pytestmark = pytest.mark.gpu
+
+F32_TOL = 2e-5
+BF16_TOL = 1e-2
+
+
+@pytest.fixture(autouse=True)
+def _announce(request):
+    print(f"\n[gpu] {request.node.nodeid}", flush=True)
+    sys.stdout.flush()
+    yield
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _oracle_threads():
+    oracle.set_threads(16)
+
+
+def assert_close(got, want, tol):
+    got = np.asarray(got, np.float32).reshape(-1)
+    want = np.asarray(want, np.float32).reshape(-1)
+    assert got.shape == want.shape
+    gn, wn = np.isnan(got), np.isnan(want)
+    assert np.array_equal(gn, wn), f"NaN mismatch at {np.nonzero(gn != wn)[0][:10]}"
+    ok = ~wn
+    err = float(np.abs(got[ok] - want[ok]).max()) if ok.any() else 0.0
+    assert err <= tol, f"max abs error {err} > {tol}"
+    return err
+
+
+def encoder_valid(length, batch, sparse):
+    valid = np.zeros(length * batch, np.uint8)
+    for b in range(batch):
+        for l in range(length):
+            if sparse:
+                v = l == 0 or l == length - 1
+            elif length == 1:
+                v = True
+            elif batch == 1 or b == 0:
+                v = l != 1
+            else:
+                v = l < length - 1
+            valid[l + length * b] = v
+    return valid
+
+
+# ------------------------------------------------------------------ Laya
+
+def laya_gpu(ctx, qkv, keep, d, heads, L, B, base):
+    return te.laya_attention_block(qkv, keep, d, heads, base, qkv_shape=(3 * d, L, B), ctx=ctx)
+
+
+def test_laya_c1_matches_oracle(gpu_ctx):
+    w = laya_config(1)
+    got = laya_gpu(gpu_ctx, w.qkv, w.keep, w.hidden, w.heads, w.length, w.batch, w.rope_base)
+    want = oracle.laya_attention_block(w.qkv, w.keep, w.hidden, w.heads, w.length, w.batch, w.rope_base)
+    assert_close(got, want, F32_TOL)
+
+
+@pytest.mark.parametrize("length", [1, 2, 31, 32, 33, 63, 64, 65, 127, 129, 200])
+@pytest.mark.parametrize("hd", [4, 16, 64, 128])
+def test_laya_sweep_keep_and_structured(gpu_ctx, length, hd):
+    """laya-infer tests/model.rs:338-373 masks (interior hole, padded rows,
+    sparse rows) on global (rope 160000) and sliding (rope 10000) layers."""
+    heads, batch = 2, 2
+    d = heads * hd
+    rng = Lcg(1000 + length + hd)
+    qkv = (rng.uniform(3 * d * length * batch) * 2.0 - 1.0).astype(np.float32)
+    for sparse in (False, True):
+        valid = encoder_valid(length, batch, sparse)
+        for window, base in ((-1, 160000.0), (1, 10000.0), (64, 10000.0)):
+            keep = oracle.laya_build_mask(valid, length, batch, window)
+            want = oracle.laya_attention_block(qkv, keep, d, heads, length, batch, base)
+            got = laya_gpu(gpu_ctx, qkv, keep, d, heads, length, batch, base)
+            assert_close(got, want, F32_TOL)
+            st = te.laya_attention_structured(qkv, valid, d, heads, length, batch, window, base,
+                                              ctx=gpu_ctx)
+            # same tiles, same order: the structured entry is bitwise equal
+            assert np.array_equal(np.asarray(st).view(np.uint32), np.asarray(got).view(np.uint32))
+
+
+@pytest.mark.parametrize("excluded", [1.0, float("nan"), float("inf"), float("-inf")])
+def test_laya_masked_nonfinite_values_and_empty_rows(gpu_ctx, excluded):
+    """cpu-kernels lib.rs:1212-1250 on the GPU."""
+    length, d = 65, 4
+    qkv = np.zeros(3 * d * length, np.float32)
+    for key in range(length):
+        qkv[3 * d * key + 2 * d:3 * d * key + 3 * d] = np.arange(1, d + 1)
+    keep = np.ones(length * length, np.uint8)
+    keep[np.arange(length) + length * 32] = 0
+    keep[length * np.arange(length)] = 0
+    keep[length - 1 + length * np.arange(length)] = 0
+    qkv[3 * d * 32 + 2 * d:3 * d * 32 + 3 * d] = excluded
+    out = np.asarray(laya_gpu(gpu_ctx, qkv, keep, d, 1, length, 1, 0.0)).reshape(length, d)
+    assert np.all(np.isnan(out[0])) and np.all(np.isnan(out[-1]))
+    assert np.abs(out[1:-1] - np.arange(1, d + 1)).max() <= 1e-6
+
+
+def test_laya_kept_nonfinite_value_propagates(gpu_ctx):
+    """A kept infinite value reaches the rows that keep it (p > 0)."""
+    length, d, heads = 40, 8, 1
+    rng = Lcg(5)
+    qkv = rng.normal(3 * d * length).astype(np.float32)
+    qkv[3 * d * 7 + 2 * d + 3] = np.inf
+    keep = np.ones(length * length, np.uint8)
+    want = oracle.laya_attention_block(qkv, keep, d, heads, length, 1, 0.0)
+    got = laya_gpu(gpu_ctx, qkv, keep, d, heads, length, 1, 0.0)
+    g, w = np.asarray(got), want
+    assert np.array_equal(np.isinf(g), np.isinf(w))
+    fin = np.isfinite(w)
+    assert np.abs(g[fin] - w[fin]).max() <= F32_TOL
+
+
+def test_laya_heads_not_dividing_writes_zeros(gpu_ctx):
+    out = np.full(6 * 4, 7.0, np.float32)
+    te.laya_attention_block(np.ones(3 * 6 * 4, np.float32), np.ones(16, np.uint8), 6, 4, 0.0,
+                            qkv_shape=(18, 4, 1), ctx=gpu_ctx, out=out)
+    assert np.all(out == 0.0)
+
+
+@pytest.mark.parametrize("cfg", [2, 3])
+def test_laya_full_config_device_pointers(gpu_ctx, cfg):
+    """C2 (global, padded) and C3 (sliding +-64, L 2048) at full size, device
+    pointers, against the oracle; the structured entry must agree bitwise."""
+    import torch
+
+    w = laya_config(cfg)
+    want = oracle.laya_attention_block(w.qkv, w.keep, w.hidden, w.heads, w.length, w.batch, w.rope_base)
+    dev = torch.device("cuda:0")
+    qkv = torch.from_numpy(w.qkv).to(dev)
+    keep = torch.from_numpy(w.keep).to(dev)
+    valid = torch.from_numpy(w.valid).to(dev)
+    torch.cuda.synchronize()
+    got = te.laya_attention_block(qkv, keep, w.hidden, w.heads, w.rope_base,
+                                  qkv_shape=(3 * w.hidden, w.length, w.batch), ctx=gpu_ctx)
+    st = te.laya_attention_structured(qkv, valid, w.hidden, w.heads, w.length, w.batch, w.window,
+                                      w.rope_base, ctx=gpu_ctx)
+    err = assert_close(got.cpu().numpy(), want, F32_TOL)
+    print(f"C{cfg} max abs error {err:.3e}")
+    assert torch.equal(got, st)
+
+
+# ------------------------------------------------------------------ Jeff
+
+def jeff_case(seed, length, heads, hd, kv_heads, holes):
+    rng = Lcg(seed)
+    W, KW = heads * hd, kv_heads * hd
+    q = rng.normal(length * W).astype(np.float32)
+    k = rng.normal(length * KW).astype(np.float32)
+    v = rng.normal(length * KW).astype(np.float32)
+    g = rng.normal(length * W).astype(np.float32)
+    qn = (rng.normal(hd) * 0.1).astype(np.float32)
+    kn = (rng.normal(hd) * 0.1).astype(np.float32)
+    mask = np.ones(length, np.float32)
+    if holes and length > 3:
+        mask[: length // 4] = 0.0
+        mask[length // 2] = 0.0
+    return q, k, v, g, qn, kn, mask
+
+
+@pytest.mark.parametrize("length", [1, 2, 3, 6, 17, 33, 64, 100])
+@pytest.mark.parametrize("hd,rot", [(4, 2), (16, 16), (64, 32), (256, 64)])
+def test_jeff_dropin_matches_oracle(gpu_ctx, length, hd, rot):
+    heads = 2
+    for holes in (False, True):
+        q, k, v, g, qn, kn, mask = jeff_case(7 * length + hd, length, heads, hd, heads, holes)
+        want = oracle.jeff_full_attention(q, k, v, g, qn, kn, mask, length, heads, hd, rot, 1e7, 1e-6)
+        got = te.jeff_full_attention(q, k, v, g, qn, kn, mask, heads, hd, rot, 1e7, 1e-6,
+                                     q_shape=(length, heads * hd), ctx=gpu_ctx)
+        assert_close(got, want, F32_TOL)
+
+
+@pytest.mark.parametrize("heads,kv_heads", [(8, 2), (4, 4), (6, 3), (8, 1), (2, 1)])
+def test_jeff_rows_gqa_matches_oracle(gpu_ctx, heads, kv_heads):
+    rows, length, hd, rot = 3, 70, 64, 16
+    rng = Lcg(heads * 10 + kv_heads)
+    W, KW = heads * hd, kv_heads * hd
+    q = rng.normal(rows * length * W).astype(np.float32)
+    g = rng.normal(rows * length * W).astype(np.float32)
+    k = rng.normal(rows * length * KW).astype(np.float32)
+    v = rng.normal(rows * length * KW).astype(np.float32)
+    qn = (rng.normal(hd) * 0.1).astype(np.float32)
+    kn = (rng.normal(hd) * 0.1).astype(np.float32)
+    mask = np.ones(rows * length, np.float32)
+    mask[length:length + 9] = 0.0     # row 1 left-padded
+    mask[2 * length + 30] = 0.0       # row 2 interior hole
+    for trim in (False, True):
+        want = oracle.jeff_rows(q, k, v, g, qn, kn, mask, rows, length, heads, kv_heads, hd, rot,
+                                1e6, 1e-6, trim_leading=trim)
+        got = te.jeff_full_attention_rows(q, k, v, g, qn, kn, mask, rows, length, heads, kv_heads,
+                                          hd, rot, 1e6, 1e-6, trim_leading=trim, ctx=gpu_ctx)
+        assert_close(got, want, F32_TOL)
+
+
+def test_jeff_masked_nonfinite_values_and_empty_rows(gpu_ctx):
+    length, heads, hd = 40, 2, 64
+    q, k, v, g, qn, kn, mask = jeff_case(3, length, heads, hd, heads, False)
+    mask[:3] = 0.0
+    mask[20] = 0.0
+    V = v.reshape(heads * hd, length)
+    V[:, 20] = np.nan          # masked key: must not leak
+    V[5, 1] = np.inf           # masked leading key
+    want = oracle.jeff_full_attention(q, k, v, g, qn, kn, mask, length, heads, hd, 32, 1e7, 1e-6)
+    got = te.jeff_full_attention(q, k, v, g, qn, kn, mask, heads, hd, 32, 1e7, 1e-6,
+                                 q_shape=(length, heads * hd), ctx=gpu_ctx)
+    assert np.all(np.isfinite(want))
+    assert_close(got, want, F32_TOL)
+    out = np.asarray(got).reshape(heads * hd, length)
+    assert np.all(out[:, :3] == 0.0)  # no active key at or before these queries
+
+
+def test_jeff_c4_full_gqa_and_dropin(gpu_ctx):
+    """C4 at full size: GQA rows entry (k/v at kv width) and the drop-in op
+    row by row on expanded K/V, both against the oracle."""
+    import torch
+
+    w = jeff_config(4)
+    want = oracle.jeff_rows(w.q, w.k, w.v, w.gate, w.q_norm, w.k_norm, w.mask, w.rows, w.length,
+                            w.heads, w.kv_heads, w.head_dim, w.rotary_dim, w.theta, w.eps)
+    dev = torch.device("cuda:0")
+    t = {n: torch.from_numpy(getattr(w, n)).to(dev) for n in ("q", "k", "v", "gate", "q_norm", "k_norm", "mask")}
+    torch.cuda.synchronize()
+    got = te.jeff_full_attention_rows(t["q"], t["k"], t["v"], t["gate"], t["q_norm"], t["k_norm"],
+                                      t["mask"], w.rows, w.length, w.heads, w.kv_heads, w.head_dim,
+                                      w.rotary_dim, w.theta, w.eps, ctx=gpu_ctx)
+    err = assert_close(got.cpu().numpy(), want, F32_TOL)
+    print(f"C4 rows max abs error {err:.3e}")
+    L, W, KW = w.length, w.heads * w.head_dim, w.kv_heads * w.head_dim
+    for r in (0, w.rows - 1):
+        ke = oracle.expand_kv(w.k[r * L * KW:(r + 1) * L * KW], L, w.heads, w.kv_heads, w.head_dim)
+        ve = oracle.expand_kv(w.v[r * L * KW:(r + 1) * L * KW], L, w.heads, w.kv_heads, w.head_dim)
+        sl = slice(r * L * W, (r + 1) * L * W)
+        one = te.jeff_full_attention(w.q[sl], ke, ve, w.gate[sl], w.q_norm, w.k_norm,
+                                     w.mask[r * L:(r + 1) * L], w.heads, w.head_dim, w.rotary_dim,
+                                     w.theta, w.eps, q_shape=(L, W), ctx=gpu_ctx)
+        assert_close(one, want[sl], F32_TOL)
