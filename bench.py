@@ -100,7 +100,10 @@ def run(args):
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    ctx = te.Context(0, stream=torch.cuda.current_stream().cuda_stream)
+    # One dedicated stream for the library and torch's timing events.
+    stream = torch.cuda.Stream(device=dev)
+    torch.cuda.set_stream(stream)
+    ctx = te.Context(0, stream=stream.cuda_stream)
     gpu_name = torch.cuda.get_device_name(0)
 
     # ------------------------------------------------------------ C2 headline
@@ -245,6 +248,46 @@ def run(args):
     return result
 
 
+def run_only(args):
+    """One configuration's op alone (for rocprofv3 runs of a single kernel)."""
+    import numpy as np
+    import torch
+
+    import tenferro_ext as te
+    from tenferro_ext.workloads import jeff_config, laya_config
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.Stream(device=dev)
+    torch.cuda.set_stream(stream)
+    ctx = te.Context(0, stream=stream.cuda_stream)
+    cfg = int(args.only[1])
+    if cfg in (2, 3):
+        w = laya_config(cfg)
+        flops = 4 * w.head_dim * w.kept_pairs() * w.heads
+        qkv = torch.from_numpy(w.qkv).to(dev)
+        keep = torch.from_numpy(w.keep).to(dev)
+        out = torch.empty(w.hidden * w.length * w.batch, dtype=torch.float32, device=dev)
+        shape = (3 * w.hidden, w.length, w.batch)
+        fn = lambda: te.laya_attention_block(qkv, keep, w.hidden, w.heads, w.rope_base,
+                                             qkv_shape=shape, ctx=ctx, out=out)
+    else:
+        w = jeff_config(cfg)
+        flops = 4 * w.head_dim * w.kept_pairs() * w.heads
+        conv = (lambda x: torch.from_numpy(te.to_bf16_bits(x).view(np.int16)).to(dev)) if w.bf16 \
+            else (lambda x: torch.from_numpy(x).to(dev))
+        t = [conv(getattr(w, n)) for n in ("q", "k", "v", "gate")]
+        t += [torch.from_numpy(getattr(w, n)).to(dev) for n in ("q_norm", "k_norm", "mask")]
+        out = torch.empty(w.rows * w.length * w.heads * w.head_dim, dtype=torch.float32, device=dev)
+        fn = lambda: te.jeff_full_attention_rows(*t, w.rows, w.length, w.heads, w.kv_heads,
+                                                 w.head_dim, w.rotary_dim, w.theta, w.eps,
+                                                 bf16=w.bf16, ctx=ctx, out=out)
+    ms, kern = time_gpu(fn, args.steps, args.warmup, ctx)
+    ctx.close()
+    return {"only": f"C{cfg}", "ms_per_step": round(ms, 5), "kernel_ms": round(kern, 5),
+            "kernel_tflops": round(flops / (kern * 1e-3) / 1e12, 3), "algorithmic_flops": flops}
+
+
 def _cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -262,12 +305,15 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="only the C2 headline")
+    ap.add_argument("--only", choices=["c2", "c3", "c4", "c5"], default=None,
+                    help="profiling aid: run one configuration's op (steps + warmup calls), "
+                         "print its timing line and skip everything else")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)",
               file=sys.stderr)
         sys.exit(2)
-    print(json.dumps(run(args)), flush=True)
+    print(json.dumps(run_only(args) if args.only else run(args)), flush=True)
 
 
 if __name__ == "__main__":

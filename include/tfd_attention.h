@@ -69,7 +69,7 @@ const char *tfd_jeff_full_attention_family_id(void);
 
 /* Context life cycle. Creation does not touch the GPU; the first op call
  * selects `device` and creates the stream (or adopts `stream`, a hipStream_t
- * the caller keeps alive). The reference keeps the matching per-op state in
+ * the caller keeps alive; NULL adopts the null stream). The reference keeps the matching per-op state in
  * the runtime's ExtensionCacheStore (laya_attention.rs:142-159). */
 int tfd_ctx_create(int device, tfd_ctx **out);
 int tfd_ctx_create_on_stream(int device, void *stream, tfd_ctx **out);

@@ -54,10 +54,20 @@ __device__ __forceinline__ float rms_scale(float sumsq, int hd, float eps) {
 __device__ __forceinline__ void scan_active(const float *maskr, int L, int tid, int lane,
                                             int *s_span) {
   int lo = 0x7fffffff, hi = -1;
-  for (int k = tid; k < L; k += 256) {
-    if (maskr[k] != 0.0f) {
-      lo = min(lo, k);
-      hi = max(hi, k);
+  for (int k0 = 0; k0 < L; k0 += 256 * 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {  // 8 loads in flight per thread
+      const int k = k0 + tid + 256 * u;
+      v[u] = k < L ? maskr[k] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int k = k0 + tid + 256 * u;
+      if (v[u] != 0.0f) {
+        lo = min(lo, k);
+        hi = max(hi, k);
+      }
     }
   }
   lo = wave_min(lo);
@@ -68,16 +78,179 @@ __device__ __forceinline__ void scan_active(const float *maskr, int L, int tid, 
   }
 }
 
-template <int HDP>
-__global__ __launch_bounds__(256, 2) void jeff_attention_f32_kernel(const JeffArgs a) {
-  constexpr int QS = HDP / 4;   // Q registers per lane (4 lane groups split hd)
-  constexpr int NB = HDP / 16;  // 16-row blocks of O^T
-  constexpr int DP = HDP / 8;   // dims per staging thread (8 threads per key)
-  constexpr int KS = HDP + 4;   // K and V stored [key][d]
-  __shared__ __attribute__((aligned(16))) float Ks[kKeyTile * KS];
-  __shared__ __attribute__((aligned(16))) float Vs[kKeyTile * KS];
+// First active key of a row (rows with no active key: 0), for TFD_TRIM_LEADING.
+__device__ __forceinline__ int row_start(const JeffArgs &a, const float *maskr, int tid, int lane,
+                                         int *s_span) {
+  if (!a.trim) return 0;
+  if (tid == 0) {
+    s_span[0] = 0x7fffffff;
+    s_span[1] = -1;
+  }
+  __syncthreads();
+  scan_active(maskr, a.L, tid, lane, s_span);
+  __syncthreads();
+  return s_span[1] >= 0 ? s_span[0] : 0;
+}
+
+// ---------------------------------------------------------------- K prep
+
+// RMSNorm (lib.rs:676-691) and partial RoPE (692-709) of every key of one
+// (row, kv head) once per call, so attention workgroups stage finished keys.
+// One workgroup = 32 keys; output kp[row][kvh][key][HDP] (zero-padded past
+// hd), written in whole coalesced rows. Out: f32, or bf16 (RNE) for the
+// bf16 attention kernel.
+template <int HDP, typename OutT>
+__global__ __launch_bounds__(256) void jeff_k_prep_kernel(const JeffArgs a, OutT *__restrict__ kp) {
+  constexpr int DP = HDP / 8;
+  constexpr int KS = HDP + 1;
+  __shared__ float Kt[kKeyTile * KS];
   __shared__ float s_red[8 * kKeyTile];
-  __shared__ float Ps[kWavesPerGroup * kKeyTile * kJeffWaveQueries];
+  __shared__ int s_span[2];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int row = blockIdx.z, kvh = blockIdx.y;
+  const int L = a.L, hd = a.hd, rh = a.rot_half;
+  const int k0 = blockIdx.x * kKeyTile;
+  const float *maskr = a.mask + (size_t)row * L;
+  const int start = row_start(a, maskr, tid, lane, s_span);
+  const bool bf = sizeof(OutT) == 2;
+  const size_t kv_off = row * a.kv_row + (size_t)kvh * hd * L;
+  const int kk = tid & 31, part = tid >> 5;
+  const int key = k0 + kk;
+  const bool kin = key < L;
+  float ss = 0.0f;
+  float xs[DP];
+#pragma unroll
+  for (int i = 0; i < DP; ++i) {  // all DP loads in flight at once
+    const int d = part * DP + i;
+    const int dc = d < hd ? d : hd - 1;
+    const size_t at = kv_off + (kin ? key : 0) + (size_t)L * dc;
+    const float x = bf ? __uint_as_float((uint32_t)static_cast<const uint16_t *>(a.k)[at] << 16)
+                       : static_cast<const float *>(a.k)[at];
+    xs[i] = (kin && d < hd) ? x : 0.0f;
+  }
+#pragma unroll
+  for (int i = 0; i < DP; ++i) {
+    ss += xs[i] * xs[i];
+    Kt[kk * KS + part * DP + i] = xs[i];
+  }
+  s_red[part * kKeyTile + kk] = ss;
+  __syncthreads();
+  {
+    float tot = 0.0f;
+#pragma unroll
+    for (int p = 0; p < 8; ++p) tot += s_red[p * kKeyTile + kk];
+    const float scale = rms_scale(tot, hd, a.eps);
+#pragma unroll 4
+    for (int i = 0; i < DP; ++i) {
+      const int d = part * DP + i;
+      if (kin && d < hd) Kt[kk * KS + d] = rms_apply(Kt[kk * KS + d], scale, a.k_norm[d]);
+    }
+  }
+  if (a.cos_t != nullptr && rh > 0) {
+    __syncthreads();
+    for (int e = tid; e < kKeyTile * rh; e += 256) {
+      const int k2 = e / rh, i = e - k2 * rh;
+      if (k0 + k2 < L) {
+        const int pos = max(k0 + k2 - start, 0);
+        const float c = a.cos_t[(size_t)pos * rh + i], sn = a.sin_t[(size_t)pos * rh + i];
+        const float x = Kt[k2 * KS + i], y = Kt[k2 * KS + i + rh];
+        Kt[k2 * KS + i] = rope_lo(x, y, c, sn);
+        Kt[k2 * KS + i + rh] = rope_hi(x, y, c, sn);
+      }
+    }
+  }
+  __syncthreads();
+  OutT *dst = kp + (((size_t)row * a.kv_heads + kvh) * L + k0) * HDP;
+  const int nkeys = min(kKeyTile, L - k0);
+  for (int e = tid; e < nkeys * HDP; e += 256) {
+    const float y = Kt[(e / HDP) * KS + (e % HDP)];
+    if constexpr (sizeof(OutT) == 2) {
+      const __bf16 h = (__bf16)y;
+      dst[e] = *reinterpret_cast<const uint16_t *>(&h);
+    } else {
+      dst[e] = y;
+    }
+  }
+}
+
+// ----------------------------------------------------------- f32 attention
+
+// Tile data for one 16-key tile, prefetched into registers: finished K rows
+// from the prep workspace (16-byte loads) and the V columns (16-byte loads
+// along tokens when VEC, else element loads), written to LDS as [key][d].
+template <int HDP, bool VEC>
+struct JeffStage {
+  static constexpr int KT = kJeffKeyTile;
+  static constexpr int TASKS = KT * HDP / 4;      // 16-byte chunks of K (and of V)
+  static constexpr int KN = (TASKS + 255) / 256;  // K chunks per thread
+  static constexpr int VN = (TASKS + 255) / 256;  // V 4-key groups per thread
+  f32x4 k[KN], v[VN];
+
+  __device__ __forceinline__ void fetch(const float *kp_tile, const float *V, int L, int hd,
+                                        int k0, int tid) {
+#pragma unroll
+    for (int i = 0; i < KN; ++i) {
+      const int e = tid + 256 * i;  // chunk of the contiguous KT x HDP tile
+      k[i] = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (e < TASKS && k0 + (4 * e) / HDP < L) k[i] = reinterpret_cast<const f32x4 *>(kp_tile)[e];
+    }
+#pragma unroll
+    for (int i = 0; i < VN; ++i) {
+      const int e = tid + 256 * i;
+      const int d = e / (KT / 4), g = e % (KT / 4);  // feature d, keys k0 + 4g .. 4g+3
+      const int key = k0 + 4 * g;
+      v[i] = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (e < TASKS && d < hd) {
+        const float *src = V + key + (size_t)L * d;
+        if (VEC && key + 3 < L) {
+          v[i] = *reinterpret_cast<const f32x4 *>(src);
+        } else {
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            if (key + t < L) v[i][t] = src[t];
+        }
+      }
+    }
+  }
+
+  __device__ __forceinline__ int commit(float *Ks, float *Vs, int tid) {
+    constexpr int KS = HDP + 4;
+    int nonfinite = 0;
+#pragma unroll
+    for (int i = 0; i < KN; ++i) {
+      const int e = tid + 256 * i;
+      const int kk = (4 * e) / HDP, d = (4 * e) % HDP;
+      if (e < TASKS) *reinterpret_cast<f32x4 *>(&Ks[kk * KS + d]) = k[i];
+    }
+#pragma unroll
+    for (int i = 0; i < VN; ++i) {
+      const int e = tid + 256 * i;
+      const int d = e / (KT / 4), g = e % (KT / 4);
+      if (e >= TASKS) continue;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        nonfinite |= !__builtin_isfinite(v[i][t]);
+        Vs[(4 * g + t) * KS + d] = v[i][t];
+      }
+    }
+    return nonfinite;
+  }
+};
+
+template <int HDP, bool VEC>
+__global__ __launch_bounds__(256, 2) void jeff_attention_f32_kernel(const JeffArgs a,
+                                                                    const float *__restrict__ kp) {
+  constexpr int KT = kJeffKeyTile;  // 16 keys per tile
+  constexpr int QS = HDP / 4;       // Q registers per lane (4 lane groups split hd)
+  constexpr int NB = HDP / 16;      // 16-row blocks of O^T
+  constexpr int KS = HDP + 4;       // K and V stored [key][d]
+  // K and V double buffers; before the key loop the same bytes hold each
+  // wave's raw Q tile (16 queries x (HDP + 1)) for the Q prep.
+  static_assert(kWavesPerGroup * kJeffWaveQueries * (HDP + 1) <= 4 * KT * KS, "Q scratch");
+  __shared__ __attribute__((aligned(16))) float smem[4 * KT * KS];
+  float(*Ks)[KT * KS] = reinterpret_cast<float(*)[KT * KS]>(smem);
+  float(*Vs)[KT * KS] = reinterpret_cast<float(*)[KT * KS]>(smem + 2 * KT * KS);
+  __shared__ float Ps[kWavesPerGroup * KT * kJeffWaveQueries];
   __shared__ int s_span[2];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -94,8 +267,8 @@ __global__ __launch_bounds__(256, 2) void jeff_attention_f32_kernel(const JeffAr
   const float *maskr = a.mask + (size_t)row * L;
   const float *Q = static_cast<const float *>(a.q) + row * a.q_row + (size_t)head * hd * L;
   const float *Gt = static_cast<const float *>(a.gate) + row * a.q_row + (size_t)head * hd * L;
-  const float *K = static_cast<const float *>(a.k) + row * a.kv_row + (size_t)kvh * hd * L;
   const float *V = static_cast<const float *>(a.v) + row * a.kv_row + (size_t)kvh * hd * L;
+  const float *KP = kp + ((size_t)row * a.kv_heads + kvh) * L * HDP;
   float *OUT = a.out + row * a.q_row + (size_t)head * hd * L;
   const bool rope = a.cos_t != nullptr && rh > 0;
 
@@ -113,45 +286,72 @@ __global__ __launch_bounds__(256, 2) void jeff_attention_f32_kernel(const JeffAr
   {
     const int kl = min(last, min(qa + QT, L) - 1);
     if (last >= 0 && first <= kl) {
-      kt_begin = first / kKeyTile;
-      kt_end = kl / kKeyTile + 1;
+      kt_begin = first / KT;
+      kt_end = kl / KT + 1;
     }
   }
 
-  // -------- Q: RMSNorm + partial RoPE into registers.
-  // Lane (col, grp) holds Qn[q][grp*QS + s], the B operand of step s.
+  // -------- Q: RMSNorm + partial RoPE into registers, in wave-local LDS
+  // phases (raw, normalized in place, rotated pairs) so that no long chain
+  // of global loads is in flight beside the registers the key loop needs.
+  // Lane (col, grp) ends with Qn[q][grp*QS + s], the B operand of step s.
   float qreg[QS];
   const bool q_live = qin && q >= start;
   {
+    constexpr int QP = HDP + 1;
+    float *qw = smem + wave * (kJeffWaveQueries * QP);
+    float *qs = qw + col * QP;
     float ss = 0.0f;
-#pragma unroll
-    for (int s = 0; s < QS; ++s) {
+    const int qc = q_live ? q : 0;
+#pragma unroll 16
+    for (int s = 0; s < QS; ++s) {  // clamped, unconditional loads batch together
       const int d = grp * QS + s;
-      const float x = (q_live && d < hd) ? Q[q + (size_t)L * d] : 0.0f;
-      qreg[s] = x;
-      ss += x * x;
+      const float x = Q[qc + (size_t)L * (d < hd ? d : hd - 1)];
+      const float y = (q_live && d < hd) ? x : 0.0f;
+      qs[d] = y;
+      ss += y * y;
     }
     ss += __shfl_xor(ss, 16);
     ss += __shfl_xor(ss, 32);
     const float scale = rms_scale(ss, hd, a.eps);
-    const int pos = q_live ? q - start : 0;
-#pragma unroll
+#pragma unroll 8
     for (int s = 0; s < QS; ++s) {
       const int d = grp * QS + s;
-      float y = 0.0f;
-      if (q_live && d < hd) {
-        y = rms_apply(qreg[s], scale, a.q_norm[d]);
-        if (rope && d < 2 * rh) {
-          const int p = d < rh ? d + rh : d - rh;
-          const int i = d < rh ? d : d - rh;
-          const float yp = rms_apply(Q[q + (size_t)L * p], scale, a.q_norm[p]);
+      if (d < hd) qs[d] = rms_apply(qs[d], scale, a.q_norm[d]);
+    }
+    if (rope) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const int q0 = qa + (wave / hg) * kJeffWaveQueries;
+      for (int e = lane; e < kJeffWaveQueries * rh; e += 64) {
+        const int qi = e / rh, i = e - qi * rh;
+        const int qq = q0 + qi;
+        if (qq < L && qq >= start) {
+          const int pos = qq - start;
           const float c = a.cos_t[(size_t)pos * rh + i], sn = a.sin_t[(size_t)pos * rh + i];
-          y = d < rh ? rope_lo(y, yp, c, sn) : rope_hi(yp, y, c, sn);
+          const float x = qw[qi * QP + i], y = qw[qi * QP + i + rh];
+          qw[qi * QP + i] = rope_lo(x, y, c, sn);
+          qw[qi * QP + i + rh] = rope_hi(x, y, c, sn);
         }
       }
-      qreg[s] = y;
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int s = 0; s < QS; ++s) qreg[s] = qs[grp * QS + s];
   }
+  __syncthreads();  // the Q scratch becomes the K/V buffers
+
+  // Keep word for a 16-key tile: active key, key >= start, causal key <= query.
+  auto keep_word = [&](int kt) -> uint32_t {
+    const int k0 = kt * KT;
+    const int kc = k0 + (lane & 15);
+    const bool act = kc < L && kc >= start && maskr[kc] != 0.0f;
+    const uint32_t abits = (uint32_t)__ballot(act) & 0xffffu;
+    return q_live ? (abits & range_bits(0, q - k0)) : 0u;
+  };
 
   f32x4 O[NB];
 #pragma unroll
@@ -160,155 +360,96 @@ __global__ __launch_bounds__(256, 2) void jeff_attention_f32_kernel(const JeffAr
     for (int r = 0; r < 4; ++r) O[j][r] = 0.0f;
   float m = -INFINITY, l = 0.0f;
 
-  const int kk = tid & 31, part = tid >> 5;
+  JeffStage<HDP, VEC> st;
+  int nonfinite = 0;
+  uint32_t w = 0u;
+  if (kt_begin < kt_end) {
+    st.fetch(KP + (size_t)kt_begin * KT * HDP, V, L, hd, kt_begin * KT, tid);
+    nonfinite = st.commit(Ks[0], Vs[0], tid);
+    w = keep_word(kt_begin);
+  }
+  int nf = __syncthreads_or(nonfinite);
+
   for (int kt = kt_begin; kt < kt_end; ++kt) {
-    const int k0 = kt * kKeyTile;
-    const int key = k0 + kk;
-    const bool kin = key < L;
-    // -------- stage in three light phases so little is live beside Q and O:
-    // (1) raw K and V slices to LDS with partial sums of squares; V goes as
-    // is, the MFMA product only runs on tiles whose V is all finite;
-    // (2) RMSNorm of this thread's K slice in place; (3) RoPE on the pairs.
-    float ss = 0.0f;
-    int nonfinite = 0;
-    {
-      const float *kp = K + key;
-      const float *vp = V + key;
-#pragma unroll 4
-      for (int i = 0; i < DP; ++i) {
-        const int d = part * DP + i;
-        float x = 0.0f, vv = 0.0f;
-        if (kin && d < hd) {
-          x = kp[(size_t)L * d];
-          vv = vp[(size_t)L * d];
-        }
-        ss += x * x;
-        nonfinite |= !__builtin_isfinite(vv);
-        Ks[kk * KS + d] = x;
-        Vs[kk * KS + d] = vv;
-      }
+    const int cur = (kt - kt_begin) & 1;
+    const bool more = kt + 1 < kt_end;
+    uint32_t w_next = 0u;
+    if (more) {
+      st.fetch(KP + (size_t)(kt + 1) * KT * HDP, V, L, hd, (kt + 1) * KT, tid);
+      w_next = keep_word(kt + 1);
     }
-    s_red[part * kKeyTile + kk] = ss;
-    __syncthreads();
-    {
-      float tot = 0.0f;
-#pragma unroll
-      for (int p = 0; p < 8; ++p) tot += s_red[p * kKeyTile + kk];
-      const float scale = rms_scale(tot, hd, a.eps);
-#pragma unroll 4
-      for (int i = 0; i < DP; ++i) {
-        const int d = part * DP + i;
-        if (kin && d < hd) Ks[kk * KS + d] = rms_apply(Ks[kk * KS + d], scale, a.k_norm[d]);
-      }
-    }
-    if (rope) {
-      __syncthreads();
-      for (int e = tid; e < kKeyTile * rh; e += 256) {
-        const int k2 = e / rh, i = e - k2 * rh;
-        const int pos = max(k0 + k2 - start, 0);
-        if (k0 + k2 < L) {
-          const float c = a.cos_t[(size_t)pos * rh + i], sn = a.sin_t[(size_t)pos * rh + i];
-          const float x = Ks[k2 * KS + i], y = Ks[k2 * KS + i + rh];
-          Ks[k2 * KS + i] = rope_lo(x, y, c, sn);
-          Ks[k2 * KS + i + rh] = rope_hi(x, y, c, sn);
-        }
-      }
-    }
-    // -------- keep word: active key, key >= start, causal key <= query
-    uint32_t w = 0u;
-    {
-      const int kc = k0 + (lane & 31);
-      const bool act = kc < L && kc >= start && maskr[kc] != 0.0f;
-      const uint32_t abits = (uint32_t)__ballot(act);
-      if (q_live) w = abits & range_bits(0, q - k0);
-    }
-    const int nf = __syncthreads_or(nonfinite);
+    const float *Kc = Ks[cur];
+    const float *Vc = Vs[cur];
 
     if (__ballot(w != 0u) != 0) {
-      f32x4 s0, s1;
+      f32x4 s0, s1;  // two partial sums over alternate chunks of hd
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         s0[r] = 0.0f;
         s1[r] = 0.0f;
       }
-      // K operands are double-buffered one step ahead; the scheduling fences
-      // keep the compiler from hoisting every LDS read (and its registers) to
-      // the top of the loop.
-      const f32x4 *k0row = reinterpret_cast<const f32x4 *>(&Ks[col * KS + grp * QS]);
-      const f32x4 *k1row = reinterpret_cast<const f32x4 *>(&Ks[(16 + col) * KS + grp * QS]);
-      f32x4 ka = k0row[0], kb = k1row[0];
+      const f32x4 *krow = reinterpret_cast<const f32x4 *>(&Kc[col * KS + grp * QS]);
 #pragma unroll
       for (int c = 0; c < QS / 4; ++c) {
-        f32x4 na = ka, nb = kb;
-        if (c + 1 < QS / 4) {
-          na = k0row[c + 1];
-          nb = k1row[c + 1];
-        }
+        const f32x4 ka = krow[c];
+        if (c & 1) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          s0 = mfma_16x16x4(ka[e], qreg[4 * c + e], s0);
-          s1 = mfma_16x16x4(kb[e], qreg[4 * c + e], s1);
+          for (int e = 0; e < 4; ++e) s1 = mfma_16x16x4(ka[e], qreg[4 * c + e], s1);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) s0 = mfma_16x16x4(ka[e], qreg[4 * c + e], s0);
         }
-        __builtin_amdgcn_sched_barrier(0);
-        ka = na;
-        kb = nb;
+        if ((c & 3) == 3) __builtin_amdgcn_sched_barrier(0);
       }
-      const float alpha = softmax_tile16(s0, s1, w, grp, a.c1, m, l);
+      s0 += s1;
+      // masked softmax over the 16 keys (lane group g holds keys 4g + r)
+      float mx = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float x = ((w >> (4 * grp + r)) & 1u) ? s0[r] * a.c1 : -INFINITY;
+        s0[r] = x;
+        mx = fmaxf(mx, x);
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float mn = fmaxf(m, mx);
+      const float alpha = (m == mn) ? 1.0f : fast_exp2(m - mn);
+      float rs = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float e = __builtin_isfinite(s0[r]) ? fast_exp2(s0[r] - mn) : 0.0f;
+        s0[r] = e;
+        rs += e;
+      }
+      l = l * alpha + rs;
+      m = mn;
       if (alpha != 1.0f) {
 #pragma unroll
         for (int j = 0; j < NB; ++j) O[j] *= alpha;
       }
       if (!nf) {
-        const float *v0 = &Vs[(4 * grp) * KS + col];
-        const float *v1 = &Vs[(16 + 4 * grp) * KS + col];
-        float va[4], vb[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          va[r] = v0[r * KS];
-          vb[r] = v1[r * KS];
-        }
+        const float *v0 = &Vc[(4 * grp) * KS + col];
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
-          float na[4], nb[4];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            na[r] = va[r];
-            nb[r] = vb[r];
-            if (j + 1 < NB) {
-              na[r] = v0[r * KS + (j + 1) * 16];
-              nb[r] = v1[r * KS + (j + 1) * 16];
-            }
-          }
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            O[j] = mfma_16x16x4(va[r], s0[r], O[j]);
-            O[j] = mfma_16x16x4(vb[r], s1[r], O[j]);
-          }
-          __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            va[r] = na[r];
-            vb[r] = nb[r];
-          }
+          for (int r = 0; r < 4; ++r) O[j] = mfma_16x16x4(v0[r * KS + j * 16], s0[r], O[j]);
+          if ((j & 3) == 3) __builtin_amdgcn_sched_barrier(0);
         }
       } else {
         // Non-finite value in the tile: accumulate key by key, skipping p == 0
         // (lib.rs:746-748), so masked NaN/inf values never leak. The wave's
         // probabilities go through its own LDS slice (wave-local, in order).
-        float *pw = Ps + wave * (kKeyTile * kJeffWaveQueries);
+        float *pw = Ps + wave * (KT * kJeffWaveQueries);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          pw[(4 * grp + r) * kJeffWaveQueries + col] = s0[r];
-          pw[(16 + 4 * grp + r) * kJeffWaveQueries + col] = s1[r];
-        }
+        for (int r = 0; r < 4; ++r) pw[(4 * grp + r) * kJeffWaveQueries + col] = s0[r];
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma nounroll
-        for (int kx = 0; kx < kKeyTile; ++kx) {
+        for (int kx = 0; kx < KT; ++kx) {
           const float p = pw[kx * kJeffWaveQueries + col];
           if (p == 0.0f) continue;
-          const float *vrow = &Vs[kx * KS + 4 * grp];
+          const float *vrow = &Vc[kx * KS + 4 * grp];
 #pragma unroll
           for (int j = 0; j < NB; ++j) {
 #pragma unroll
@@ -318,7 +459,10 @@ __global__ __launch_bounds__(256, 2) void jeff_attention_f32_kernel(const JeffAr
         }
       }
     }
-    __syncthreads();
+    nonfinite = 0;
+    if (more) nonfinite = st.commit(Ks[cur ^ 1], Vs[cur ^ 1], tid);
+    nf = __syncthreads_or(nonfinite);
+    w = w_next;
   }
 
   // -------- o / sum (0 when nothing was kept), sigmoid gate, store
@@ -345,26 +489,40 @@ __global__ __launch_bounds__(256, 2) void jeff_attention_f32_kernel(const JeffAr
 // ----------------------------------------------------------------- launchers
 
 template <int HDP>
-static hipError_t launch_jeff_f32_hd(const JeffArgs &a, int rows, hipStream_t stream) {
+static hipError_t launch_jeff_f32_hd(const JeffArgs &a, int rows, float *kp, hipStream_t stream) {
+  dim3 pgrid((a.L + kKeyTile - 1) / kKeyTile, a.kv_heads, rows);
+  hipLaunchKernelGGL((jeff_k_prep_kernel<HDP, float>), pgrid, dim3(256), 0, stream, a, kp);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
   const int qsubs = kWavesPerGroup / a.heads_per_group;
   const int qt = kJeffWaveQueries * qsubs;
   dim3 grid((a.L + qt - 1) / qt, a.heads / a.heads_per_group, rows);
-  hipLaunchKernelGGL((jeff_attention_f32_kernel<HDP>), grid, dim3(256), 0, stream, a);
+  // 16-byte V loads along tokens need L % 4 == 0 and an aligned base.
+  const bool vec = a.L % 4 == 0 && (reinterpret_cast<uintptr_t>(a.v) & 15) == 0;
+  if (vec)
+    hipLaunchKernelGGL((jeff_attention_f32_kernel<HDP, true>), grid, dim3(256), 0, stream, a, kp);
+  else
+    hipLaunchKernelGGL((jeff_attention_f32_kernel<HDP, false>), grid, dim3(256), 0, stream, a, kp);
   return hipGetLastError();
 }
 
-hipError_t launch_jeff_attention_f32(const JeffArgs &a, int rows, int hd_pad,
+hipError_t launch_jeff_attention_f32(const JeffArgs &a, int rows, int hd_pad, void *kp,
                                      hipStream_t stream) {
+  float *k = static_cast<float *>(kp);
   switch (hd_pad) {
-    case 32: return launch_jeff_f32_hd<32>(a, rows, stream);
-    case 64: return launch_jeff_f32_hd<64>(a, rows, stream);
-    case 128: return launch_jeff_f32_hd<128>(a, rows, stream);
-    case 256: return launch_jeff_f32_hd<256>(a, rows, stream);
+    case 32: return launch_jeff_f32_hd<32>(a, rows, k, stream);
+    case 64: return launch_jeff_f32_hd<64>(a, rows, k, stream);
+    case 128: return launch_jeff_f32_hd<128>(a, rows, k, stream);
+    case 256: return launch_jeff_f32_hd<256>(a, rows, k, stream);
     default: return hipErrorInvalidValue;
   }
 }
 
-hipError_t launch_jeff_attention_bf16(const JeffArgs &, int, int, hipStream_t) {
+size_t jeff_kp_bytes(const JeffArgs &a, int rows, int hd_pad, bool bf16) {
+  return (size_t)rows * a.kv_heads * a.L * hd_pad * (bf16 ? 2 : 4);
+}
+
+hipError_t launch_jeff_attention_bf16(const JeffArgs &, int, int, void *, hipStream_t) {
   return hipErrorNotSupported;
 }
 

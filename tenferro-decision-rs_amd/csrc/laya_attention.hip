@@ -34,8 +34,13 @@ __global__ __launch_bounds__(256) void laya_keep_bits_kernel(const uint8_t *__re
   const uint8_t *base = keep + (size_t)L * L * b + q;
   const int k0 = kt * kKeyTile;
   const int n = min(kKeyTile, L - k0);
+  uint8_t v[kKeyTile];
+#pragma unroll
+  for (int kk = 0; kk < kKeyTile; ++kk)  // all loads in flight at once
+    v[kk] = kk < n ? base[(size_t)L * (k0 + kk)] : 0;
   uint32_t w = 0;
-  for (int kk = 0; kk < n; ++kk) w |= (uint32_t)(base[(size_t)L * (k0 + kk)] != 0) << kk;
+#pragma unroll
+  for (int kk = 0; kk < kKeyTile; ++kk) w |= (uint32_t)(v[kk] != 0) << kk;
   bits[((size_t)b * nkt + kt) * L + q] = w;
 }
 
@@ -47,27 +52,150 @@ __global__ __launch_bounds__(256) void laya_keep_bits_kernel(const uint8_t *__re
 __device__ __forceinline__ float rope_elem(const float *row, int dd, int hd, int half,
                                            const float *cr, const float *sr) {
 #pragma clang fp contract(off)
-  if (dd >= hd) return 0.0f;
-  const float x = row[dd];
-  if (cr == nullptr) return x;
-  if (dd < half) return x * cr[dd] - row[dd + half] * sr[dd];
-  if (dd < 2 * half) {
-    const int i = dd - half;
-    return row[i] * sr[i] + x * cr[i];
-  }
-  return x;
+  // Branch-free with clamped indices so that a caller's loads over many dd
+  // are all issued before the first is waited on.
+  const int dc = dd < hd ? dd : hd - 1;
+  const float x = row[dc];
+  if (cr == nullptr) return dd < hd ? x : 0.0f;
+  const bool lo = dc < half, hi = !lo && dc < 2 * half;
+  const int i = lo ? dc : (hi ? dc - half : 0);
+  const int partner = lo ? dc + half : (hi ? dc - half : dc);
+  const float y = row[partner];
+  const float c = half > 0 ? cr[i] : 1.0f, s = half > 0 ? sr[i] : 0.0f;
+  const float r = lo ? x * c - y * s : (hi ? y * s + x * c : x);
+  return dd < hd ? r : 0.0f;
 }
+
+// ------------------------------------------------------------------ staging
+
+// x*c - y*s and x*s + y*c elementwise, uncontracted like the reference.
+__device__ __forceinline__ f32x4 rot_lo(f32x4 x, f32x4 y, f32x4 c, f32x4 s) {
+#pragma clang fp contract(off)
+  return x * c - y * s;
+}
+__device__ __forceinline__ f32x4 rot_hi(f32x4 x, f32x4 y, f32x4 c, f32x4 s) {
+#pragma clang fp contract(off)
+  return x * s + y * c;
+}
+
+__device__ __forceinline__ bool all_finite(f32x4 v) {
+  return __builtin_isfinite(v[0]) && __builtin_isfinite(v[1]) && __builtin_isfinite(v[2]) &&
+         __builtin_isfinite(v[3]);
+}
+
+// One K/V tile's global data held in registers between the prefetch (issued
+// before the previous tile's products) and the LDS commit (after them).
+//
+// VEC (hd == HDP, hd % 8 == 0, 16-byte aligned rows): a K task is one
+// (key, chunk c) with its RoPE partner chunk c + half/4 and the table chunks,
+// all 16-byte loads; a V task is one (key, chunk). Otherwise (any hd) the
+// commit loads and rotates element by element and the prefetch is empty.
+template <int HDP, bool VEC>
+struct LayaStage {
+  static constexpr int KTASKS = kKeyTile * HDP / 8;
+  static constexpr int VTASKS = kKeyTile * HDP / 4;
+  static constexpr int KN = VEC ? (KTASKS + 255) / 256 : 1;
+  static constexpr int VN = VEC ? (VTASKS + 255) / 256 : 1;
+  f32x4 ka[KN], kb[KN], c[KN], s[KN];
+  f32x4 v[VN];
+
+  __device__ __forceinline__ void fetch(const LayaArgs &a, const float *xb, size_t tok, int k0,
+                                        int tid) {
+    if constexpr (VEC) {
+      const int hh = a.half;
+#pragma unroll
+      for (int i = 0; i < KN; ++i) {
+        const int task = tid + 256 * i;
+        const int key = k0 + task / (HDP / 8), cp = task % (HDP / 8);
+        f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+        ka[i] = kb[i] = z;
+        c[i] = {1.0f, 1.0f, 1.0f, 1.0f};
+        s[i] = z;
+        if (task < KTASKS && key < a.L) {
+          const float *row = xb + (size_t)key * tok + a.d;
+          ka[i] = *reinterpret_cast<const f32x4 *>(row + 4 * cp);
+          kb[i] = *reinterpret_cast<const f32x4 *>(row + 4 * cp + hh);
+          if (a.cos_t) {
+            c[i] = *reinterpret_cast<const f32x4 *>(a.cos_t + (size_t)key * hh + 4 * cp);
+            s[i] = *reinterpret_cast<const f32x4 *>(a.sin_t + (size_t)key * hh + 4 * cp);
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < VN; ++i) {
+        const int task = tid + 256 * i;
+        const int key = k0 + task / (HDP / 4), ch = task % (HDP / 4);
+        v[i] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (task < VTASKS && key < a.L)
+          v[i] = *reinterpret_cast<const f32x4 *>(xb + (size_t)key * tok + 2 * a.d + 4 * ch);
+      }
+    }
+  }
+
+  // Writes the tile to LDS (K rotated); returns 1 if a V value is NaN or inf.
+  __device__ __forceinline__ int commit(const LayaArgs &a, const float *xb, size_t tok, int k0,
+                                        int tid, float *Ks, float *Vs) {
+    constexpr int KS = HDP + 4, VS = HDP + 8;
+    int nonfinite = 0;
+    if constexpr (VEC) {
+      const int hh = a.half;
+      const bool rope = a.cos_t != nullptr;
+#pragma unroll
+      for (int i = 0; i < KN; ++i) {
+        const int task = tid + 256 * i;
+        if (task < KTASKS) {
+          const int kk = task / (HDP / 8), cp = task % (HDP / 8);
+          f32x4 lo = ka[i], hi = kb[i];
+          if (rope) {
+            lo = rot_lo(ka[i], kb[i], c[i], s[i]);
+            hi = rot_hi(ka[i], kb[i], c[i], s[i]);
+          }
+          *reinterpret_cast<f32x4 *>(&Ks[kk * KS + 4 * cp]) = lo;
+          *reinterpret_cast<f32x4 *>(&Ks[kk * KS + hh + 4 * cp]) = hi;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < VN; ++i) {
+        const int task = tid + 256 * i;
+        if (task < VTASKS) {
+          const int kk = task / (HDP / 4), ch = task % (HDP / 4);
+          nonfinite |= !all_finite(v[i]);
+          *reinterpret_cast<f32x4 *>(&Vs[kk * VS + 4 * ch]) = v[i];
+        }
+      }
+    } else {
+      const int L = a.L, hd = a.hd, hh = a.half;
+      const bool rope = a.cos_t != nullptr;
+      for (int e = tid; e < kKeyTile * HDP; e += 256) {
+        const int kk = e / HDP, dd = e % HDP;
+        const int key = k0 + kk;
+        float kv = 0.0f, vv = 0.0f;
+        if (key < L && dd < hd) {
+          const float *row = xb + (size_t)key * tok;
+          const float *cr = rope ? a.cos_t + (size_t)key * hh : nullptr;
+          const float *sr = rope ? a.sin_t + (size_t)key * hh : nullptr;
+          kv = rope_elem(row + a.d, dd, hd, hh, cr, sr);
+          vv = row[2 * a.d + dd];
+          nonfinite |= !__builtin_isfinite(vv);
+        }
+        Ks[kk * KS + dd] = kv;
+        Vs[kk * VS + dd] = vv;
+      }
+    }
+    return nonfinite;
+  }
+};
 
 // ------------------------------------------------------------------- kernel
 
-template <int HDP, int MODE>
+template <int HDP, int MODE, bool VEC>
 __global__ __launch_bounds__(256) void laya_attention_kernel(const LayaArgs a) {
   constexpr int KS = HDP + 4;  // K row stride (floats): 16-byte rows, conflict-free b128 reads
   constexpr int VS = HDP + 8;  // V row stride: the two lane halves read rows 4 apart
   constexpr int QS = HDP / 2;  // Q registers per lane
   constexpr int NB = HDP / 32; // 32-row blocks of O^T
-  __shared__ __attribute__((aligned(16))) float Ks[kKeyTile * KS];
-  __shared__ __attribute__((aligned(16))) float Vs[kKeyTile * VS];
+  __shared__ __attribute__((aligned(16))) float Ks[2][kKeyTile * KS];
+  __shared__ __attribute__((aligned(16))) float Vs[2][kKeyTile * VS];
   __shared__ int s_span[3];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -90,12 +218,22 @@ __global__ __launch_bounds__(256) void laya_attention_kernel(const LayaArgs a) {
   __syncthreads();
   if (MODE == kMaskBits) {
     int lo = 0x7fffffff, hi = -1;
-    for (int i = tid; i < kLayaGroupQueries * nkt; i += 256) {
-      const int qq = qg0 + (i & (kLayaGroupQueries - 1));
-      const int kt = i / kLayaGroupQueries;
-      if (qq < L && a.bits[((size_t)b * nkt + kt) * L + qq] != 0u) {
-        lo = min(lo, kt);
-        hi = max(hi, kt);
+    for (int i0 = 0; i0 < kLayaGroupQueries * nkt; i0 += 256 * 8) {
+      uint32_t word[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {  // 8 loads in flight per thread
+        const int i = i0 + tid + 256 * u;
+        const int qq = qg0 + (i & (kLayaGroupQueries - 1));
+        const int kt = i / kLayaGroupQueries;
+        word[u] = (i < kLayaGroupQueries * nkt && qq < L) ? a.bits[((size_t)b * nkt + kt) * L + qq] : 0u;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int kt = (i0 + tid + 256 * u) / kLayaGroupQueries;
+        if (word[u] != 0u) {
+          lo = min(lo, kt);
+          hi = max(hi, kt);
+        }
       }
     }
     lo = wave_min(lo);
@@ -107,10 +245,20 @@ __global__ __launch_bounds__(256) void laya_attention_kernel(const LayaArgs a) {
   } else {
     const uint8_t *vb = a.valid + (size_t)b * L;
     int lo = 0x7fffffff, hi = -1, padded = 0;
-    for (int k = tid; k < L; k += 256) {
-      if (vb[k]) {
-        lo = min(lo, k);
-        hi = max(hi, k);
+    for (int k0 = 0; k0 < L; k0 += 256 * 8) {
+      uint8_t v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int k = k0 + tid + 256 * u;
+        v[u] = k < L ? vb[k] : 0;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int k = k0 + tid + 256 * u;
+        if (v[u]) {
+          lo = min(lo, k);
+          hi = max(hi, k);
+        }
       }
     }
     if (tid < kLayaGroupQueries) {
@@ -153,46 +301,46 @@ __global__ __launch_bounds__(256) void laya_attention_kernel(const LayaArgs a) {
   {
     const int qq = qin ? q : 0;
     const float *row = xb + (size_t)qq * tok;
-    const float *cr = rope ? a.cos_t + (size_t)qq * hh : nullptr;
-    const float *sr = rope ? a.sin_t + (size_t)qq * hh : nullptr;
+    if constexpr (VEC) {
+      // hd == HDP: this lane's half of the row and its RoPE partner half are
+      // the two halves of the row; 16-byte loads, all in flight together.
+      f32x4 lo[QS / 4], hi[QS / 4], cs[QS / 4], sn[QS / 4];
 #pragma unroll
-    for (int s = 0; s < QS; ++s) qreg[s] = qin ? rope_elem(row, half * QS + s, hd, hh, cr, sr) : 0.0f;
+      for (int c = 0; c < QS / 4; ++c) {
+        lo[c] = reinterpret_cast<const f32x4 *>(row)[c];
+        hi[c] = reinterpret_cast<const f32x4 *>(row + QS)[c];
+        cs[c] = f32x4{1.0f, 1.0f, 1.0f, 1.0f};
+        sn[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (rope) {
+          cs[c] = reinterpret_cast<const f32x4 *>(a.cos_t + (size_t)qq * hh)[c];
+          sn[c] = reinterpret_cast<const f32x4 *>(a.sin_t + (size_t)qq * hh)[c];
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < QS / 4; ++c) {
+        f32x4 v = half ? hi[c] : lo[c];
+        if (rope) v = half ? rot_hi(lo[c], hi[c], cs[c], sn[c]) : rot_lo(lo[c], hi[c], cs[c], sn[c]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) qreg[4 * c + e] = qin ? v[e] : 0.0f;
+      }
+    } else {
+      const float *cr = rope ? a.cos_t + (size_t)qq * hh : nullptr;
+      const float *sr = rope ? a.sin_t + (size_t)qq * hh : nullptr;
+#pragma unroll
+      for (int s = 0; s < QS; ++s)
+        qreg[s] = qin ? rope_elem(row, half * QS + s, hd, hh, cr, sr) : 0.0f;
+    }
   }
   bool q_valid = false;
   if (MODE == kMaskStruct) q_valid = qin && a.valid[(size_t)b * L + q] != 0;
 
-  f32x16 O[NB];
-#pragma unroll
-  for (int j = 0; j < NB; ++j)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) O[j][r] = 0.0f;
-  float m = -INFINITY, l = 0.0f;
-
-  for (int kt = kt_begin; kt < kt_end; ++kt) {
-    const int k0 = kt * kKeyTile;
-    // -------- stage K (rotated) and V (as is; the MFMA product only runs on
-    // tiles whose V is all finite)
-    int nonfinite = 0;
-    for (int e = tid; e < kKeyTile * HDP; e += 256) {
-      const int kk = e / HDP, dd = e % HDP;
-      const int key = k0 + kk;
-      float kv = 0.0f, vv = 0.0f;
-      if (key < L && dd < hd) {
-        const float *row = xb + (size_t)key * tok;
-        const float *cr = rope ? a.cos_t + (size_t)key * hh : nullptr;
-        const float *sr = rope ? a.sin_t + (size_t)key * hh : nullptr;
-        kv = rope_elem(row + a.d, dd, hd, hh, cr, sr);
-        vv = row[2 * a.d + dd];
-        nonfinite |= !__builtin_isfinite(vv);
-      }
-      Ks[kk * KS + dd] = kv;
-      Vs[kk * VS + dd] = vv;
-    }
-    // -------- this lane's keep word for the tile
+  // This lane's keep word for key tile kt (bit j: key 32*kt + j).
+  auto keep_word = [&](int kt) -> uint32_t {
     uint32_t w = 0u;
     if (MODE == kMaskBits) {
       if (qin) w = a.bits[((size_t)b * nkt + kt) * L + q];
     } else {
+      const int k0 = kt * kKeyTile;
       const int key = k0 + col;
       const bool kv = key < L && a.valid[(size_t)b * L + key] != 0;
       const uint32_t vbits = (uint32_t)__ballot(kv);  // lanes 0..31 = keys of the tile
@@ -201,13 +349,45 @@ __global__ __launch_bounds__(256) void laya_attention_kernel(const LayaArgs a) {
         if (a.window >= 0 && q_valid) w &= range_bits(q - a.window - k0, q + a.window - k0);
       }
     }
-    const int nf = __syncthreads_or(nonfinite);
+    return w;
+  };
+
+  f32x16 O[NB];
+#pragma unroll
+  for (int j = 0; j < NB; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) O[j][r] = 0.0f;
+  float m = -INFINITY, l = 0.0f;
+
+  // -------- software pipeline: tile kt+1 is fetched into registers before
+  // the products of tile kt and committed to the other LDS buffer after
+  // them; one barrier per tile.
+  LayaStage<HDP, VEC> st;
+  int nonfinite = 0;
+  uint32_t w = 0u;
+  if (kt_begin < kt_end) {
+    st.fetch(a, xb, tok, kt_begin * kKeyTile, tid);
+    nonfinite = st.commit(a, xb, tok, kt_begin * kKeyTile, tid, Ks[0], Vs[0]);
+    w = keep_word(kt_begin);
+  }
+  int nf = __syncthreads_or(nonfinite);
+
+  for (int kt = kt_begin; kt < kt_end; ++kt) {
+    const int cur = (kt - kt_begin) & 1;
+    const bool more = kt + 1 < kt_end;
+    uint32_t w_next = 0u;
+    if (more) {
+      st.fetch(a, xb, tok, (kt + 1) * kKeyTile, tid);
+      w_next = keep_word(kt + 1);
+    }
+    const float *Kc = Ks[cur];
+    const float *Vc = Vs[cur];
 
     if (__ballot(w != 0u) != 0) {  // wave-uniform: skip tiles this wave never keeps
       f32x16 s;
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[r] = 0.0f;
-      const f32x4 *krow = reinterpret_cast<const f32x4 *>(&Ks[col * KS + half * QS]);
+      const f32x4 *krow = reinterpret_cast<const f32x4 *>(&Kc[col * KS + half * QS]);
 #pragma unroll
       for (int c = 0; c < QS / 4; ++c) {
         const f32x4 kv = krow[c];
@@ -226,7 +406,7 @@ __global__ __launch_bounds__(256) void laya_attention_kernel(const LayaArgs a) {
         for (int j = 0; j < NB; ++j)
 #pragma unroll
           for (int r = 0; r < 16; ++r)
-            O[j] = mfma_32x32x2(Vs[acc_row(r, half) * VS + j * 32 + col], s[r], O[j]);
+            O[j] = mfma_32x32x2(Vc[acc_row(r, half) * VS + j * 32 + col], s[r], O[j]);
       } else {
         // A value in this tile is NaN or infinite: accumulate key by key and
         // skip zero probabilities, as the reference's scalar path does
@@ -237,11 +417,14 @@ __global__ __launch_bounds__(256) void laya_attention_kernel(const LayaArgs a) {
 #pragma unroll
           for (int j = 0; j < NB; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) O[j][r] += p * Vs[kk * VS + j * 32 + acc_row(r, half)];
+            for (int r = 0; r < 16; ++r) O[j][r] += p * Vc[kk * VS + j * 32 + acc_row(r, half)];
         }
       }
     }
-    __syncthreads();
+    nonfinite = 0;
+    if (more) nonfinite = st.commit(a, xb, tok, (kt + 1) * kKeyTile, tid, Ks[cur ^ 1], Vs[cur ^ 1]);
+    nf = __syncthreads_or(nonfinite);
+    w = w_next;
   }
 
   // -------- normalize and store: out[feat + d + hidden*(q + L*b)]
@@ -283,23 +466,35 @@ hipError_t launch_laya_keep_bits(const uint8_t *keep, uint32_t *bits, int L, int
   return hipGetLastError();
 }
 
-template <int HDP>
+template <int HDP, bool VEC>
 static hipError_t launch_laya_hd(const LayaArgs &a, int heads, int batch, int mode,
                                  hipStream_t stream) {
   dim3 grid((a.L + kLayaGroupQueries - 1) / kLayaGroupQueries, heads, batch);
   if (mode == kMaskBits)
-    hipLaunchKernelGGL((laya_attention_kernel<HDP, kMaskBits>), grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((laya_attention_kernel<HDP, kMaskBits, VEC>), grid, dim3(256), 0, stream, a);
   else
-    hipLaunchKernelGGL((laya_attention_kernel<HDP, kMaskStruct>), grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((laya_attention_kernel<HDP, kMaskStruct, VEC>), grid, dim3(256), 0, stream,
+                       a);
   return hipGetLastError();
+}
+
+template <int HDP>
+static hipError_t launch_laya_pick(const LayaArgs &a, int heads, int batch, int mode,
+                                   hipStream_t stream) {
+  // 16-byte row loads need hd == HDP, hd % 8 == 0 (RoPE halves in whole
+  // chunks), a row stride of whole chunks and an aligned base.
+  const bool vec = a.hd == HDP && a.hd % 8 == 0 && a.d % 4 == 0 &&
+                   (reinterpret_cast<uintptr_t>(a.qkv) & 15) == 0;
+  return vec ? launch_laya_hd<HDP, true>(a, heads, batch, mode, stream)
+             : launch_laya_hd<HDP, false>(a, heads, batch, mode, stream);
 }
 
 hipError_t launch_laya_attention(const LayaArgs &a, int heads, int batch, int hd_pad, int mode,
                                  hipStream_t stream) {
   switch (hd_pad) {
-    case 32: return launch_laya_hd<32>(a, heads, batch, mode, stream);
-    case 64: return launch_laya_hd<64>(a, heads, batch, mode, stream);
-    case 128: return launch_laya_hd<128>(a, heads, batch, mode, stream);
+    case 32: return launch_laya_pick<32>(a, heads, batch, mode, stream);
+    case 64: return launch_laya_pick<64>(a, heads, batch, mode, stream);
+    case 128: return launch_laya_pick<128>(a, heads, batch, mode, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -47,11 +47,13 @@ struct RopeEntry {
 struct tfd_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
+  bool adopted = false;  // stream given by the caller (may be the null stream)
   bool own_stream = false;
   bool ready = false;
   std::string err;
   DevBuf staging[8];  // uploads of host-pointer operands
   DevBuf bits;        // Laya packed keep words
+  DevBuf kp;          // Jeff normalized + rotated keys
   std::vector<RopeEntry> rope;
   uint64_t clock = 0;
   bool timing = false;
@@ -102,7 +104,7 @@ int ensure_ready(tfd_ctx *c) {
     return fail(c, TFD_EHIP, "device %d out of range (%d devices)", c->device, count);
   TFD_HIP(c, hipSetDevice(c->device), "hipSetDevice");
   if (!c->ready) {
-    if (c->stream == nullptr) {
+    if (!c->adopted) {
       TFD_HIP(c, hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreate");
       c->own_stream = true;
     }
@@ -397,10 +399,11 @@ int jeff_run(tfd_ctx *c, const char *op, bool bf16, size_t rows, size_t length, 
                          &a.sin_t)))
       return rc;
   }
+  if ((rc = reserve(c, c->kp, tfd::jeff_kp_bytes(a, (int)rows, hd_pad, bf16)))) return rc;
   hipEvent_t after;
   if ((rc = timing_begin(c, &after))) return rc;
-  hipError_t e = bf16 ? tfd::launch_jeff_attention_bf16(a, (int)rows, hd_pad, c->stream)
-                      : tfd::launch_jeff_attention_f32(a, (int)rows, hd_pad, c->stream);
+  hipError_t e = bf16 ? tfd::launch_jeff_attention_bf16(a, (int)rows, hd_pad, c->kp.ptr, c->stream)
+                      : tfd::launch_jeff_attention_f32(a, (int)rows, hd_pad, c->kp.ptr, c->stream);
   if ((rc = timing_end(c, after))) return rc;
   if (e == hipErrorNotSupported)
     return fail(c, TFD_EUNSUPPORTED, "%s: this variant is not available", op);
@@ -452,6 +455,7 @@ int tfd_ctx_create_on_stream(int device, void *stream, tfd_ctx **out) {
   int rc = tfd_ctx_create(device, out);
   if (rc) return rc;
   (*out)->stream = static_cast<hipStream_t>(stream);
+  (*out)->adopted = true;
   return TFD_OK;
 }
 
@@ -463,6 +467,7 @@ void tfd_ctx_destroy(tfd_ctx *c) {
     for (auto &b : c->staging)
       if (b.ptr) (void)hipFree(b.ptr);
     if (c->bits.ptr) (void)hipFree(c->bits.ptr);
+    if (c->kp.ptr) (void)hipFree(c->kp.ptr);
     for (auto &e : c->rope) {
       (void)hipFree(e.cos_d);
       (void)hipFree(e.sin_d);
@@ -491,7 +496,7 @@ void *tfd_ctx_stream(tfd_ctx *c) {
 
 size_t tfd_ctx_retained_bytes(const tfd_ctx *c) {
   if (!c) return 0;
-  size_t total = sizeof(tfd_ctx) + c->bits.cap;
+  size_t total = sizeof(tfd_ctx) + c->bits.cap + c->kp.cap;
   for (const auto &b : c->staging) total += b.cap;
   for (const auto &e : c->rope) total += e.bytes;
   return total;

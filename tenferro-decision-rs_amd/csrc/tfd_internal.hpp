@@ -15,6 +15,7 @@ constexpr int kWaveQueries = 32;
 constexpr int kWavesPerGroup = 4;   // 256 threads per workgroup
 constexpr int kLayaGroupQueries = kWaveQueries * kWavesPerGroup;
 constexpr int kJeffWaveQueries = 16;  // Jeff waves use the 16x16x4 MFMA
+constexpr int kJeffKeyTile = 16;      // keys per Jeff f32 tile
 
 enum LayaMaskMode : int {
   kMaskBits = 0,    // general (L, L, B) keep tensor, pre-packed into 32-key words
@@ -53,9 +54,12 @@ hipError_t launch_laya_keep_bits(const uint8_t *keep, uint32_t *bits, int L, int
                                  hipStream_t stream);
 hipError_t launch_laya_attention(const LayaArgs &a, int heads, int batch, int hd_pad, int mode,
                                  hipStream_t stream);
-hipError_t launch_jeff_attention_f32(const JeffArgs &a, int rows, int hd_pad,
+// Jeff launchers run a K prep kernel into `kp` (workspace of
+// jeff_kp_bytes()) and then the attention kernel.
+size_t jeff_kp_bytes(const JeffArgs &a, int rows, int hd_pad, bool bf16);
+hipError_t launch_jeff_attention_f32(const JeffArgs &a, int rows, int hd_pad, void *kp,
                                      hipStream_t stream);
-hipError_t launch_jeff_attention_bf16(const JeffArgs &a, int rows, int hd_pad,
+hipError_t launch_jeff_attention_bf16(const JeffArgs &a, int rows, int hd_pad, void *kp,
                                       hipStream_t stream);
 
 }  // namespace tfd

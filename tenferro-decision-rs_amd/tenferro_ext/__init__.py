@@ -105,6 +105,14 @@ def load_library(path: Optional[str] = None) -> ctypes.CDLL:
             f"{path} is not built; run `make -C tenferro-decision-rs_amd` "
             "(there is no CPU fallback for these ops)"
         )
+    # torch ships its own HIP runtime with the same soname (libamdhip64.so.7)
+    # but loads it under another name, so two runtimes end up in one process
+    # if the library is loaded first. Loading torch first makes the library
+    # bind to the runtime torch already holds: one HIP runtime per process.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = ctypes.CDLL(path)
     P, S, U32, I, F = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint32, ctypes.c_int, ctypes.c_uint
     SP = ctypes.POINTER(ctypes.c_size_t)
