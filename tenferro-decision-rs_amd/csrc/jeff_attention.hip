@@ -177,7 +177,8 @@ __global__ __launch_bounds__(256) void jeff_k_prep_kernel(const JeffArgs a, OutT
 
 // Tile data for one 16-key tile, prefetched into registers: finished K rows
 // from the prep workspace (16-byte loads) and the V columns (16-byte loads
-// along tokens when VEC, else element loads), written to LDS as [key][d].
+// along tokens when VEC, else element loads). LDS holds K as [key][d] and V
+// as [d][key], V's layout in global memory.
 template <int HDP, bool VEC>
 struct JeffStage {
   static constexpr int KT = kJeffKeyTile;
@@ -215,6 +216,7 @@ struct JeffStage {
 
   __device__ __forceinline__ int commit(float *Ks, float *Vs, int tid) {
     constexpr int KS = HDP + 4;
+    constexpr int VS = KT + 4;
     int nonfinite = 0;
 #pragma unroll
     for (int i = 0; i < KN; ++i) {
@@ -227,11 +229,14 @@ struct JeffStage {
       const int e = tid + 256 * i;
       const int d = e / (KT / 4), g = e % (KT / 4);
       if (e >= TASKS) continue;
+      f32x4 x = v[i];
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        nonfinite |= !__builtin_isfinite(v[i][t]);
-        Vs[(4 * g + t) * KS + d] = v[i][t];
+        const bool fin = __builtin_isfinite(x[t]);
+        nonfinite |= !fin;
+        x[t] = fin ? x[t] : 0.0f;
       }
+      *reinterpret_cast<f32x4 *>(&Vs[d * VS + 4 * g]) = x;
     }
     return nonfinite;
   }
@@ -243,14 +248,15 @@ __global__ __launch_bounds__(256, 2) void jeff_attention_f32_kernel(const JeffAr
   constexpr int KT = kJeffKeyTile;  // 16 keys per tile
   constexpr int QS = HDP / 4;       // Q registers per lane (4 lane groups split hd)
   constexpr int NB = HDP / 16;      // 16-row blocks of O^T
-  constexpr int KS = HDP + 4;       // K and V stored [key][d]
+  constexpr int KS = HDP + 4;       // K stored [key][d]
+  constexpr int VS = KT + 4;        // V stored [d][key]: conflict-free 16-byte reads
+  constexpr int KBUF = KT * KS, VBUF = HDP * VS;
   // K and V double buffers; before the key loop the same bytes hold each
   // wave's raw Q tile (16 queries x (HDP + 1)) for the Q prep.
-  static_assert(kWavesPerGroup * kJeffWaveQueries * (HDP + 1) <= 4 * KT * KS, "Q scratch");
-  __shared__ __attribute__((aligned(16))) float smem[4 * KT * KS];
-  float(*Ks)[KT * KS] = reinterpret_cast<float(*)[KT * KS]>(smem);
-  float(*Vs)[KT * KS] = reinterpret_cast<float(*)[KT * KS]>(smem + 2 * KT * KS);
-  __shared__ float Ps[kWavesPerGroup * KT * kJeffWaveQueries];
+  static_assert(kWavesPerGroup * kJeffWaveQueries * (HDP + 1) <= 2 * (KBUF + VBUF), "Q scratch");
+  __shared__ __attribute__((aligned(16))) float smem[2 * (KBUF + VBUF)];
+  float(*Ks)[KBUF] = reinterpret_cast<float(*)[KBUF]>(smem);
+  float(*Vs)[VBUF] = reinterpret_cast<float(*)[VBUF]>(smem + 2 * KBUF);
   __shared__ int s_span[2];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -369,6 +375,7 @@ __global__ __launch_bounds__(256, 2) void jeff_attention_f32_kernel(const JeffAr
     w = keep_word(kt_begin);
   }
   int nf = __syncthreads_or(nonfinite);
+  int any_nf = 0;  // workgroup-uniform: some staged V value was NaN or inf
 
   for (int kt = kt_begin; kt < kt_end; ++kt) {
     const int cur = (kt - kt_begin) & 1;
@@ -427,47 +434,57 @@ __global__ __launch_bounds__(256, 2) void jeff_attention_f32_kernel(const JeffAr
 #pragma unroll
         for (int j = 0; j < NB; ++j) O[j] *= alpha;
       }
-      if (!nf) {
-        const float *v0 = &Vc[(4 * grp) * KS + col];
+      // V tiles are staged with NaN/inf replaced by 0, so this product is
+      // the exact sum over the finite values; the non-finite ones are folded
+      // in after the key loop.
+      // A operand of block j: V[key 4*grp + r][d = 16*j + col], one 16-byte read.
+      const float *v0 = &Vc[col * VS + 4 * grp];
 #pragma unroll
-        for (int j = 0; j < NB; ++j) {
+      for (int j = 0; j < NB; ++j) {
+        const f32x4 vv = *reinterpret_cast<const f32x4 *>(v0 + j * 16 * VS);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) O[j] = mfma_16x16x4(v0[r * KS + j * 16], s0[r], O[j]);
-          if ((j & 3) == 3) __builtin_amdgcn_sched_barrier(0);
-        }
-      } else {
-        // Non-finite value in the tile: accumulate key by key, skipping p == 0
-        // (lib.rs:746-748), so masked NaN/inf values never leak. The wave's
-        // probabilities go through its own LDS slice (wave-local, in order).
-        float *pw = Ps + wave * (KT * kJeffWaveQueries);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) pw[(4 * grp + r) * kJeffWaveQueries + col] = s0[r];
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma nounroll
-        for (int kx = 0; kx < KT; ++kx) {
-          const float p = pw[kx * kJeffWaveQueries + col];
-          if (p == 0.0f) continue;
-          const float *vrow = &Vc[kx * KS + 4 * grp];
-#pragma unroll
-          for (int j = 0; j < NB; ++j) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) O[j][r] += p * vrow[j * 16 + r];
-            if ((j & 3) == 3) __builtin_amdgcn_sched_barrier(0);
-          }
-        }
+        for (int r = 0; r < 4; ++r) O[j] = mfma_16x16x4(vv[r], s0[r], O[j]);
+        if ((j & 3) == 3) __builtin_amdgcn_sched_barrier(0);
       }
     }
+    any_nf |= nf;
     nonfinite = 0;
     if (more) nonfinite = st.commit(Ks[cur ^ 1], Vs[cur ^ 1], tid);
     nf = __syncthreads_or(nonfinite);
     w = w_next;
   }
 
+  // -------- non-finite values of kept keys (rare): o = sum p*v over p != 0
+  // (lib.rs:746-748) is +-inf or NaN wherever such a value is kept. A kept
+  // key's p is never 0 here: q and k are RMS-normalized, so |score| stays
+  // far from exp's underflow. Flags per output: bit 0 NaN, 1 +inf, 2 -inf.
+  uint32_t special[NB];
+#pragma unroll
+  for (int j = 0; j < NB; ++j) special[j] = 0u;
+  if (any_nf) {
+    const int k_lo = kt_begin * KT, k_hi = min(kt_end * KT, L);
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int d = j * 16 + 4 * grp + r;
+        uint32_t f = 0u;
+        if (q_live && d < hd) {
+#pragma nounroll
+          for (int k = k_lo; k < k_hi && k <= q; ++k) {
+            if (k < start || maskr[k] == 0.0f) continue;
+            const float v = V[k + (size_t)L * d];
+            if (!__builtin_isfinite(v)) f |= __builtin_isnan(v) ? 1u : (v > 0.0f ? 2u : 4u);
+          }
+        }
+        special[j] |= f << (8 * r);
+      }
+  }
+
   // -------- o / sum (0 when nothing was kept), sigmoid gate, store
   float lt = l + __shfl_xor(l, 16);
   lt += __shfl_xor(lt, 32);
+  const float inv = lt > 0.0f ? fast_rcp(lt) : 0.0f;
   if (qin) {
     const bool dropped = a.trim && q < start;
 #pragma unroll
@@ -477,10 +494,10 @@ __global__ __launch_bounds__(256, 2) void jeff_attention_f32_kernel(const JeffAr
         const int d = j * 16 + 4 * grp + r;
         if (d < hd) {
           const size_t at = q + (size_t)L * d;
-          const float o = lt > 0.0f ? O[j][r] / lt : 0.0f;
-          const float g = Gt[at];
-          const float sig = 1.0f / (1.0f + expf(-g));
-          OUT[at] = dropped ? 0.0f : o * sig;
+          float o = O[j][r] * inv;
+          const uint32_t f = (special[j] >> (8 * r)) & 7u;
+          if (f) o = ((f & 1u) || f == 6u) ? __builtin_nanf("") : (f == 2u ? INFINITY : -INFINITY);
+          OUT[at] = dropped ? 0.0f : o * fast_sigmoid(Gt[at]);
         }
       }
   }

@@ -428,7 +428,9 @@ __global__ __launch_bounds__(256) void laya_attention_kernel(const LayaArgs a) {
   }
 
   // -------- normalize and store: out[feat + d + hidden*(q + L*b)]
+  // 0/0 gives NaN for a query that kept nothing, as the reference does.
   const float lt = l + __shfl_xor(l, 32);
+  const float inv = lt > 0.0f ? fast_rcp(lt) : __builtin_nanf("");
   if (qin) {
     float *orow = a.out + ((size_t)b * L + q) * a.d + (size_t)head * hd;
 #pragma unroll
@@ -436,7 +438,7 @@ __global__ __launch_bounds__(256) void laya_attention_kernel(const LayaArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int dd = j * 32 + acc_row(r, half);
-        if (dd < hd) orow[dd] = O[j][r] / lt;
+        if (dd < hd) orow[dd] = O[j][r] * inv;
       }
   }
 }

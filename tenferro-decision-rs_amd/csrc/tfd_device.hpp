@@ -37,6 +37,15 @@ __device__ __forceinline__ uint32_t range_bits(int lo, int hi) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// 1 / x to 1 ulp (hardware reciprocal).
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+
+// 1 / (1 + exp(-g)) with the hardware exp2 and reciprocal (a few ulp from
+// the libm evaluation the reference uses).
+__device__ __forceinline__ float fast_sigmoid(float g) {
+  return fast_rcp(1.0f + fast_exp2(-g * 1.4426950408889634f));
+}
+
 __device__ __forceinline__ int wave_min(int v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o));

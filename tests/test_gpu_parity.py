@@ -222,6 +222,27 @@ def test_jeff_masked_nonfinite_values_and_empty_rows(gpu_ctx):
     assert np.all(out[:, :3] == 0.0)  # no active key at or before these queries
 
 
+@pytest.mark.parametrize("hd", [16, 256])
+def test_jeff_kept_nonfinite_values_propagate(gpu_ctx, hd):
+    """Kept inf / NaN values reach exactly the outputs whose p is non-zero."""
+    length, heads = 50, 2
+    q, k, v, g, qn, kn, mask = jeff_case(9, length, heads, hd, heads, False)
+    mask[:4] = 0.0
+    V = v.reshape(heads * hd, length)
+    V[3, 10] = np.inf
+    V[3, 20] = -np.inf      # +inf and -inf both kept from query 20 on: NaN
+    V[hd + 1, 30] = np.nan
+    V[5, 2] = np.nan        # masked: must not leak
+    want = oracle.jeff_full_attention(q, k, v, g, qn, kn, mask, length, heads, hd, 8, 1e4, 1e-6)
+    got = np.asarray(te.jeff_full_attention(q, k, v, g, qn, kn, mask, heads, hd, 8, 1e4, 1e-6,
+                                            q_shape=(length, heads * hd), ctx=gpu_ctx))
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.array_equal(np.isposinf(got), np.isposinf(want))
+    assert np.array_equal(np.isneginf(got), np.isneginf(want))
+    fin = np.isfinite(want)
+    assert np.abs(got[fin] - want[fin]).max() <= F32_TOL
+
+
 def test_jeff_c4_full_gqa_and_dropin(gpu_ctx):
     """C4 at full size: GQA rows entry (k/v at kv width) and the drop-in op
     row by row on expanded K/V, both against the oracle."""
