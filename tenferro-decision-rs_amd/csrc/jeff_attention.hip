@@ -59,7 +59,8 @@ __device__ __forceinline__ void scan_active(const float *maskr, int L, int tid, 
 #pragma unroll
     for (int u = 0; u < 8; ++u) {  // 8 loads in flight per thread
       const int k = k0 + tid + 256 * u;
-      v[u] = k < L ? maskr[k] : 0.0f;
+      const float x = maskr[min(k, L - 1)];
+      v[u] = k < L ? x : 0.0f;
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
@@ -140,22 +141,36 @@ __global__ __launch_bounds__(256) void jeff_k_prep_kernel(const JeffArgs a, OutT
 #pragma unroll
     for (int p = 0; p < 8; ++p) tot += s_red[p * kKeyTile + kk];
     const float scale = rms_scale(tot, hd, a.eps);
-#pragma unroll 4
+    float wn[DP];
+#pragma unroll
+    for (int i = 0; i < DP; ++i) wn[i] = a.k_norm[min(part * DP + i, hd - 1)];
+#pragma unroll
     for (int i = 0; i < DP; ++i) {
       const int d = part * DP + i;
-      if (kin && d < hd) Kt[kk * KS + d] = rms_apply(Kt[kk * KS + d], scale, a.k_norm[d]);
+      if (kin && d < hd) Kt[kk * KS + d] = rms_apply(Kt[kk * KS + d], scale, wn[i]);
     }
   }
   if (a.cos_t != nullptr && rh > 0) {
     __syncthreads();
-    for (int e = tid; e < kKeyTile * rh; e += 256) {
-      const int k2 = e / rh, i = e - k2 * rh;
-      if (k0 + k2 < L) {
-        const int pos = max(k0 + k2 - start, 0);
-        const float c = a.cos_t[(size_t)pos * rh + i], sn = a.sin_t[(size_t)pos * rh + i];
-        const float x = Kt[k2 * KS + i], y = Kt[k2 * KS + i + rh];
-        Kt[k2 * KS + i] = rope_lo(x, y, c, sn);
-        Kt[k2 * KS + i + rh] = rope_hi(x, y, c, sn);
+    for (int e0 = 0; e0 < kKeyTile * rh; e0 += 256 * 4) {
+      float c[4], sn[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {  // clamped table loads, all in flight
+        const int e = min(e0 + tid + 256 * u, kKeyTile * rh - 1);
+        const int k2 = e / rh, i = e - k2 * rh;
+        const int pos = min(max(k0 + k2 - start, 0), L - 1);
+        c[u] = a.cos_t[(size_t)pos * rh + i];
+        sn[u] = a.sin_t[(size_t)pos * rh + i];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int e = e0 + tid + 256 * u;
+        const int k2 = e / rh, i = e - k2 * rh;
+        if (e < kKeyTile * rh && k0 + k2 < L) {
+          const float x = Kt[k2 * KS + i], y = Kt[k2 * KS + i + rh];
+          Kt[k2 * KS + i] = rope_lo(x, y, c[u], sn[u]);
+          Kt[k2 * KS + i + rh] = rope_hi(x, y, c[u], sn[u]);
+        }
       }
     }
   }
@@ -189,40 +204,39 @@ struct JeffStage {
 
   __device__ __forceinline__ void fetch(const float *kp_tile, const float *V, int L, int hd,
                                         int k0, int tid) {
+    // Unconditional loads with clamped indices (all in flight together);
+    // keys past L and features past hd are zeroed at commit time.
 #pragma unroll
     for (int i = 0; i < KN; ++i) {
-      const int e = tid + 256 * i;  // chunk of the contiguous KT x HDP tile
-      k[i] = {0.0f, 0.0f, 0.0f, 0.0f};
-      if (e < TASKS && k0 + (4 * e) / HDP < L) k[i] = reinterpret_cast<const f32x4 *>(kp_tile)[e];
+      const int e = min(tid + 256 * i, TASKS - 1);  // chunk of the contiguous KT x HDP tile
+      const int kk = min((4 * e) / HDP, L - 1 - k0);
+      k[i] = reinterpret_cast<const f32x4 *>(kp_tile)[kk * (HDP / 4) + e % (HDP / 4)];
     }
 #pragma unroll
     for (int i = 0; i < VN; ++i) {
-      const int e = tid + 256 * i;
-      const int d = e / (KT / 4), g = e % (KT / 4);  // feature d, keys k0 + 4g .. 4g+3
+      const int e = min(tid + 256 * i, TASKS - 1);
+      const int d = min(e / (KT / 4), hd - 1), g = e % (KT / 4);  // feature d, keys k0+4g..+3
+      const float *src = V + (size_t)L * d;
       const int key = k0 + 4 * g;
-      v[i] = {0.0f, 0.0f, 0.0f, 0.0f};
-      if (e < TASKS && d < hd) {
-        const float *src = V + key + (size_t)L * d;
-        if (VEC && key + 3 < L) {
-          v[i] = *reinterpret_cast<const f32x4 *>(src);
-        } else {
+      if (VEC) {
+        v[i] = *reinterpret_cast<const f32x4 *>(src + min(key, L - 4));
+      } else {
 #pragma unroll
-          for (int t = 0; t < 4; ++t)
-            if (key + t < L) v[i][t] = src[t];
-        }
+        for (int t = 0; t < 4; ++t) v[i][t] = src[min(key + t, L - 1)];
       }
     }
   }
 
-  __device__ __forceinline__ int commit(float *Ks, float *Vs, int tid) {
+  __device__ __forceinline__ int commit(float *Ks, float *Vs, int tid, int k0, int L, int hd) {
     constexpr int KS = HDP + 4;
     constexpr int VS = KT + 4;
+    const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
     int nonfinite = 0;
 #pragma unroll
     for (int i = 0; i < KN; ++i) {
       const int e = tid + 256 * i;
       const int kk = (4 * e) / HDP, d = (4 * e) % HDP;
-      if (e < TASKS) *reinterpret_cast<f32x4 *>(&Ks[kk * KS + d]) = k[i];
+      if (e < TASKS) *reinterpret_cast<f32x4 *>(&Ks[kk * KS + d]) = k0 + kk < L ? k[i] : z;
     }
 #pragma unroll
     for (int i = 0; i < VN; ++i) {
@@ -230,11 +244,21 @@ struct JeffStage {
       const int d = e / (KT / 4), g = e % (KT / 4);
       if (e >= TASKS) continue;
       f32x4 x = v[i];
+      const int key = k0 + 4 * g;
+      if (VEC && key + 4 > L) {  // the clamped load was shifted back: realign
+        const int sh = key - (L - 4);
+        f32x4 y = z;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          if (t + sh < 4) y[t] = x[t + sh];
+        x = y;
+      }
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
+        const bool live = d < hd && key + t < L;
         const bool fin = __builtin_isfinite(x[t]);
-        nonfinite |= !fin;
-        x[t] = fin ? x[t] : 0.0f;
+        nonfinite |= live && !fin;
+        x[t] = (live && fin) ? x[t] : 0.0f;
       }
       *reinterpret_cast<f32x4 *>(&Vs[d * VS + 4 * g]) = x;
     }
@@ -309,7 +333,7 @@ __global__ __launch_bounds__(256, 2) void jeff_attention_f32_kernel(const JeffAr
     float *qs = qw + col * QP;
     float ss = 0.0f;
     const int qc = q_live ? q : 0;
-#pragma unroll 16
+#pragma unroll
     for (int s = 0; s < QS; ++s) {  // clamped, unconditional loads batch together
       const int d = grp * QS + s;
       const float x = Q[qc + (size_t)L * (d < hd ? d : hd - 1)];
@@ -320,25 +344,38 @@ __global__ __launch_bounds__(256, 2) void jeff_attention_f32_kernel(const JeffAr
     ss += __shfl_xor(ss, 16);
     ss += __shfl_xor(ss, 32);
     const float scale = rms_scale(ss, hd, a.eps);
-#pragma unroll 8
+#pragma unroll 16
     for (int s = 0; s < QS; ++s) {
       const int d = grp * QS + s;
-      if (d < hd) qs[d] = rms_apply(qs[d], scale, a.q_norm[d]);
+      const float wq = a.q_norm[min(d, hd - 1)];
+      const float y = rms_apply(qs[d], scale, wq);
+      qs[d] = d < hd ? y : 0.0f;
     }
     if (rope) {
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       const int q0 = qa + (wave / hg) * kJeffWaveQueries;
-      for (int e = lane; e < kJeffWaveQueries * rh; e += 64) {
-        const int qi = e / rh, i = e - qi * rh;
-        const int qq = q0 + qi;
-        if (qq < L && qq >= start) {
-          const int pos = qq - start;
-          const float c = a.cos_t[(size_t)pos * rh + i], sn = a.sin_t[(size_t)pos * rh + i];
-          const float x = qw[qi * QP + i], y = qw[qi * QP + i + rh];
-          qw[qi * QP + i] = rope_lo(x, y, c, sn);
-          qw[qi * QP + i + rh] = rope_hi(x, y, c, sn);
+      for (int e0 = 0; e0 < kJeffWaveQueries * rh; e0 += 64 * 8) {
+        float c[8], sn[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {  // clamped table loads, all in flight
+          const int e = min(e0 + lane + 64 * u, kJeffWaveQueries * rh - 1);
+          const int qi = e / rh, i = e - qi * rh;
+          const int pos = min(max(q0 + qi - start, 0), L - 1);
+          c[u] = a.cos_t[(size_t)pos * rh + i];
+          sn[u] = a.sin_t[(size_t)pos * rh + i];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int e = e0 + lane + 64 * u;
+          const int qi = e / rh, i = e - qi * rh;
+          const int qq = q0 + qi;
+          if (e < kJeffWaveQueries * rh && qq < L && qq >= start) {
+            const float x = qw[qi * QP + i], y = qw[qi * QP + i + rh];
+            qw[qi * QP + i] = rope_lo(x, y, c[u], sn[u]);
+            qw[qi * QP + i + rh] = rope_hi(x, y, c[u], sn[u]);
+          }
         }
       }
     }
@@ -351,10 +388,14 @@ __global__ __launch_bounds__(256, 2) void jeff_attention_f32_kernel(const JeffAr
   __syncthreads();  // the Q scratch becomes the K/V buffers
 
   // Keep word for a 16-key tile: active key, key >= start, causal key <= query.
-  auto keep_word = [&](int kt) -> uint32_t {
+  // The mask value is fetched one tile ahead (mask_of) and turned into the
+  // word (keep_word) only when that tile comes up, so no wait on it stalls
+  // the tile prefetch issued next to it.
+  auto mask_of = [&](int kt) -> float { return maskr[min(kt * KT + (lane & 15), L - 1)]; };
+  auto keep_word = [&](int kt, float mv) -> uint32_t {
     const int k0 = kt * KT;
     const int kc = k0 + (lane & 15);
-    const bool act = kc < L && kc >= start && maskr[kc] != 0.0f;
+    const bool act = kc < L && kc >= start && mv != 0.0f;
     const uint32_t abits = (uint32_t)__ballot(act) & 0xffffu;
     return q_live ? (abits & range_bits(0, q - k0)) : 0u;
   };
@@ -369,10 +410,12 @@ __global__ __launch_bounds__(256, 2) void jeff_attention_f32_kernel(const JeffAr
   JeffStage<HDP, VEC> st;
   int nonfinite = 0;
   uint32_t w = 0u;
+  float m_next = 0.0f;
   if (kt_begin < kt_end) {
+    const float m0 = mask_of(kt_begin);
     st.fetch(KP + (size_t)kt_begin * KT * HDP, V, L, hd, kt_begin * KT, tid);
-    nonfinite = st.commit(Ks[0], Vs[0], tid);
-    w = keep_word(kt_begin);
+    nonfinite = st.commit(Ks[0], Vs[0], tid, kt_begin * KT, L, hd);
+    w = keep_word(kt_begin, m0);
   }
   int nf = __syncthreads_or(nonfinite);
   int any_nf = 0;  // workgroup-uniform: some staged V value was NaN or inf
@@ -380,10 +423,9 @@ __global__ __launch_bounds__(256, 2) void jeff_attention_f32_kernel(const JeffAr
   for (int kt = kt_begin; kt < kt_end; ++kt) {
     const int cur = (kt - kt_begin) & 1;
     const bool more = kt + 1 < kt_end;
-    uint32_t w_next = 0u;
     if (more) {
+      m_next = mask_of(kt + 1);
       st.fetch(KP + (size_t)(kt + 1) * KT * HDP, V, L, hd, (kt + 1) * KT, tid);
-      w_next = keep_word(kt + 1);
     }
     const float *Kc = Ks[cur];
     const float *Vc = Vs[cur];
@@ -449,9 +491,9 @@ __global__ __launch_bounds__(256, 2) void jeff_attention_f32_kernel(const JeffAr
     }
     any_nf |= nf;
     nonfinite = 0;
-    if (more) nonfinite = st.commit(Ks[cur ^ 1], Vs[cur ^ 1], tid);
+    if (more) nonfinite = st.commit(Ks[cur ^ 1], Vs[cur ^ 1], tid, (kt + 1) * KT, L, hd);
     nf = __syncthreads_or(nonfinite);
-    w = w_next;
+    if (more) w = keep_word(kt + 1, m_next);
   }
 
   // -------- non-finite values of kept keys (rare): o = sum p*v over p != 0
@@ -487,18 +529,25 @@ __global__ __launch_bounds__(256, 2) void jeff_attention_f32_kernel(const JeffAr
   const float inv = lt > 0.0f ? fast_rcp(lt) : 0.0f;
   if (qin) {
     const bool dropped = a.trim && q < start;
+    // Every gate load is issued before any is used (clamped, unconditional),
+    // so the epilogue waits on memory once rather than once per output.
+    f32x4 gv[NB];
 #pragma unroll
     for (int j = 0; j < NB; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int d = j * 16 + 4 * grp + r;
-        if (d < hd) {
-          const size_t at = q + (size_t)L * d;
-          float o = O[j][r] * inv;
-          const uint32_t f = (special[j] >> (8 * r)) & 7u;
-          if (f) o = ((f & 1u) || f == 6u) ? __builtin_nanf("") : (f == 2u ? INFINITY : -INFINITY);
-          OUT[at] = dropped ? 0.0f : o * fast_sigmoid(Gt[at]);
-        }
+        gv[j][r] = Gt[q + (size_t)L * (d < hd ? d : hd - 1)];
+      }
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int d = j * 16 + 4 * grp + r;
+        float o = O[j][r] * inv;
+        const uint32_t f = (special[j] >> (8 * r)) & 7u;
+        if (f) o = ((f & 1u) || f == 6u) ? __builtin_nanf("") : (f == 2u ? INFINITY : -INFINITY);
+        if (d < hd) OUT[q + (size_t)L * d] = dropped ? 0.0f : o * fast_sigmoid(gv[j][r]);
       }
   }
 }

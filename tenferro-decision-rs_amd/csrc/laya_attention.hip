@@ -36,8 +36,10 @@ __global__ __launch_bounds__(256) void laya_keep_bits_kernel(const uint8_t *__re
   const int n = min(kKeyTile, L - k0);
   uint8_t v[kKeyTile];
 #pragma unroll
-  for (int kk = 0; kk < kKeyTile; ++kk)  // all loads in flight at once
-    v[kk] = kk < n ? base[(size_t)L * (k0 + kk)] : 0;
+  for (int kk = 0; kk < kKeyTile; ++kk)  // unconditional (clamped) loads: all in flight at once
+    v[kk] = base[(size_t)L * (k0 + min(kk, n - 1))];
+#pragma unroll
+  for (int kk = 0; kk < kKeyTile; ++kk) v[kk] = kk < n ? v[kk] : 0;
   uint32_t w = 0;
 #pragma unroll
   for (int kk = 0; kk < kKeyTile; ++kk) w |= (uint32_t)(v[kk] != 0) << kk;
@@ -102,32 +104,30 @@ struct LayaStage {
   __device__ __forceinline__ void fetch(const LayaArgs &a, const float *xb, size_t tok, int k0,
                                         int tid) {
     if constexpr (VEC) {
+      // Every load is unconditional with a clamped (in-bounds) index, so all
+      // of them are in flight together; out-of-range keys are zeroed at
+      // commit time.
       const int hh = a.half;
 #pragma unroll
       for (int i = 0; i < KN; ++i) {
-        const int task = tid + 256 * i;
-        const int key = k0 + task / (HDP / 8), cp = task % (HDP / 8);
-        f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
-        ka[i] = kb[i] = z;
-        c[i] = {1.0f, 1.0f, 1.0f, 1.0f};
-        s[i] = z;
-        if (task < KTASKS && key < a.L) {
-          const float *row = xb + (size_t)key * tok + a.d;
-          ka[i] = *reinterpret_cast<const f32x4 *>(row + 4 * cp);
-          kb[i] = *reinterpret_cast<const f32x4 *>(row + 4 * cp + hh);
-          if (a.cos_t) {
-            c[i] = *reinterpret_cast<const f32x4 *>(a.cos_t + (size_t)key * hh + 4 * cp);
-            s[i] = *reinterpret_cast<const f32x4 *>(a.sin_t + (size_t)key * hh + 4 * cp);
-          }
+        const int task = min(tid + 256 * i, KTASKS - 1);
+        const int key = min(k0 + task / (HDP / 8), a.L - 1), cp = task % (HDP / 8);
+        const float *row = xb + (size_t)key * tok + a.d;
+        ka[i] = *reinterpret_cast<const f32x4 *>(row + 4 * cp);
+        kb[i] = *reinterpret_cast<const f32x4 *>(row + 4 * cp + hh);
+        if (a.cos_t) {
+          c[i] = *reinterpret_cast<const f32x4 *>(a.cos_t + (size_t)key * hh + 4 * cp);
+          s[i] = *reinterpret_cast<const f32x4 *>(a.sin_t + (size_t)key * hh + 4 * cp);
+        } else {
+          c[i] = f32x4{1.0f, 1.0f, 1.0f, 1.0f};
+          s[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
       }
 #pragma unroll
       for (int i = 0; i < VN; ++i) {
-        const int task = tid + 256 * i;
-        const int key = k0 + task / (HDP / 4), ch = task % (HDP / 4);
-        v[i] = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (task < VTASKS && key < a.L)
-          v[i] = *reinterpret_cast<const f32x4 *>(xb + (size_t)key * tok + 2 * a.d + 4 * ch);
+        const int task = min(tid + 256 * i, VTASKS - 1);
+        const int key = min(k0 + task / (HDP / 4), a.L - 1), ch = task % (HDP / 4);
+        v[i] = *reinterpret_cast<const f32x4 *>(xb + (size_t)key * tok + 2 * a.d + 4 * ch);
       }
     }
   }
@@ -140,16 +140,20 @@ struct LayaStage {
     if constexpr (VEC) {
       const int hh = a.half;
       const bool rope = a.cos_t != nullptr;
+      const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int i = 0; i < KN; ++i) {
         const int task = tid + 256 * i;
         if (task < KTASKS) {
           const int kk = task / (HDP / 8), cp = task % (HDP / 8);
+          const bool live = k0 + kk < a.L;
           f32x4 lo = ka[i], hi = kb[i];
           if (rope) {
             lo = rot_lo(ka[i], kb[i], c[i], s[i]);
             hi = rot_hi(ka[i], kb[i], c[i], s[i]);
           }
+          lo = live ? lo : z;
+          hi = live ? hi : z;
           *reinterpret_cast<f32x4 *>(&Ks[kk * KS + 4 * cp]) = lo;
           *reinterpret_cast<f32x4 *>(&Ks[kk * KS + hh + 4 * cp]) = hi;
         }
@@ -159,8 +163,9 @@ struct LayaStage {
         const int task = tid + 256 * i;
         if (task < VTASKS) {
           const int kk = task / (HDP / 4), ch = task % (HDP / 4);
-          nonfinite |= !all_finite(v[i]);
-          *reinterpret_cast<f32x4 *>(&Vs[kk * VS + 4 * ch]) = v[i];
+          const f32x4 x = k0 + kk < a.L ? v[i] : z;
+          nonfinite |= !all_finite(x);
+          *reinterpret_cast<f32x4 *>(&Vs[kk * VS + 4 * ch]) = x;
         }
       }
     } else {
@@ -225,7 +230,9 @@ __global__ __launch_bounds__(256) void laya_attention_kernel(const LayaArgs a) {
         const int i = i0 + tid + 256 * u;
         const int qq = qg0 + (i & (kLayaGroupQueries - 1));
         const int kt = i / kLayaGroupQueries;
-        word[u] = (i < kLayaGroupQueries * nkt && qq < L) ? a.bits[((size_t)b * nkt + kt) * L + qq] : 0u;
+        const bool ok = i < kLayaGroupQueries * nkt && qq < L;
+        const uint32_t x = a.bits[((size_t)b * nkt + min(kt, nkt - 1)) * L + min(qq, L - 1)];
+        word[u] = ok ? x : 0u;
       }
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
@@ -250,7 +257,8 @@ __global__ __launch_bounds__(256) void laya_attention_kernel(const LayaArgs a) {
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         const int k = k0 + tid + 256 * u;
-        v[u] = k < L ? vb[k] : 0;
+        const uint8_t x = vb[min(k, L - 1)];
+        v[u] = k < L ? x : 0;
       }
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
@@ -332,17 +340,27 @@ __global__ __launch_bounds__(256) void laya_attention_kernel(const LayaArgs a) {
     }
   }
   bool q_valid = false;
-  if (MODE == kMaskStruct) q_valid = qin && a.valid[(size_t)b * L + q] != 0;
+  if (MODE == kMaskStruct) {
+    const uint8_t x = a.valid[(size_t)b * L + min(q, L - 1)];
+    q_valid = qin && x != 0;
+  }
 
-  // This lane's keep word for key tile kt (bit j: key 32*kt + j).
-  auto keep_word = [&](int kt) -> uint32_t {
+  // This lane's keep word for key tile kt (bit j: key 32*kt + j). The raw
+  // word or validity byte is fetched one tile ahead (mask_of) and turned into
+  // the word (keep_word) only when the tile comes up, so waiting on it never
+  // stalls the tile prefetch issued beside it.
+  auto mask_of = [&](int kt) -> uint32_t {
+    if (MODE == kMaskBits) return a.bits[((size_t)b * nkt + kt) * L + min(q, L - 1)];
+    return a.valid[(size_t)b * L + min(kt * kKeyTile + col, L - 1)];
+  };
+  auto keep_word = [&](int kt, uint32_t x) -> uint32_t {
     uint32_t w = 0u;
     if (MODE == kMaskBits) {
-      if (qin) w = a.bits[((size_t)b * nkt + kt) * L + q];
+      w = qin ? x : 0u;
     } else {
       const int k0 = kt * kKeyTile;
       const int key = k0 + col;
-      const bool kv = key < L && a.valid[(size_t)b * L + key] != 0;
+      const bool kv = key < L && x != 0;
       const uint32_t vbits = (uint32_t)__ballot(kv);  // lanes 0..31 = keys of the tile
       if (qin) {
         w = vbits;
@@ -365,20 +383,21 @@ __global__ __launch_bounds__(256) void laya_attention_kernel(const LayaArgs a) {
   LayaStage<HDP, VEC> st;
   int nonfinite = 0;
   uint32_t w = 0u;
+  uint32_t m_next = 0u;
   if (kt_begin < kt_end) {
+    const uint32_t m0 = mask_of(kt_begin);
     st.fetch(a, xb, tok, kt_begin * kKeyTile, tid);
     nonfinite = st.commit(a, xb, tok, kt_begin * kKeyTile, tid, Ks[0], Vs[0]);
-    w = keep_word(kt_begin);
+    w = keep_word(kt_begin, m0);
   }
   int nf = __syncthreads_or(nonfinite);
 
   for (int kt = kt_begin; kt < kt_end; ++kt) {
     const int cur = (kt - kt_begin) & 1;
     const bool more = kt + 1 < kt_end;
-    uint32_t w_next = 0u;
     if (more) {
+      m_next = mask_of(kt + 1);
       st.fetch(a, xb, tok, (kt + 1) * kKeyTile, tid);
-      w_next = keep_word(kt + 1);
     }
     const float *Kc = Ks[cur];
     const float *Vc = Vs[cur];
@@ -424,7 +443,7 @@ __global__ __launch_bounds__(256) void laya_attention_kernel(const LayaArgs a) {
     nonfinite = 0;
     if (more) nonfinite = st.commit(a, xb, tok, (kt + 1) * kKeyTile, tid, Ks[cur ^ 1], Vs[cur ^ 1]);
     nf = __syncthreads_or(nonfinite);
-    w = w_next;
+    if (more) w = keep_word(kt + 1, m_next);
   }
 
   // -------- normalize and store: out[feat + d + hidden*(q + L*b)]
