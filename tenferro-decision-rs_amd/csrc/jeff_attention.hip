@@ -552,6 +552,348 @@ __global__ __launch_bounds__(256, 2) void jeff_attention_f32_kernel(const JeffAr
   }
 }
 
+// ---------------------------------------------------------- bf16 attention
+
+// Tile data for one 32-key bf16 tile: finished K rows from the prep workspace
+// and the V columns, all as 16-byte loads with clamped indices. LDS holds K
+// as [key][d] and V as [d][key] (bf16).
+template <int HDP, bool VEC>
+struct JeffStageBf16 {
+  static constexpr int KT = 32;
+  static constexpr int KTASKS = KT * HDP / 8;  // 16-byte chunks of K
+  static constexpr int VTASKS = HDP * KT / 8;  // 16-byte chunks of V
+  static constexpr int KN = (KTASKS + 255) / 256;
+  static constexpr int VN = (VTASKS + 255) / 256;
+  u16x8 k[KN], v[VN];
+
+  __device__ __forceinline__ void fetch(const uint16_t *kp_tile, const uint16_t *V, int L, int hd,
+                                        int k0, int tid) {
+#pragma unroll
+    for (int i = 0; i < KN; ++i) {
+      const int e = min(tid + 256 * i, KTASKS - 1);
+      const int kk = min(e / (HDP / 8), L - 1 - k0);
+      k[i] = reinterpret_cast<const u16x8 *>(kp_tile)[kk * (HDP / 8) + e % (HDP / 8)];
+    }
+#pragma unroll
+    for (int i = 0; i < VN; ++i) {
+      const int e = min(tid + 256 * i, VTASKS - 1);
+      const int d = min(e / (KT / 8), hd - 1), g = e % (KT / 8);
+      const uint16_t *src = V + (size_t)L * d;
+      const int key = k0 + 8 * g;
+      if (VEC) {
+        v[i] = *reinterpret_cast<const u16x8 *>(src + min(key, L - 8));
+      } else {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) v[i][t] = src[min(key + t, L - 1)];
+      }
+    }
+  }
+
+  __device__ __forceinline__ int commit(uint16_t *Ks, uint16_t *Vs, int tid, int k0, int L, int hd) {
+    constexpr int KSB = HDP + 8, VSB = KT + 8;
+    const u16x8 z = {0, 0, 0, 0, 0, 0, 0, 0};
+    int nonfinite = 0;
+#pragma unroll
+    for (int i = 0; i < KN; ++i) {
+      const int e = tid + 256 * i;
+      const int kk = e / (HDP / 8), c = e % (HDP / 8);
+      if (e < KTASKS) *reinterpret_cast<u16x8 *>(&Ks[kk * KSB + 8 * c]) = k0 + kk < L ? k[i] : z;
+    }
+#pragma unroll
+    for (int i = 0; i < VN; ++i) {
+      const int e = tid + 256 * i;
+      const int d = e / (KT / 8), g = e % (KT / 8);
+      if (e >= VTASKS) continue;
+      u16x8 x = v[i];
+      const int key = k0 + 8 * g;
+      if (VEC && key + 8 > L) {  // the clamped load was shifted back: realign
+        const int sh = key - (L - 8);
+        u16x8 y = z;
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+          if (t + sh < 8) y[t] = x[t + sh];
+        x = y;
+      }
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const bool live = d < hd && key + t < L;
+        const bool fin = bf16_finite(x[t]);
+        nonfinite |= live && !fin;
+        x[t] = (live && fin) ? x[t] : (unsigned short)0;
+      }
+      *reinterpret_cast<u16x8 *>(&Vs[d * VSB + 8 * g]) = x;
+    }
+    return nonfinite;
+  }
+};
+
+// Same arithmetic as jeff_attention_f32_kernel with q, k, v and gate in bf16:
+// normalized/rotated q and k and the probabilities are rounded to bf16 for
+// v_mfma_f32_16x16x32_bf16; softmax, accumulation and output stay f32.
+// A 32-key tile is two 16-key S^T blocks (lane group g holds keys 4g + r and
+// 16 + 4g + r of its query), which together are exactly the B operand of one
+// P.V MFMA per 16-row block of O^T.
+template <int HDP, bool VEC>
+__global__ __launch_bounds__(256, 2) void jeff_attention_bf16_kernel(const JeffArgs a,
+                                                                     const uint16_t *__restrict__ kp) {
+  constexpr int KT = 32;
+  constexpr int QS8 = HDP / 32;  // bf16x8 B operands of Q per lane
+  constexpr int NB = HDP / 16;   // 16-row blocks of O^T
+  constexpr int KSB = HDP + 8, VSB = KT + 8;
+  constexpr int KBUF = KT * KSB, VBUF = HDP * VSB;  // uint16 elements
+  constexpr int QP = HDP + 1;
+  constexpr int TILE_BYTES = 2 * (KBUF + VBUF) * 2;
+  constexpr int QSCR_BYTES = kWavesPerGroup * kJeffWaveQueries * QP * 4;
+  constexpr int SMEM = TILE_BYTES > QSCR_BYTES ? TILE_BYTES : QSCR_BYTES;
+  __shared__ __attribute__((aligned(16))) unsigned char smem_raw[SMEM];
+  uint16_t *const lds16 = reinterpret_cast<uint16_t *>(smem_raw);
+  float *const qscr = reinterpret_cast<float *>(smem_raw);
+  __shared__ int s_span[2];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int col = lane & 15, grp = lane >> 4;
+  const int hg = a.heads_per_group, qsubs = kWavesPerGroup / hg;
+  const int row = blockIdx.z;
+  const int head = blockIdx.y * hg + wave % hg;
+  const int kvh = min(head / a.groups, a.kv_heads - 1);
+  const int L = a.L, hd = a.hd, rh = a.rot_half;
+  const int QT = kJeffWaveQueries * qsubs;
+  const int qa = blockIdx.x * QT;
+  const int q = qa + (wave / hg) * kJeffWaveQueries + col;
+  const bool qin = q < L;
+  const float *maskr = a.mask + (size_t)row * L;
+  const uint16_t *Q = static_cast<const uint16_t *>(a.q) + row * a.q_row + (size_t)head * hd * L;
+  const uint16_t *Gt = static_cast<const uint16_t *>(a.gate) + row * a.q_row + (size_t)head * hd * L;
+  const uint16_t *V = static_cast<const uint16_t *>(a.v) + row * a.kv_row + (size_t)kvh * hd * L;
+  const uint16_t *KP = kp + ((size_t)row * a.kv_heads + kvh) * L * HDP;
+  float *OUT = a.out + row * a.q_row + (size_t)head * hd * L;
+  const bool rope = a.cos_t != nullptr && rh > 0;
+
+  if (tid == 0) {
+    s_span[0] = 0x7fffffff;
+    s_span[1] = -1;
+  }
+  __syncthreads();
+  scan_active(maskr, L, tid, lane, s_span);
+  __syncthreads();
+  const int first = s_span[0], last = s_span[1];
+  const int start = (a.trim && last >= 0) ? first : 0;
+  int kt_begin = 0, kt_end = 0;
+  {
+    const int kl = min(last, min(qa + QT, L) - 1);
+    if (last >= 0 && first <= kl) {
+      kt_begin = first / KT;
+      kt_end = kl / KT + 1;
+    }
+  }
+
+  // -------- Q: RMSNorm + partial RoPE in f32 (wave-local LDS phases), then
+  // rounded to bf16: lane (col, grp) holds Q[q][32*s + 8*grp + e] in qb[s].
+  bf16x8 qb[QS8];
+  const bool q_live = qin && q >= start;
+  {
+    float *qw = qscr + wave * (kJeffWaveQueries * QP);
+    float *qs = qw + col * QP;
+    constexpr int QQ = HDP / 4;
+    float ss = 0.0f;
+    const int qc = q_live ? q : 0;
+#pragma unroll
+    for (int s = 0; s < QQ; ++s) {
+      const int d = grp * QQ + s;
+      const float x = bf16_to_f32(Q[qc + (size_t)L * (d < hd ? d : hd - 1)]);
+      const float y = (q_live && d < hd) ? x : 0.0f;
+      qs[d] = y;
+      ss += y * y;
+    }
+    ss += __shfl_xor(ss, 16);
+    ss += __shfl_xor(ss, 32);
+    const float scale = rms_scale(ss, hd, a.eps);
+#pragma unroll 16
+    for (int s = 0; s < QQ; ++s) {
+      const int d = grp * QQ + s;
+      const float wq = a.q_norm[min(d, hd - 1)];
+      const float y = rms_apply(qs[d], scale, wq);
+      qs[d] = d < hd ? y : 0.0f;
+    }
+    if (rope) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const int q0 = qa + (wave / hg) * kJeffWaveQueries;
+      for (int e0 = 0; e0 < kJeffWaveQueries * rh; e0 += 64 * 8) {
+        float c[8], sn[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int e = min(e0 + lane + 64 * u, kJeffWaveQueries * rh - 1);
+          const int qi = e / rh, i = e - qi * rh;
+          const int pos = min(max(q0 + qi - start, 0), L - 1);
+          c[u] = a.cos_t[(size_t)pos * rh + i];
+          sn[u] = a.sin_t[(size_t)pos * rh + i];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int e = e0 + lane + 64 * u;
+          const int qi = e / rh, i = e - qi * rh;
+          const int qq = q0 + qi;
+          if (e < kJeffWaveQueries * rh && qq < L && qq >= start) {
+            const float x = qw[qi * QP + i], y = qw[qi * QP + i + rh];
+            qw[qi * QP + i] = rope_lo(x, y, c[u], sn[u]);
+            qw[qi * QP + i + rh] = rope_hi(x, y, c[u], sn[u]);
+          }
+        }
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int s = 0; s < QS8; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qb[s][e] = (__bf16)qs[32 * s + 8 * grp + e];
+  }
+  __syncthreads();  // the Q scratch becomes the K/V buffers
+
+  auto mask_of = [&](int kt) -> float { return maskr[min(kt * KT + (lane & 31), L - 1)]; };
+  auto keep_word = [&](int kt, float mv) -> uint32_t {
+    const int k0 = kt * KT;
+    const int kc = k0 + (lane & 31);
+    const bool act = kc < L && kc >= start && mv != 0.0f;
+    const uint32_t abits = (uint32_t)__ballot(act);  // lanes 0..31 = keys of the tile
+    return q_live ? (abits & range_bits(0, q - k0)) : 0u;
+  };
+
+  f32x4 O[NB];
+#pragma unroll
+  for (int j = 0; j < NB; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) O[j][r] = 0.0f;
+  float m = -INFINITY, l = 0.0f;
+
+  JeffStageBf16<HDP, VEC> st;
+  int nonfinite = 0;
+  uint32_t w = 0u;
+  float m_next = 0.0f;
+  if (kt_begin < kt_end) {
+    const float m0 = mask_of(kt_begin);
+    st.fetch(KP + (size_t)kt_begin * KT * HDP, V, L, hd, kt_begin * KT, tid);
+    nonfinite = st.commit(lds16, lds16 + 2 * KBUF, tid, kt_begin * KT, L, hd);
+    w = keep_word(kt_begin, m0);
+  }
+  int nf = __syncthreads_or(nonfinite);
+  int any_nf = 0;
+
+  for (int kt = kt_begin; kt < kt_end; ++kt) {
+    const int cur = (kt - kt_begin) & 1;
+    const bool more = kt + 1 < kt_end;
+    if (more) {
+      m_next = mask_of(kt + 1);
+      st.fetch(KP + (size_t)(kt + 1) * KT * HDP, V, L, hd, (kt + 1) * KT, tid);
+    }
+    const uint16_t *Kc = lds16 + cur * KBUF;
+    const uint16_t *Vc = lds16 + 2 * KBUF + cur * VBUF;
+
+    if (__ballot(w != 0u) != 0) {
+      f32x4 s0, s1;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        s0[r] = 0.0f;
+        s1[r] = 0.0f;
+      }
+      const uint16_t *k0row = Kc + col * KSB + 8 * grp;
+      const uint16_t *k1row = Kc + (16 + col) * KSB + 8 * grp;
+#pragma unroll
+      for (int st8 = 0; st8 < QS8; ++st8) {
+        const bf16x8 ka = *reinterpret_cast<const bf16x8 *>(k0row + 32 * st8);
+        const bf16x8 kb = *reinterpret_cast<const bf16x8 *>(k1row + 32 * st8);
+        s0 = mfma_16x16x32_bf16(ka, qb[st8], s0);
+        s1 = mfma_16x16x32_bf16(kb, qb[st8], s1);
+      }
+      const float alpha = softmax_tile16(s0, s1, w, grp, a.c1, m, l);
+      if (alpha != 1.0f) {
+#pragma unroll
+        for (int j = 0; j < NB; ++j) O[j] *= alpha;
+      }
+      bf16x8 pb;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        pb[r] = (__bf16)s0[r];
+        pb[4 + r] = (__bf16)s1[r];
+      }
+      // A operand of block j: V[keys 4g+0..3 and 16+4g+0..3][d = 16*j + col].
+      const uint16_t *v0 = Vc + col * VSB + 4 * grp;
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        const u16x4 lo = *reinterpret_cast<const u16x4 *>(v0 + j * 16 * VSB);
+        const u16x4 hi = *reinterpret_cast<const u16x4 *>(v0 + j * 16 * VSB + 16);
+        u16x8 vv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          vv[e] = lo[e];
+          vv[4 + e] = hi[e];
+        }
+        O[j] = mfma_16x16x32_bf16(__builtin_bit_cast(bf16x8, vv), pb, O[j]);
+        if ((j & 7) == 7) __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    any_nf |= nf;
+    nonfinite = 0;
+    if (more)
+      nonfinite = st.commit(lds16 + (cur ^ 1) * KBUF, lds16 + 2 * KBUF + (cur ^ 1) * VBUF, tid,
+                            (kt + 1) * KT, L, hd);
+    nf = __syncthreads_or(nonfinite);
+    if (more) w = keep_word(kt + 1, m_next);
+  }
+
+  // -------- non-finite values of kept keys (rare), as in the f32 kernel
+  uint32_t special[NB];
+#pragma unroll
+  for (int j = 0; j < NB; ++j) special[j] = 0u;
+  if (any_nf) {
+    const int k_lo = kt_begin * KT, k_hi = min(kt_end * KT, L);
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int d = j * 16 + 4 * grp + r;
+        uint32_t f = 0u;
+        if (q_live && d < hd) {
+#pragma nounroll
+          for (int k = k_lo; k < k_hi && k <= q; ++k) {
+            if (k < start || maskr[k] == 0.0f) continue;
+            const float v = bf16_to_f32(V[k + (size_t)L * d]);
+            if (!__builtin_isfinite(v)) f |= __builtin_isnan(v) ? 1u : (v > 0.0f ? 2u : 4u);
+          }
+        }
+        special[j] |= f << (8 * r);
+      }
+  }
+
+  float lt = l + __shfl_xor(l, 16);
+  lt += __shfl_xor(lt, 32);
+  const float inv = lt > 0.0f ? fast_rcp(lt) : 0.0f;
+  if (qin) {
+    const bool dropped = a.trim && q < start;
+    f32x4 gv[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int d = j * 16 + 4 * grp + r;
+        gv[j][r] = bf16_to_f32(Gt[q + (size_t)L * (d < hd ? d : hd - 1)]);
+      }
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int d = j * 16 + 4 * grp + r;
+        float o = O[j][r] * inv;
+        const uint32_t f = (special[j] >> (8 * r)) & 7u;
+        if (f) o = ((f & 1u) || f == 6u) ? __builtin_nanf("") : (f == 2u ? INFINITY : -INFINITY);
+        if (d < hd) OUT[q + (size_t)L * d] = dropped ? 0.0f : o * fast_sigmoid(gv[j][r]);
+      }
+  }
+}
+
 // ----------------------------------------------------------------- launchers
 
 template <int HDP>
@@ -588,8 +930,35 @@ size_t jeff_kp_bytes(const JeffArgs &a, int rows, int hd_pad, bool bf16) {
   return (size_t)rows * a.kv_heads * a.L * hd_pad * (bf16 ? 2 : 4);
 }
 
-hipError_t launch_jeff_attention_bf16(const JeffArgs &, int, int, void *, hipStream_t) {
-  return hipErrorNotSupported;
+template <int HDP>
+static hipError_t launch_jeff_bf16_hd(const JeffArgs &a, int rows, uint16_t *kp,
+                                      hipStream_t stream) {
+  dim3 pgrid((a.L + kKeyTile - 1) / kKeyTile, a.kv_heads, rows);
+  hipLaunchKernelGGL((jeff_k_prep_kernel<HDP, uint16_t>), pgrid, dim3(256), 0, stream, a, kp);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int qsubs = kWavesPerGroup / a.heads_per_group;
+  const int qt = kJeffWaveQueries * qsubs;
+  dim3 grid((a.L + qt - 1) / qt, a.heads / a.heads_per_group, rows);
+  // 16-byte V loads along tokens need L % 8 == 0 and an aligned base.
+  const bool vec = a.L % 8 == 0 && (reinterpret_cast<uintptr_t>(a.v) & 15) == 0;
+  if (vec)
+    hipLaunchKernelGGL((jeff_attention_bf16_kernel<HDP, true>), grid, dim3(256), 0, stream, a, kp);
+  else
+    hipLaunchKernelGGL((jeff_attention_bf16_kernel<HDP, false>), grid, dim3(256), 0, stream, a, kp);
+  return hipGetLastError();
+}
+
+hipError_t launch_jeff_attention_bf16(const JeffArgs &a, int rows, int hd_pad, void *kp,
+                                      hipStream_t stream) {
+  uint16_t *k = static_cast<uint16_t *>(kp);
+  switch (hd_pad) {
+    case 32: return launch_jeff_bf16_hd<32>(a, rows, k, stream);
+    case 64: return launch_jeff_bf16_hd<64>(a, rows, k, stream);
+    case 128: return launch_jeff_bf16_hd<128>(a, rows, k, stream);
+    case 256: return launch_jeff_bf16_hd<256>(a, rows, k, stream);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace tfd

@@ -8,6 +8,9 @@ namespace tfd {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned short u16x4 __attribute__((ext_vector_type(4)));
 
 // D(32x32) += A(32x2) * B(2x32) on the f32 matrix cores.
 // Lane l supplies A[l%32][l/32] and B[l/32][l%32]; D row for accumulator r is
@@ -21,6 +24,25 @@ __device__ __forceinline__ f32x16 mfma_32x32x2(float a, float b, f32x16 c) {
 __device__ __forceinline__ f32x4 mfma_16x16x4(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
+
+// D(16x16) += A(16x32) * B(32x16) in bf16 with f32 accumulation. Lane l
+// supplies A[l%16][8*(l/16) + e] and B[8*(l/16) + e][l%16], e = 0..7;
+// accumulator r holds D[4*(l/16) + r][l%16].
+__device__ __forceinline__ f32x4 mfma_16x16x32_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float bf16_to_f32(unsigned short h) {
+  return __uint_as_float((uint32_t)h << 16);
+}
+
+// Round to nearest even.
+__device__ __forceinline__ unsigned short f32_to_bf16(float x) {
+  const __bf16 h = (__bf16)x;
+  return *reinterpret_cast<const unsigned short *>(&h);
+}
+
+__device__ __forceinline__ bool bf16_finite(unsigned short h) { return ((h >> 7) & 0xff) != 0xff; }
 
 __device__ __forceinline__ int acc_row(int r, int half) {
   return 8 * (r >> 2) + 4 * half + (r & 3);

@@ -268,3 +268,84 @@ def test_jeff_c4_full_gqa_and_dropin(gpu_ctx):
                                      w.mask[r * L:(r + 1) * L], w.heads, w.head_dim, w.rotary_dim,
                                      w.theta, w.eps, q_shape=(L, W), ctx=gpu_ctx)
         assert_close(one, want[sl], F32_TOL)
+
+
+# ------------------------------------------------------------------ Jeff bf16
+
+def bf16_case(seed, rows, length, heads, kv_heads, hd, holes):
+    rng = Lcg(seed)
+    W, KW = heads * hd, kv_heads * hd
+    q, g = (rng.normal(rows * length * W).astype(np.float32) for _ in range(2))
+    k, v = (rng.normal(rows * length * KW).astype(np.float32) for _ in range(2))
+    qn = (rng.normal(hd) * 0.1).astype(np.float32)
+    kn = (rng.normal(hd) * 0.1).astype(np.float32)
+    mask = np.ones(rows * length, np.float32)
+    if holes and length > 8:
+        mask[: length // 3] = 0.0            # row 0 left-padded
+        mask[length + length // 2] = 0.0     # row 1 interior hole
+    bits = [te.to_bf16_bits(x) for x in (q, k, v, g)]
+    vals = [te.bf16_bits_to_f32(b) for b in bits]
+    return bits, vals, qn, kn, mask
+
+
+@pytest.mark.parametrize("length", [1, 17, 64, 100, 257])
+@pytest.mark.parametrize("hd,rot,heads,kv", [(16, 8, 2, 2), (64, 32, 4, 2), (256, 64, 8, 2)])
+def test_jeff_bf16_rows_match_oracle(gpu_ctx, length, hd, rot, heads, kv):
+    rows = 2
+    for trim in (False, True):
+        bits, vals, qn, kn, mask = bf16_case(length + hd, rows, length, heads, kv, hd, True)
+        want = oracle.jeff_rows(*vals, qn, kn, mask, rows, length, heads, kv, hd, rot, 1e7, 1e-6,
+                                trim_leading=trim)
+        got = te.jeff_full_attention_rows(*bits, qn, kn, mask, rows, length, heads, kv, hd, rot,
+                                          1e7, 1e-6, trim_leading=trim, bf16=True, ctx=gpu_ctx)
+        assert_close(got, want, BF16_TOL)
+
+
+def test_jeff_bf16_kept_nonfinite_values_propagate(gpu_ctx):
+    rows, length, heads, kv, hd = 1, 70, 4, 2, 64
+    bits, vals, qn, kn, mask = bf16_case(3, rows, length, heads, kv, hd, False)
+    Vb = bits[2].reshape(kv * hd, length)
+    Vb[7, 12] = 0x7F80   # +inf, kept from query 12 on
+    Vb[hd + 2, 40] = 0x7FC0  # NaN
+    mask[5] = 0.0
+    Vb[9, 5] = 0x7FC0    # masked NaN: must not leak
+    vals[2] = te.bf16_bits_to_f32(bits[2])
+    want = oracle.jeff_rows(*vals, qn, kn, mask, rows, length, heads, kv, hd, 16, 1e4, 1e-6)
+    got = np.asarray(te.jeff_full_attention_rows(*bits, qn, kn, mask, rows, length, heads, kv, hd,
+                                                 16, 1e4, 1e-6, bf16=True, ctx=gpu_ctx))
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.array_equal(np.isinf(got), np.isinf(want))
+    fin = np.isfinite(want)
+    assert np.abs(got[fin] - want[fin]).max() <= BF16_TOL
+
+
+def test_jeff_c5_reduced_matches_oracle(gpu_ctx):
+    """C5 shape (GQA 8/2 x 256, causal, all active) at L 1024 against the oracle."""
+    w = jeff_config(5, rows=2, length=1024)
+    bits = [te.to_bf16_bits(getattr(w, n)) for n in ("q", "k", "v", "gate")]
+    want = oracle.jeff_rows(w.q, w.k, w.v, w.gate, w.q_norm, w.k_norm, w.mask, w.rows, w.length,
+                            w.heads, w.kv_heads, w.head_dim, w.rotary_dim, w.theta, w.eps)
+    got = te.jeff_full_attention_rows(*bits, w.q_norm, w.k_norm, w.mask, w.rows, w.length,
+                                      w.heads, w.kv_heads, w.head_dim, w.rotary_dim, w.theta,
+                                      w.eps, bf16=True, ctx=gpu_ctx)
+    err = assert_close(got, want, BF16_TOL)
+    print(f"C5 (L 1024) bf16 max abs error vs oracle {err:.3e}")
+
+
+def test_jeff_c5_full_bf16_matches_f32_gpu(gpu_ctx):
+    """C5 at full size (2 rows x 8192): the bf16 kernel against the f32 kernel
+    (itself parity-tested against the oracle) on the same bf16-valued inputs."""
+    import torch
+
+    w = jeff_config(5)
+    dev = torch.device("cuda:0")
+    bits = [torch.from_numpy(te.to_bf16_bits(getattr(w, n)).view(np.int16)).to(dev)
+            for n in ("q", "k", "v", "gate")]
+    vals = [torch.from_numpy(getattr(w, n)).to(dev) for n in ("q", "k", "v", "gate")]
+    rest = [torch.from_numpy(getattr(w, n)).to(dev) for n in ("q_norm", "k_norm", "mask")]
+    torch.cuda.synchronize()
+    args = (w.rows, w.length, w.heads, w.kv_heads, w.head_dim, w.rotary_dim, w.theta, w.eps)
+    got = te.jeff_full_attention_rows(*bits, *rest, *args, bf16=True, ctx=gpu_ctx)
+    ref = te.jeff_full_attention_rows(*vals, *rest, *args, ctx=gpu_ctx)
+    err = assert_close(got.cpu().numpy(), ref.cpu().numpy(), BF16_TOL)
+    print(f"C5 full bf16 vs f32 max abs error {err:.3e}")
