@@ -58,8 +58,11 @@ def time_gpu(fn, steps, warmup, ctx):
 
 
 def laya_bytes(w):
-    """Minimal I/O: q, k, v of the valid tokens' rows once, out once, keep once."""
-    return 4 * (3 * w.hidden * w.length * w.batch) + 4 * w.hidden * w.length * w.batch
+    """Algorithmic bytes of one attention-kernel launch: the (3d, L, B) qkv
+    read once and the (d, L, B) output written once (f32), plus the packed
+    keep words (4 bytes per query per 32-key tile)."""
+    words = 4 * w.length * w.batch * ((w.length + 31) // 32)
+    return 4 * (3 * w.hidden * w.length * w.batch) + 4 * w.hidden * w.length * w.batch + words
 
 
 def cpu_laya(w, threads, reps=15, warmup=5):
@@ -148,7 +151,8 @@ def run(args):
         "roofline": {"bound": "mfma", "kernel": "laya_attention_kernel<64, keep bits>",
                      "achieved": round(achieved, 3), "peak": F32_MFMA_PEAK, "unit": "TFLOP/s",
                      "frac": round(achieved / F32_MFMA_PEAK, 4), "kernel_ms": round(kern_ms, 5),
-                     "traffic": None},
+                     "traffic": _traffic("laya_attention_kernel"),
+                     "algorithmic_bytes": laya_bytes(w)},
         "gpu": gpu_name,
     }
 
@@ -260,6 +264,15 @@ def run_only(args):
     torch.cuda.set_device(dev)
     stream = torch.cuda.Stream(device=dev)
     torch.cuda.set_stream(stream)
+    if args.only == "copy":
+        # Calibration for PMC byte counters: a plain device copy of known size.
+        n = 1 << 27  # 128 Mi floats = 512 MiB each way
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(args.warmup + args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        return {"only": "copy", "bytes_read_per_copy": 4 * n, "bytes_written_per_copy": 4 * n}
     ctx = te.Context(0, stream=stream.cuda_stream)
     cfg = int(args.only[1])
     if cfg in (2, 3):
@@ -288,6 +301,18 @@ def run_only(args):
             "kernel_tflops": round(flops / (kern * 1e-3) / 1e12, 3), "algorithmic_flops": flops}
 
 
+def _traffic(kernel):
+    """HBM bytes per launch of `kernel` on C2, from the committed rocprofv3
+    FETCH_SIZE + WRITE_SIZE measurement (profiles/traffic_c2.json), or None."""
+    path = os.path.join(ROOT, "profiles", "traffic_c2.json")
+    try:
+        with open(path) as f:
+            data = json.load(f)
+        return data["kernels"][kernel]["hbm_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def _cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -305,7 +330,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="only the C2 headline")
-    ap.add_argument("--only", choices=["c2", "c3", "c4", "c5"], default=None,
+    ap.add_argument("--only", choices=["c2", "c3", "c4", "c5", "copy"], default=None,
                     help="profiling aid: run one configuration's op (steps + warmup calls), "
                          "print its timing line and skip everything else")
     args = ap.parse_args()
