@@ -68,6 +68,28 @@ __device__ __forceinline__ float fast_sigmoid(float g) {
   return fast_rcp(1.0f + fast_exp2(-g * 1.4426950408889634f));
 }
 
+// max / sum of x over the lane pair (l, l ^ 32), identical in both lanes, with
+// one v_permlane32_swap (lanes 32..63 of the first operand trade places with
+// lanes 0..31 of the second) instead of an LDS permute.
+__device__ __forceinline__ float pair_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Online softmax with a lazily moved reference: exponents are taken against
+// a reference m (log2 units) that only moves when a tile's max exceeds it by
+// more than kRescaleSlack, so most tiles skip rescaling the accumulators.
+// Probabilities stay below 2^kRescaleSlack; O / l is unchanged.
+constexpr float kRescaleSlack = 8.0f;
+// Initial reference: finite, so exp2(fma(-inf, c1, -m)) is exp2(-inf) = 0.
+constexpr float kNoMax = -3.402823466e38f;
+
 __device__ __forceinline__ int wave_min(int v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o));
@@ -98,7 +120,7 @@ __device__ __forceinline__ float softmax_tile(f32x16 &s, uint32_t keep, int half
     s[r] = x;
     mx = fmaxf(mx, x);
   }
-  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  mx = pair_max(mx);
   const float mn = fmaxf(m, mx);
   const float alpha = (m == mn) ? 1.0f : fast_exp2(m - mn);
   float rs = 0.0f;

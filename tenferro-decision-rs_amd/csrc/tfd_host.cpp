@@ -50,6 +50,7 @@ struct tfd_ctx {
   bool adopted = false;  // stream given by the caller (may be the null stream)
   bool own_stream = false;
   bool ready = false;
+  int cus = 0;  // compute units of the device (launch shape heuristics)
   std::string err;
   DevBuf staging[8];  // uploads of host-pointer operands
   DevBuf bits;        // Laya packed keep words
@@ -108,6 +109,8 @@ int ensure_ready(tfd_ctx *c) {
       TFD_HIP(c, hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreate");
       c->own_stream = true;
     }
+    TFD_HIP(c, hipDeviceGetAttribute(&c->cus, hipDeviceAttributeMultiprocessorCount, c->device),
+            "hipDeviceGetAttribute");
     c->ready = true;
   }
   return TFD_OK;
@@ -317,15 +320,20 @@ int laya_run(tfd_ctx *c, const char *op, const float *qkv, const uint8_t *keep,
   int mode = tfd::kMaskStruct;
   if (keep) {
     mode = tfd::kMaskBits;
-    size_t words = 0;
-    if (!mul_ok((size_t)a.nkt * batch, length, &words))
+    // Workspace: the packed words, then the per-(tile, 64-query group) map.
+    size_t words = 0, groups = 0;
+    if (!mul_ok((size_t)a.nkt * batch, length, &words) ||
+        !mul_ok((size_t)a.nkt * batch, (length + 63) / 64, &groups) || words > SIZE_MAX / 8)
       return invalid(c, op, "shape", "attention dimensions overflow");
-    if ((rc = reserve(c, c->bits, sizeof(uint32_t) * words))) return rc;
-    a.bits = static_cast<const uint32_t *>(c->bits.ptr);
+    const size_t map_off = (sizeof(uint32_t) * words + 255) & ~(size_t)255;
+    if ((rc = reserve(c, c->bits, map_off + groups))) return rc;
+    uint8_t *base = static_cast<uint8_t *>(c->bits.ptr);
+    a.bits = reinterpret_cast<const uint32_t *>(base);
+    a.any = base + map_off;
     TFD_HIP(c,
             tfd::launch_laya_keep_bits(static_cast<const uint8_t *>(mask_d),
-                                       static_cast<uint32_t *>(c->bits.ptr), a.L, (int)batch,
-                                       a.nkt, c->stream),
+                                       reinterpret_cast<uint32_t *>(base), base + map_off, a.L,
+                                       (int)batch, a.nkt, c->stream),
             "laya_keep_bits launch");
   } else {
     a.valid = static_cast<const uint8_t *>(mask_d);

@@ -25,6 +25,8 @@ enum LayaMaskMode : int {
 struct LayaArgs {
   const float *qkv;      // (3d, L, B)
   const uint32_t *bits;  // kMaskBits: word (b*nkt + kt)*L + q, bit j = key 32*kt + j kept
+  const uint8_t *any;    // kMaskBits: byte (b*nkt + kt)*ceil(L/64) + q/64, tile kt kept by any
+                         // query of that 64-query group
   const uint8_t *valid;  // kMaskStruct: (L, B)
   const float *cos_t;    // (L, half) or nullptr (no RoPE)
   const float *sin_t;
@@ -50,8 +52,8 @@ struct JeffArgs {
 // Kernel launchers (return the launch status). hd_pad selects the
 // compile-time padded head dim (32, 64, 128 or 256).
 hipError_t launch_fill_zero(float *out, size_t n, hipStream_t stream);
-hipError_t launch_laya_keep_bits(const uint8_t *keep, uint32_t *bits, int L, int B, int nkt,
-                                 hipStream_t stream);
+hipError_t launch_laya_keep_bits(const uint8_t *keep, uint32_t *bits, uint8_t *any, int L, int B,
+                                 int nkt, hipStream_t stream);
 hipError_t launch_laya_attention(const LayaArgs &a, int heads, int batch, int hd_pad, int mode,
                                  hipStream_t stream);
 // Jeff launchers run a K prep kernel into `kp` (workspace of

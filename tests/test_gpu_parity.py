@@ -124,6 +124,76 @@ def test_laya_kept_nonfinite_value_propagates(gpu_ctx):
     assert np.abs(g[fin] - w[fin]).max() <= F32_TOL
 
 
+def assert_same_nonfinite(got, want, tol):
+    """NaN, +inf and -inf at the same positions; the finite rest within tol."""
+    g = np.asarray(got, np.float32).reshape(-1)
+    w = np.asarray(want, np.float32).reshape(-1)
+    for pick in (np.isnan, np.isposinf, np.isneginf):
+        bad = np.nonzero(pick(g) != pick(w))[0]
+        assert bad.size == 0, f"{pick.__name__} mismatch at {bad[:10]}"
+    fin = np.isfinite(w)
+    if fin.any():
+        err = float(np.abs(g[fin] - w[fin]).max())
+        assert err <= tol, f"max abs error {err} > {tol}"
+
+
+# (feature block, token, dim, value): q block 0, k block 1. Tokens sit in
+# different key tiles, so the walk meets them part-way through.
+_SCORE_CASES = {
+    "k_nan_kept": [(1, 70, 3, np.nan)],
+    "k_inf_kept": [(1, 100, 0, np.inf)],
+    "k_neg_inf_kept": [(1, 45, 5, -np.inf)],
+    "k_nan_masked": [(1, 33, 2, np.nan)],
+    "q_nan": [(0, 12, 1, np.nan), (0, 140, 7, np.inf)],
+    "mixed": [(1, 70, 3, np.nan), (1, 130, 1, np.inf), (0, 5, 0, -np.inf)],
+}
+
+
+@pytest.mark.parametrize("case", sorted(_SCORE_CASES))
+@pytest.mark.parametrize("scale", [1.0, 6.0])
+def test_laya_nonfinite_scores_mid_walk(gpu_ctx, case, scale):
+    """NaN / inf scores met part-way through a key walk (reference softmax:
+    a non-finite score weighs 0, a +inf one empties its row, lib.rs:1111-1136),
+    with q and k scaled so the running max keeps moving across tiles."""
+    length, hd, heads, batch = 160, 16, 2, 1
+    d = hd * heads
+    rng = Lcg(77)
+    qkv = rng.normal(3 * d * length).astype(np.float32).reshape(length, 3 * d)
+    qkv[:, :2 * d] *= scale
+    for blk, tok, dim, val in _SCORE_CASES[case]:
+        for h in range(heads):
+            qkv[tok, blk * d + h * hd + dim] = val
+    qkv = qkv.reshape(-1)
+    keep = np.ones((length, length), np.uint8)   # [key][query]: keep[q + L*key]
+    keep[33, :] = 0                               # a masked key every query drops
+    keep[:, 150:] = 0                             # queries that keep nothing
+    keep[100:, 140:150] = 0
+    keep = keep.reshape(-1)
+    want = oracle.laya_attention_block(qkv, keep, d, heads, length, batch, 160000.0)
+    got = laya_gpu(gpu_ctx, qkv, keep, d, heads, length, batch, 160000.0)
+    assert_same_nonfinite(got, want, F32_TOL)
+
+
+@pytest.mark.parametrize("hd", [32, 64, 128])
+def test_laya_running_max_growth(gpu_ctx, hd):
+    """Scores that climb tile after tile (keys scaled up along the row), so
+    the reference max moves on most tiles of the walk; values unscaled."""
+    length, heads, batch = 300, 2, 2
+    d = hd * heads
+    rng = Lcg(hd)
+    qkv = rng.normal(3 * d * length * batch).astype(np.float32).reshape(batch, length, 3 * d)
+    ramp = np.linspace(0.2, 4.0, length, dtype=np.float32)[None, :, None]
+    qkv[:, :, d:2 * d] *= ramp
+    qkv[:, :, :d] *= 2.0
+    qkv = qkv.reshape(-1)
+    valid = np.ones(length * batch, np.uint8)
+    valid[length + 250:] = 0
+    keep = oracle.laya_build_mask(valid, length, batch, -1)
+    want = oracle.laya_attention_block(qkv, keep, d, heads, length, batch, 160000.0)
+    got = laya_gpu(gpu_ctx, qkv, keep, d, heads, length, batch, 160000.0)
+    assert_close(got, want, F32_TOL)
+
+
 def test_laya_heads_not_dividing_writes_zeros(gpu_ctx):
     out = np.full(6 * 4, 7.0, np.float32)
     te.laya_attention_block(np.ones(3 * 6 * 4, np.float32), np.ones(16, np.uint8), 6, 4, 0.0,
