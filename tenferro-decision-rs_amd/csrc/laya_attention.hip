@@ -88,20 +88,27 @@ __device__ __forceinline__ f32x4 rot_hi(f32x4 x, f32x4 y, f32x4 c, f32x4 s) {
   return x * s + y * c;
 }
 
-__device__ __forceinline__ bool all_finite(f32x4 v) {
-  return __builtin_isfinite(v[0]) && __builtin_isfinite(v[1]) && __builtin_isfinite(v[2]) &&
-         __builtin_isfinite(v[3]);
+// Raw buffer loads through an SGPR resource: the per-lane byte offset is
+// fixed for the whole walk, the tile base is a scalar offset, and any byte
+// at or past `bytes` reads as 0 (the hardware range check), so keys past the
+// row's end need no clamping or selects.
+constexpr int kBufferWord3 = 0x00020000;  // gfx9 raw buffer (no format, no swizzle)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
+                                           kBufferWord3);
+}
+__device__ __forceinline__ f32x4 buffer_load4(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
 
 // One K/V tile's global data held in registers between the prefetch (issued
-// at the top of a step) and the LDS commit (interleaved with that step's P.V
-// products).
+// before the previous tile's products) and the LDS commit (after them).
 //
-// VEC (hd == HDP, hd % 8 == 0, 16-byte aligned rows): a K task is one
-// (key, chunk c) with its RoPE partner chunk c + half/4 (and, with ROPE, the
-// table chunks), all 16-byte loads; a V task is one (key, chunk). Otherwise
-// (any hd) the commit loads and rotates element by element and the prefetch
-// is empty.
+// VEC (hd == HDP, hd % 8 == 0, 16-byte aligned rows, the batch row within
+// 2 GiB): buffer loads; a K task is one (key, chunk c) with its RoPE partner
+// chunk c + half/4 (and, with ROPE, the table chunks); a V task is one
+// (key, chunk). Keys at or past L read as 0. Otherwise (any hd) the commit
+// loads and rotates element by element and the prefetch is empty.
 template <int HDP, bool VEC, bool ROPE>
 struct LayaStage {
   static constexpr int KTASKS = kKeyTile * HDP / 8;
@@ -111,96 +118,73 @@ struct LayaStage {
   static constexpr int CN = ROPE ? KN : 1;
   f32x4 ka[KN], kb[KN], c[CN], s[CN];
   f32x4 v[VN];
+  // Resources and per-lane byte offsets, fixed for the walk.
+  __amdgpu_buffer_rsrc_t rk, rv, rc, rs;
+  int ok[KN], oc[KN], ov[VN];
+  int hh4, tok4, hh4k;
 
-  __device__ __forceinline__ void fetch(const LayaArgs &a, const float *xb, size_t tok, int k0,
-                                        int tid) {
+  __device__ __forceinline__ void init(const LayaArgs &a, const float *xb, size_t tok, int tid) {
     if constexpr (VEC) {
-      // Every load is unconditional with a clamped (in-bounds) index, so all
-      // of them are in flight together; out-of-range keys are zeroed at
-      // commit time.
-      const int hh = a.half;
+      const int L = a.L, hh = a.half;
+      const uint32_t row_bytes = (uint32_t)(((size_t)(L - 1) * tok + a.hd) * 4);
+      rk = buffer_rsrc(xb + a.d, row_bytes);
+      rv = buffer_rsrc(xb + 2 * a.d, row_bytes);
+      if constexpr (ROPE) {
+        rc = buffer_rsrc(a.cos_t, (uint32_t)((size_t)L * hh * 4));
+        rs = buffer_rsrc(a.sin_t, (uint32_t)((size_t)L * hh * 4));
+      }
 #pragma unroll
       for (int i = 0; i < KN; ++i) {
         const int task = min(tid + 256 * i, KTASKS - 1);
-        const int key = min(k0 + task / (HDP / 8), a.L - 1), cp = task % (HDP / 8);
-        const float *row = xb + (size_t)key * tok + a.d;
-        ka[i] = *reinterpret_cast<const f32x4 *>(row + 4 * cp);
-        kb[i] = *reinterpret_cast<const f32x4 *>(row + 4 * cp + hh);
-        if constexpr (ROPE) {
-          c[i] = *reinterpret_cast<const f32x4 *>(a.cos_t + (size_t)key * hh + 4 * cp);
-          s[i] = *reinterpret_cast<const f32x4 *>(a.sin_t + (size_t)key * hh + 4 * cp);
-        }
+        const int kk = task / (HDP / 8), cp = task % (HDP / 8);
+        ok[i] = (int)(((size_t)kk * tok + 4 * cp) * 4);
+        oc[i] = (kk * hh + 4 * cp) * 4;
       }
 #pragma unroll
       for (int i = 0; i < VN; ++i) {
         const int task = min(tid + 256 * i, VTASKS - 1);
-        const int key = min(k0 + task / (HDP / 4), a.L - 1), ch = task % (HDP / 4);
-        v[i] = *reinterpret_cast<const f32x4 *>(xb + (size_t)key * tok + 2 * a.d + 4 * ch);
+        const int kk = task / (HDP / 4), ch = task % (HDP / 4);
+        ov[i] = (int)(((size_t)kk * tok + 4 * ch) * 4);
       }
+      hh4 = hh * 4;
+      tok4 = (int)(tok * 4);
+      hh4k = hh * 4 * kKeyTile;
     }
   }
 
-  // The VEC commit in pieces a caller can spread between other work:
-  // pieces [0, 2*KN) write K chunks (even: the low half of task i/2, odd:
-  // the high half), pieces [2*KN, 2*KN + VN) write V chunks. Each returns 1
-  // if it wrote a NaN or infinite V value.
-  static constexpr int PIECES = 2 * KN + VN;
-  __device__ __forceinline__ int commit_piece(int piece, const LayaArgs &a, int k0, int tid,
-                                              float *Ks, float *Vs) {
-    constexpr int KS = HDP + 4, VS = HDP + 8;
-    const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (piece < 2 * KN) {
-      const int i = piece / 2;
-      const int task = tid + 256 * i;
-      if (KTASKS % 256 == 0 || task < KTASKS) {
-        const int kk = task / (HDP / 8), cp = task % (HDP / 8);
-        const bool live = k0 + kk < a.L;
-        f32x4 x;
-        if (piece % 2 == 0) {
-          x = ka[i];
-          if constexpr (ROPE) x = rot_lo(ka[i], kb[i], c[i], s[i]);
-        } else {
-          x = kb[i];
-          if constexpr (ROPE) x = rot_hi(ka[i], kb[i], c[i], s[i]);
+  __device__ __forceinline__ void fetch(int k0) {
+    if constexpr (VEC) {
+      const int sk = k0 * tok4, sc = k0 * hh4;
+#pragma unroll
+      for (int i = 0; i < KN; ++i) {
+        ka[i] = buffer_load4(rk, ok[i], sk);
+        kb[i] = buffer_load4(rk, ok[i], sk + hh4);
+        if constexpr (ROPE) {
+          c[i] = buffer_load4(rc, oc[i], sc);
+          s[i] = buffer_load4(rs, oc[i], sc);
         }
-        x = live ? x : z;
-        *reinterpret_cast<f32x4 *>(&Ks[kk * KS + (piece % 2) * a.half + 4 * cp]) = x;
       }
-      return 0;
+#pragma unroll
+      for (int i = 0; i < VN; ++i) v[i] = buffer_load4(rv, ov[i], sk);
     }
-    const int i = piece - 2 * KN;
-    const int task = tid + 256 * i;
-    int nonfinite = 0;
-    if (VTASKS % 256 == 0 || task < VTASKS) {
-      const int kk = task / (HDP / 4), ch = task % (HDP / 4);
-      const f32x4 x = k0 + kk < a.L ? v[i] : z;
-      nonfinite = !all_finite(x);
-      *reinterpret_cast<f32x4 *>(&Vs[kk * VS + 4 * ch]) = x;
-    }
-    return nonfinite;
   }
 
-  // Writes the tile to LDS (K rotated); returns 1 if a V value is NaN or inf.
-  __device__ __forceinline__ int commit(const LayaArgs &a, const float *xb, size_t tok, int k0,
-                                        int tid, float *Ks, float *Vs) {
+  // Writes the tile to LDS (K rotated).
+  __device__ __forceinline__ void commit(const LayaArgs &a, const float *xb, size_t tok, int k0,
+                                         int tid, float *Ks, float *Vs) {
     constexpr int KS = HDP + 4, VS = HDP + 8;
-    int nonfinite = 0;
     if constexpr (VEC) {
       const int hh = a.half;
-      const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int i = 0; i < KN; ++i) {
         const int task = tid + 256 * i;
         if (KTASKS % 256 == 0 || task < KTASKS) {  // blockDim is 256
           const int kk = task / (HDP / 8), cp = task % (HDP / 8);
-          const bool live = k0 + kk < a.L;
           f32x4 lo = ka[i], hi = kb[i];
           if constexpr (ROPE) {
             lo = rot_lo(ka[i], kb[i], c[i], s[i]);
             hi = rot_hi(ka[i], kb[i], c[i], s[i]);
           }
-          lo = live ? lo : z;
-          hi = live ? hi : z;
           *reinterpret_cast<f32x4 *>(&Ks[kk * KS + 4 * cp]) = lo;
           *reinterpret_cast<f32x4 *>(&Ks[kk * KS + hh + 4 * cp]) = hi;
         }
@@ -210,9 +194,7 @@ struct LayaStage {
         const int task = tid + 256 * i;
         if (VTASKS % 256 == 0 || task < VTASKS) {
           const int kk = task / (HDP / 4), ch = task % (HDP / 4);
-          const f32x4 x = k0 + kk < a.L ? v[i] : z;
-          nonfinite |= !all_finite(x);
-          *reinterpret_cast<f32x4 *>(&Vs[kk * VS + 4 * ch]) = x;
+          *reinterpret_cast<f32x4 *>(&Vs[kk * VS + 4 * ch]) = v[i];
         }
       }
     } else {
@@ -227,47 +209,138 @@ struct LayaStage {
           const float *sr = ROPE ? a.sin_t + (size_t)key * hh : nullptr;
           kv = rope_elem(row + a.d, dd, hd, hh, cr, sr);
           vv = row[2 * a.d + dd];
-          nonfinite |= !__builtin_isfinite(vv);
         }
         Ks[kk * KS + dd] = kv;
         Vs[kk * VS + dd] = vv;
       }
     }
-    return nonfinite;
   }
-};
-
-// Output of the fast softmax step on one S^T tile (see the kernel).
-struct LayaSoft {
-  f32x16 p;
-  float rs, mn;
-  bool need;
 };
 
 // ------------------------------------------------------------------- kernel
 
-// Scheduling hints for one straight-line block: `n` repeats of one MFMA
-// followed by up to `v` VALU instructions (the compiler fills what exists).
-template <int n, int v>
-__device__ __forceinline__ void interleave_mfma_valu() {
+// The careful path for one wave's 32 queries (rare: NaN or inf among its
+// kept scores or values), recomputed from global memory without barriers
+// and written to out: the reference's masked softmax with an exact running
+// max (non-finite scores weigh 0, a +inf score empties the row,
+// lib.rs:1111-1136) and key-by-key accumulation that skips zero
+// probabilities (lib.rs:1143-1151). Kept out of line so that its registers
+// never weigh on the walk. Pw: 32 x 33 floats of LDS owned by the wave.
+template <int HDP, int MODE, bool ROPE>
+__device__ __noinline__ void laya_redo_wave(const LayaArgs a, int b, int head, int q0,
+                                            int kt_begin, int kt_end, float *Pw) {
+  constexpr int QS = HDP / 2, NB = HDP / 32, PS = kKeyTile + 1;
+  const int lane = threadIdx.x & 63, col = lane & 31, half = lane >> 5;
+  const int L = a.L, hd = a.hd, hh = a.half, nkt = a.nkt;
+  const int q = q0 + col;
+  const bool qin = q < L;
+  const size_t tok = 3 * (size_t)a.d;
+  const float *xb = a.qkv + (size_t)b * L * tok + (size_t)head * hd;
+  const int qq = qin ? q : 0;
+  float qreg[QS];
+  {
+    const float *row = xb + (size_t)qq * tok;
+    const float *cr = ROPE ? a.cos_t + (size_t)qq * hh : nullptr;
+    const float *sr = ROPE ? a.sin_t + (size_t)qq * hh : nullptr;
 #pragma unroll
-  for (int i = 0; i < n; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x002, v, 0);
+    for (int x = 0; x < QS; ++x) qreg[x] = qin ? rope_elem(row, half * QS + x, hd, hh, cr, sr) : 0.0f;
+  }
+  bool q_valid = false;
+  if (MODE == kMaskStruct) q_valid = qin && a.valid[(size_t)b * L + qq] != 0;
+  f32x16 O[NB];
+#pragma unroll
+  for (int j = 0; j < NB; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) O[j][r] = 0.0f;
+  float m = kNoMax, l = 0.0f;
+#pragma unroll 1
+  for (int kt = kt_begin; kt < kt_end; ++kt) {
+    const int k0 = kt * kKeyTile;
+    uint32_t wk = 0u;
+    if (MODE == kMaskBits) {
+      const uint32_t x = a.bits[((size_t)b * nkt + kt) * L + qq];
+      wk = qin ? x : 0u;
+    } else {
+      const int key = k0 + col;
+      const bool kv = key < L && a.valid[(size_t)b * L + min(key, L - 1)] != 0;
+      const uint32_t vbits = (uint32_t)__ballot(kv);
+      if (qin) {
+        wk = vbits;
+        if (a.window >= 0 && q_valid) wk &= range_bits(q - a.window - k0, q + a.window - k0);
+      }
+    }
+    if (__ballot(wk != 0u) == 0) continue;
+    const int key = k0 + col;
+    const int kc = min(key, L - 1);
+    const float *krow = xb + (size_t)kc * tok + a.d;
+    const float *cr = ROPE ? a.cos_t + (size_t)kc * hh : nullptr;
+    const float *sr = ROPE ? a.sin_t + (size_t)kc * hh : nullptr;
+    f32x16 p;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) p[r] = 0.0f;
+#pragma unroll
+    for (int x = 0; x < QS; ++x) {
+      const float kx = rope_elem(krow, half * QS + x, hd, hh, cr, sr);
+      p = mfma_32x32x2(key < L ? kx : 0.0f, qreg[x], p);
+    }
+    const float alpha = softmax_tile(p, wk, half, a.c1, m, l);
+    // alpha == 0: every earlier probability is 0 against the new max, so
+    // earlier (possibly infinite) values drop out as in the reference.
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) O[j][r] = alpha == 0.0f ? 0.0f : O[j][r] * alpha;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) Pw[acc_row(r, half) * PS + col] = p[r];
+#pragma unroll 1
+    for (int kk = 0; kk < kKeyTile; ++kk) {
+      const float pk = Pw[kk * PS + col];
+      if (pk == 0.0f) continue;  // only kept keys inside the row get here
+      const float *vrow = xb + (size_t)(k0 + kk) * tok + 2 * a.d;
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int dd = j * 32 + acc_row(r, half);
+          if (dd < hd) O[j][r] += pk * vrow[dd];
+        }
+    }
+  }
+  const float lt = pair_sum(l);
+  const float inv = lt > 0.0f ? fast_rcp(lt) : __builtin_nanf("");
+  if (qin) {
+    float *orow = a.out + ((size_t)b * L + q) * a.d + (size_t)head * hd;
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int dd = j * 32 + acc_row(r, half);
+        if (dd < hd) orow[dd] = O[j][r] * inv;
+      }
   }
 }
 
+// Occupancy target: three workgroups (12 waves) per CU where the registers
+// allow it. On gfx950 the f32 MFMAs and the vector ALU share the SIMD (they
+// never run at the same time), so the walk keeps its vector work per tile
+// small and relies on other waves to cover memory and barrier waits.
+template <int HDP>
+constexpr int laya_groups_per_cu() {
+  return HDP <= 64 ? 3 : 2;
+}
+
 template <int HDP, int MODE, bool VEC, bool ROPE>
-__global__ __launch_bounds__(256, 2) void laya_attention_kernel(const LayaArgs a) {
+__global__ __launch_bounds__(256, laya_groups_per_cu<HDP>()) void laya_attention_kernel(
+    const LayaArgs a) {
   constexpr int KS = HDP + 4;  // K row stride (floats): 16-byte rows, conflict-free b128 reads
   constexpr int VS = HDP + 8;  // V row stride: the two lane halves read rows 4 apart
   constexpr int QS = HDP / 2;  // Q registers per lane
   constexpr int NB = HDP / 32; // 32-row blocks of O^T
   constexpr int GQ = kLayaGroupQueries;
-  constexpr int NBUF = 3;      // tiles t (V read), t+1 (K read), t+2 (being written)
-  __shared__ __attribute__((aligned(16))) float Ks[NBUF][kKeyTile * KS];
-  __shared__ __attribute__((aligned(16))) float Vs[NBUF][kKeyTile * VS];
-  __shared__ int s_nf[NBUF][kWavesPerGroup];  // per-wave non-finite V flags, by buffer
+  // K buffers then V buffers, one block (reused after the walk).
+  __shared__ __attribute__((aligned(16))) float smem[2 * kKeyTile * (KS + VS)];
+  auto Ks = [&](int i) { return smem + i * (kKeyTile * KS); };
+  auto Vs = [&](int i) { return smem + 2 * kKeyTile * KS + i * (kKeyTile * VS); };
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 31, half = lane >> 5;
@@ -377,6 +450,11 @@ __global__ __launch_bounds__(256, 2) void laya_attention_kernel(const LayaArgs a
     }
   }
 
+  // The reductions above leave the same value in every lane; say so, so that
+  // the walk's counters and scalar offsets stay in scalar registers.
+  kt_begin = __builtin_amdgcn_readfirstlane(kt_begin);
+  kt_end = __builtin_amdgcn_readfirstlane(kt_end);
+
   if constexpr (VEC) {
 #pragma unroll
     for (int c = 0; c < QS / 4; ++c) {
@@ -400,10 +478,10 @@ __global__ __launch_bounds__(256, 2) void laya_attention_kernel(const LayaArgs a
     q_valid = qin && x != 0;
   }
 
-  // This lane's keep word for key tile kt (bit j: key 32*kt + j); 0 past the
-  // span. The raw word or validity byte is fetched two tiles ahead (mask_of)
-  // and turned into the word (keep_word) only after that step's barrier, so
-  // waiting on it never stalls the tile prefetch issued beside it.
+  // This lane's keep word for key tile kt (bit j: key 32*kt + j). The raw
+  // word or validity byte is fetched one tile ahead (mask_of) and turned
+  // into the word (keep_word) only after that tile's barrier, so waiting on
+  // it never stalls the tile prefetch issued beside it.
   auto mask_of = [&](int kt) -> uint32_t {
     if (MODE == kMaskBits)
       return a.bits[((size_t)b * nkt + min(kt, nkt - 1)) * L + min(q, L - 1)];
@@ -411,7 +489,6 @@ __global__ __launch_bounds__(256, 2) void laya_attention_kernel(const LayaArgs a
   };
   auto keep_word = [&](int kt, uint32_t x) -> uint32_t {
     uint32_t w = 0u;
-    if (kt >= kt_end) return 0u;
     if (MODE == kMaskBits) {
       w = qin ? x : 0u;
     } else {
@@ -451,236 +528,91 @@ __global__ __launch_bounds__(256, 2) void laya_attention_kernel(const LayaArgs a
     }
     return s;
   };
-  auto pv = [&](const float *Vc, const f32x16 &p) {
-#pragma unroll
-    for (int j = 0; j < NB; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r)
-        O[j] = mfma_32x32x2(Vc[acc_row(r, half) * VS + j * 32 + col], p[r], O[j]);
-  };
 
-  // -------- software pipeline over three LDS buffers. Step t: prefetch tile
-  // t+2 into registers; S(t+1) on the matrix cores while the vector ALUs run
-  // the softmax of S(t); P(t).V(t) on the matrix cores while tile t+2 is
-  // committed to LDS; one barrier. Whether a wave staged a NaN or infinite
-  // value travels in s_nf[buffer][wave].
-  const int nt = kt_end - kt_begin;
+  // -------- the walk: tile kt+1 is fetched into registers before the
+  // products of tile kt and committed to the other LDS buffer after them;
+  // one barrier per tile.
+  //
+  // Exponents are fma(s, c1, -m) against a reference m that only moves when
+  // a tile max exceeds it by more than kRescaleSlack. Non-finite inputs are
+  // kept off this path: a wave whose kept scores sum to NaN or inf stops
+  // computing (it still stages tiles and meets the barriers), a NaN or inf
+  // value reaches O and stays there, and either way the wave redoes its
+  // queries with the reference's exact semantics after the walk.
   LayaStage<HDP, VEC, ROPE> st;
-  auto publish = [&](int slot, int nonfin) {
-    const int wnf = __ballot(nonfin) != 0;
-    if (lane == 0) s_nf[slot][wave] = wnf;
-  };
-  auto read_nf = [&](int slot) {
-    int f = 0;
-#pragma unroll
-    for (int i = 0; i < kWavesPerGroup; ++i) f |= s_nf[slot][i];
-    return f;
-  };
-  uint32_t w0 = 0u, w1 = 0u;  // keep words of tiles t and t+1
-  int nf0 = 0, nf1 = 0;       // non-finite values in tiles t and t+1
-  {
-    LayaStage<HDP, VEC, ROPE> st1;
-    uint32_t x0 = 0u, x1 = 0u;
-    if (nt > 0) {
-      x0 = mask_of(kt_begin);
-      st.fetch(a, xb, tok, kt_begin * kKeyTile, tid);
-    }
-    if (nt > 1) {
-      x1 = mask_of(kt_begin + 1);
-      st1.fetch(a, xb, tok, (kt_begin + 1) * kKeyTile, tid);
-    }
-    int f0 = 0, f1 = 0;
-    if (nt > 0) f0 = st.commit(a, xb, tok, kt_begin * kKeyTile, tid, Ks[0], Vs[0]);
-    if (nt > 1) f1 = st1.commit(a, xb, tok, (kt_begin + 1) * kKeyTile, tid, Ks[1], Vs[1]);
-    publish(0, f0);
-    publish(1, f1);
-    __syncthreads();
-    nf0 = read_nf(0);
-    nf1 = read_nf(1);
-    if (nt > 0) w0 = keep_word(kt_begin, x0);
-    if (nt > 1) w1 = keep_word(kt_begin + 1, x1);
+  st.init(a, xb, tok, tid);
+  uint32_t w = 0u, m_next = 0u;
+  if (kt_begin < kt_end) {
+    const uint32_t m0 = mask_of(kt_begin);
+    st.fetch(kt_begin * kKeyTile);
+    st.commit(a, xb, tok, kt_begin * kKeyTile, tid, Ks(0), Vs(0));
+    w = keep_word(kt_begin, m0);
   }
-
-  f32x16 s_cur;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) s_cur[r] = 0.0f;
-  if (nt > 0 && __ballot(w0 != 0u) != 0) s_cur = scores(Ks[0]);
-
-  // Fast walk: finite scores and values. Its only accumulator updates are
-  // the P.V products and a wave-uniform rescale. A wave leaves it (without
-  // touching O, m or l) at the first tile with a non-finite kept score or
-  // value and finishes in the careful walk below; both walks commit the same
-  // tiles and run the same barriers, so waves may be in different walks.
-  int t = 0, cb = 0;
-  uint32_t m2 = 0u;
-  for (; t < nt; ++t) {
-    if (nf0) break;  // workgroup-uniform
-    const int nb = cb == NBUF - 1 ? 0 : cb + 1, fb = nb == NBUF - 1 ? 0 : nb + 1;
-    const bool more1 = t + 1 < nt, more2 = t + 2 < nt;
-    if (more2) {
-      m2 = mask_of(kt_begin + t + 2);
-      st.fetch(a, xb, tok, (kt_begin + t + 2) * kKeyTile, tid);
+  __syncthreads();
+  bool tainted = false;  // wave-uniform
+  int cur = 0;
+  for (int kt = kt_begin; kt < kt_end; ++kt) {
+    const bool more = kt + 1 < kt_end;
+    if (more) {
+      m_next = mask_of(kt + 1);
+      st.fetch((kt + 1) * kKeyTile);
     }
-    const bool act = __ballot(w0 != 0u) != 0;            // wave-uniform
-    const bool act1 = more1 && __ballot(w1 != 0u) != 0;  // wave-uniform
-    LayaSoft so;
-    if (act) {
-      if (__ballot(qin && w0 != 0xffffffffu) != 0) {
+    if (!tainted && __ballot(w != 0u) != 0) {  // wave-uniform
+      f32x16 s = scores(Ks(cur));
+      if (__ballot(qin && w != 0xffffffffu) != 0) {
         // A tile some query of the wave keeps only in part: mask it.
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          s_cur[r] = ((w0 >> acc_row(r, half)) & 1u) ? s_cur[r] : -INFINITY;
+        for (int r = 0; r < 16; ++r) s[r] = ((w >> acc_row(r, half)) & 1u) ? s[r] : -INFINITY;
       }
-      // The tile max and the exponent reference, ahead of the fused block
-      // (the cross-lane swap would otherwise fence the exponentials off from
-      // the MFMAs they are meant to overlap).
-      float mx = s_cur[0];
+      float mx = s[0];
 #pragma unroll
-      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s_cur[r]);
+      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
       const float mxs = pair_max(mx) * c1;
-      so.need = mxs > m + kRescaleSlack;
-      so.mn = so.need ? mxs : m;
-    }
-    f32x16 s_nx;
-    if (act && act1) {
-      // S(t+1) interleaved with the exponentials of S(t), in a fixed order
-      // (sched_barrier fences): each MFMA is followed by its share of the
-      // vector work, which runs while the matrix core is busy; the K operand
-      // for the next 4 MFMAs is read one group ahead.
-      so.rs = 0.0f;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s_nx[r] = 0.0f;
-      const f32x4 *krow = reinterpret_cast<const f32x4 *>(&Ks[nb][col * KS + half * QS]);
-      constexpr int STEP = QS / 16;  // MFMAs per exponential
-      f32x4 kv = krow[0];
-#pragma unroll
-      for (int c = 0; c < QS / 4; ++c) {
-        const f32x4 kvn = krow[c + 1 < QS / 4 ? c + 1 : c];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int k = 4 * c + i;
-          s_nx = mfma_32x32x2(kv[i], qreg[k], s_nx);
-          if (k % STEP == 0) {
-            const int r = k / STEP;
-            so.p[r] = fast_exp2(__builtin_fmaf(s_cur[r], c1, -so.mn));
-            so.rs += so.p[r];
-          }
-          __builtin_amdgcn_sched_barrier(0);
-        }
-        kv = kvn;
-      }
-    } else if (act) {
-      so.rs = 0.0f;
+      const bool need = mxs > m + kRescaleSlack;
+      const float mn = need ? mxs : m;
+      float rs = 0.0f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        so.p[r] = fast_exp2(__builtin_fmaf(s_cur[r], c1, -so.mn));
-        so.rs += so.p[r];
+        s[r] = fast_exp2(__builtin_fmaf(s[r], c1, -mn));
+        rs += s[r];
       }
-    } else if (act1) {
-      s_nx = scores(Ks[nb]);
-    }
-    if (act) {
-      if (__ballot(!__builtin_isfinite(so.rs)) != 0) break;
-      if (__ballot(so.need) != 0) {
-        const float alpha = fast_exp2(m - so.mn);  // exactly 1 where the reference stays
+      if (__ballot(qin && !__builtin_isfinite(rs)) != 0) {
+        tainted = true;
+      } else {
+        if (__ballot(need) != 0) {
+          const float alpha = fast_exp2(m - mn);  // exactly 1 where the reference stays
 #pragma unroll
-        for (int j = 0; j < NB; ++j) O[j] *= alpha;
-        l *= alpha;
-      }
-      l += so.rs;
-      m = so.mn;
-    }
-    int f2 = 0;
-    if (act && more2) {
-      if constexpr (VEC) {
-        // P(t).V(t) with the commit of tile t+2 spread over its first MFMAs
-        // (fixed order, as above); the two O^T blocks alternate so that
-        // consecutive MFMAs are independent, and each V operand is read four
-        // MFMAs ahead.
-        const float *Vc = Vs[cb];
-        const int k2 = (kt_begin + t + 2) * kKeyTile;
-        constexpr int NM = NB * 16;
-        constexpr int NP = LayaStage<HDP, VEC, ROPE>::PIECES;
-        constexpr int PSTEP = NM / NP >= 2 ? 2 : 1;
-        auto vop = [&](int idx) {
-          return Vc[acc_row(idx / NB, half) * VS + (idx % NB) * 32 + col];
-        };
-        float vq[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) vq[i] = vop(i);
-#pragma unroll
-        for (int idx = 0; idx < NM; ++idx) {
-          const float vcur = vq[idx % 4];
-          if (idx + 4 < NM) vq[idx % 4] = vop(idx + 4);
-          O[idx % NB] = mfma_32x32x2(vcur, so.p[idx / NB], O[idx % NB]);
-          if (idx % PSTEP == 0 && idx / PSTEP < NP)
-            f2 |= st.commit_piece(idx / PSTEP, a, k2, tid, Ks[fb], Vs[fb]);
-          __builtin_amdgcn_sched_barrier(0);
+          for (int j = 0; j < NB; ++j) O[j] *= alpha;
+          l *= alpha;
         }
-      } else {
-        pv(Vs[cb], so.p);
-        f2 = st.commit(a, xb, tok, (kt_begin + t + 2) * kKeyTile, tid, Ks[fb], Vs[fb]);
-      }
-    } else if (act) {
-      pv(Vs[cb], so.p);
-    } else if (more2) {
-      f2 = st.commit(a, xb, tok, (kt_begin + t + 2) * kKeyTile, tid, Ks[fb], Vs[fb]);
-    }
-    publish(fb, f2);
-    __syncthreads();
-    nf0 = nf1;
-    nf1 = read_nf(fb);
-    w0 = w1;
-    w1 = more2 ? keep_word(kt_begin + t + 2, m2) : 0u;
-    if (act1) s_cur = s_nx;
-    cb = nb;
-  }
-
-  // Careful walk, from the tile where the fast walk stopped: the reference's
-  // masked softmax with an exact running max (non-finite scores weigh 0, a
-  // +inf score empties the row) and, for a tile holding a non-finite value,
-  // key-by-key accumulation that skips zero probabilities.
-  for (; t < nt; ++t) {
-    const int nb = cb == NBUF - 1 ? 0 : cb + 1, fb = nb == NBUF - 1 ? 0 : nb + 1;
-    const bool more2 = t + 2 < nt;
-    if (more2) {
-      m2 = mask_of(kt_begin + t + 2);
-      st.fetch(a, xb, tok, (kt_begin + t + 2) * kKeyTile, tid);
-    }
-    if (__ballot(w0 != 0u) != 0) {
-      f32x16 p = scores(Ks[cb]);
-      const float alpha = softmax_tile(p, qin ? w0 : 0u, half, c1, m, l);
-      // alpha == 0: every earlier probability is 0 against the new max, so
-      // earlier (possibly infinite) values drop out as in the reference.
+        l += rs;
+        m = mn;
+        const float *Vc = Vs(cur);
 #pragma unroll
-      for (int j = 0; j < NB; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) O[j][r] = alpha == 0.0f ? 0.0f : O[j][r] * alpha;
-      const float *Vc = Vs[cb];
-      if (!nf0) {
-        pv(Vc, p);
-      } else {
-        // The reference's scalar path (lib.rs:1143-1151): a masked
-        // non-finite value never leaks.
-        for (int kk = 0; kk < kKeyTile; ++kk) {
-          const float pk = tile_prob(p, kk, col);
-          if (pk == 0.0f) continue;
+        for (int r = 0; r < 16; ++r)
 #pragma unroll
           for (int j = 0; j < NB; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) O[j][r] += pk * Vc[kk * VS + j * 32 + acc_row(r, half)];
-        }
+            O[j] = mfma_32x32x2(Vc[acc_row(r, half) * VS + j * 32 + col], s[r], O[j]);
       }
     }
-    int f2 = 0;
-    if (more2) f2 = st.commit(a, xb, tok, (kt_begin + t + 2) * kKeyTile, tid, Ks[fb], Vs[fb]);
-    publish(fb, f2);
+    if (more) st.commit(a, xb, tok, (kt + 1) * kKeyTile, tid, Ks(cur ^ 1), Vs(cur ^ 1));
     __syncthreads();
-    nf0 = nf1;
-    nf1 = read_nf(fb);
-    w0 = w1;
-    w1 = more2 ? keep_word(kt_begin + t + 2, m2) : 0u;
-    cb = nb;
+    if (more) w = keep_word(kt + 1, m_next);
+    cur ^= 1;
+  }
+
+  // -------- careful redo (rare): NaN / inf among this wave's kept scores
+  // or values. Every wave's LDS reads of the walk precede its last barrier,
+  // so the wave may now use its own slice of the LDS block.
+  bool bad = false;
+#pragma unroll
+  for (int j = 0; j < NB; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) bad |= !__builtin_isfinite(O[j][r]);
+  if (tainted || __ballot(qin && bad) != 0) {
+    laya_redo_wave<HDP, MODE, ROPE>(a, b, head, qg0 + wave * kWaveQueries, kt_begin, kt_end,
+                                    smem + wave * kKeyTile * (kKeyTile + 1));
+    return;
   }
 
   // -------- normalize and store: out[feat + d + hidden*(q + L*b)]
@@ -755,9 +687,11 @@ static hipError_t launch_laya_pick(const LayaArgs &a, int heads, int batch, int 
                                    hipStream_t stream) {
   // 16-byte row loads need hd == HDP, hd % 8 == 0 (RoPE halves in whole
   // chunks), a row stride of whole chunks and aligned bases.
+  // Buffer loads also need one batch row of qkv within 2 GiB.
   const bool vec = a.hd == HDP && a.hd % 8 == 0 && a.d % 4 == 0 &&
                    (reinterpret_cast<uintptr_t>(a.qkv) & 15) == 0 &&
-                   (reinterpret_cast<uintptr_t>(a.out) & 15) == 0;
+                   (reinterpret_cast<uintptr_t>(a.out) & 15) == 0 &&
+                   (size_t)a.L * 3 * (size_t)a.d * 4 < ((size_t)1 << 31);
   const bool rope = a.cos_t != nullptr;
   if (vec)
     return rope ? launch_laya_hd<HDP, true, true>(a, heads, batch, mode, stream)
