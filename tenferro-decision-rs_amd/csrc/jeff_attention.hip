@@ -95,44 +95,73 @@ __device__ __forceinline__ int row_start(const JeffArgs &a, const float *maskr, 
 
 // ---------------------------------------------------------------- K prep
 
+// First active key of a row (mask != 0; 0 for a row with none), computed by
+// one wave on its own.
+__device__ __forceinline__ int wave_first_active(const float *maskr, int L, int lane) {
+  int lo = 0x7fffffff;
+  for (int k0 = 0; k0 < L; k0 += 64 * 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = maskr[min(k0 + lane + 64 * u, L - 1)];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (k0 + lane + 64 * u < L && v[u] != 0.0f) lo = min(lo, k0 + lane + 64 * u);
+  }
+  lo = wave_min(lo);
+  return __builtin_amdgcn_readfirstlane(lo == 0x7fffffff ? 0 : lo);
+}
+
 // RMSNorm (lib.rs:676-691) and partial RoPE (692-709) of every key of one
 // (row, kv head) once per call, so attention workgroups stage finished keys.
 // One workgroup = 32 keys; output kp[row][kvh][key][HDP] (zero-padded past
-// hd), written in whole coalesced rows. Out: f32, or bf16 (RNE) for the
-// bf16 attention kernel.
+// hd), written in whole 16-byte chunks. Out: f32, or bf16 (RNE) for the
+// bf16 attention kernel. Every global load (keys, norm weights, RoPE table)
+// is issued before the first is used.
 template <int HDP, typename OutT>
 __global__ __launch_bounds__(256) void jeff_k_prep_kernel(const JeffArgs a, OutT *__restrict__ kp) {
-  constexpr int DP = HDP / 8;
+  constexpr int DP = HDP / 8;  // dims per thread: 8 threads per key
   constexpr int KS = HDP + 1;
+  constexpr int RT = (kKeyTile * (HDP / 2) + 255) / 256;  // RoPE pairs per thread, at most
   __shared__ float Kt[kKeyTile * KS];
   __shared__ float s_red[8 * kKeyTile];
-  __shared__ int s_span[2];
   const int tid = threadIdx.x, lane = tid & 63;
   const int row = blockIdx.z, kvh = blockIdx.y;
   const int L = a.L, hd = a.hd, rh = a.rot_half;
   const int k0 = blockIdx.x * kKeyTile;
-  const float *maskr = a.mask + (size_t)row * L;
-  const int start = row_start(a, maskr, tid, lane, s_span);
   const bool bf = sizeof(OutT) == 2;
   const size_t kv_off = row * a.kv_row + (size_t)kvh * hd * L;
   const int kk = tid & 31, part = tid >> 5;
   const int key = k0 + kk;
   const bool kin = key < L;
-  float ss = 0.0f;
-  float xs[DP];
+  const bool rope = a.cos_t != nullptr && rh > 0;
+  const int start = a.trim ? wave_first_active(a.mask + (size_t)row * L, L, lane) : 0;
+
+  float xs[DP], wn[DP], c[RT], sn[RT];
 #pragma unroll
-  for (int i = 0; i < DP; ++i) {  // all DP loads in flight at once
+  for (int i = 0; i < DP; ++i) {
     const int d = part * DP + i;
     const int dc = d < hd ? d : hd - 1;
     const size_t at = kv_off + (kin ? key : 0) + (size_t)L * dc;
-    const float x = bf ? __uint_as_float((uint32_t)static_cast<const uint16_t *>(a.k)[at] << 16)
-                       : static_cast<const float *>(a.k)[at];
-    xs[i] = (kin && d < hd) ? x : 0.0f;
+    xs[i] = bf ? __uint_as_float((uint32_t)static_cast<const uint16_t *>(a.k)[at] << 16)
+               : static_cast<const float *>(a.k)[at];
+    wn[i] = a.k_norm[dc];
   }
+  if (rope) {
+#pragma unroll
+    for (int u = 0; u < RT; ++u) {
+      const int e = min(tid + 256 * u, kKeyTile * rh - 1);
+      const int k2 = e / rh, i = e - k2 * rh;
+      const int pos = min(max(k0 + k2 - start, 0), L - 1);
+      c[u] = a.cos_t[(size_t)pos * rh + i];
+      sn[u] = a.sin_t[(size_t)pos * rh + i];
+    }
+  }
+  float ss = 0.0f;
 #pragma unroll
   for (int i = 0; i < DP; ++i) {
+    const int d = part * DP + i;
+    xs[i] = (kin && d < hd) ? xs[i] : 0.0f;
     ss += xs[i] * xs[i];
-    Kt[kk * KS + part * DP + i] = xs[i];
   }
   s_red[part * kKeyTile + kk] = ss;
   __syncthreads();
@@ -141,130 +170,333 @@ __global__ __launch_bounds__(256) void jeff_k_prep_kernel(const JeffArgs a, OutT
 #pragma unroll
     for (int p = 0; p < 8; ++p) tot += s_red[p * kKeyTile + kk];
     const float scale = rms_scale(tot, hd, a.eps);
-    float wn[DP];
-#pragma unroll
-    for (int i = 0; i < DP; ++i) wn[i] = a.k_norm[min(part * DP + i, hd - 1)];
 #pragma unroll
     for (int i = 0; i < DP; ++i) {
       const int d = part * DP + i;
-      if (kin && d < hd) Kt[kk * KS + d] = rms_apply(Kt[kk * KS + d], scale, wn[i]);
+      Kt[kk * KS + d] = (kin && d < hd) ? rms_apply(xs[i], scale, wn[i]) : 0.0f;
     }
   }
-  if (a.cos_t != nullptr && rh > 0) {
+  if (rope) {
     __syncthreads();
-    for (int e0 = 0; e0 < kKeyTile * rh; e0 += 256 * 4) {
-      float c[4], sn[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {  // clamped table loads, all in flight
-        const int e = min(e0 + tid + 256 * u, kKeyTile * rh - 1);
-        const int k2 = e / rh, i = e - k2 * rh;
-        const int pos = min(max(k0 + k2 - start, 0), L - 1);
-        c[u] = a.cos_t[(size_t)pos * rh + i];
-        sn[u] = a.sin_t[(size_t)pos * rh + i];
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int e = e0 + tid + 256 * u;
-        const int k2 = e / rh, i = e - k2 * rh;
-        if (e < kKeyTile * rh && k0 + k2 < L) {
-          const float x = Kt[k2 * KS + i], y = Kt[k2 * KS + i + rh];
-          Kt[k2 * KS + i] = rope_lo(x, y, c[u], sn[u]);
-          Kt[k2 * KS + i + rh] = rope_hi(x, y, c[u], sn[u]);
-        }
+    for (int u = 0; u < RT; ++u) {
+      const int e = tid + 256 * u;
+      const int k2 = e / rh, i = e - k2 * rh;
+      if (e < kKeyTile * rh && k0 + k2 < L) {
+        const float x = Kt[k2 * KS + i], y = Kt[k2 * KS + i + rh];
+        Kt[k2 * KS + i] = rope_lo(x, y, c[u], sn[u]);
+        Kt[k2 * KS + i + rh] = rope_hi(x, y, c[u], sn[u]);
       }
     }
   }
   __syncthreads();
   OutT *dst = kp + (((size_t)row * a.kv_heads + kvh) * L + k0) * HDP;
   const int nkeys = min(kKeyTile, L - k0);
-  for (int e = tid; e < nkeys * HDP; e += 256) {
-    const float y = Kt[(e / HDP) * KS + (e % HDP)];
+  constexpr int CH = 16 / (int)sizeof(OutT);  // elements per 16-byte chunk
+  for (int e = tid; e < nkeys * (HDP / CH); e += 256) {
+    const int k2 = e / (HDP / CH), d0 = (e % (HDP / CH)) * CH;
+    const float *src = &Kt[k2 * KS + d0];
     if constexpr (sizeof(OutT) == 2) {
-      const __bf16 h = (__bf16)y;
-      dst[e] = *reinterpret_cast<const uint16_t *>(&h);
+      u16x8 o;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const __bf16 h = (__bf16)src[t];
+        o[t] = *reinterpret_cast<const unsigned short *>(&h);
+      }
+      *reinterpret_cast<u16x8 *>(dst + (size_t)k2 * HDP + d0) = o;
     } else {
-      dst[e] = y;
+      const f32x4 o = {src[0], src[1], src[2], src[3]};
+      *reinterpret_cast<f32x4 *>(dst + (size_t)k2 * HDP + d0) = o;
     }
   }
 }
 
 // ----------------------------------------------------------- f32 attention
 
+// Row span of the mask, computed by one wave on its own (no barrier): first
+// and last active key (mask != 0), or (0, -1) for a row with none.
+__device__ __forceinline__ void wave_active_span(const float *maskr, int L, int lane, int &first,
+                                                 int &last) {
+  int lo = 0x7fffffff, hi = -1;
+  for (int k0 = 0; k0 < L; k0 += 64 * 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = maskr[min(k0 + lane + 64 * u, L - 1)];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int k = k0 + lane + 64 * u;
+      if (k < L && v[u] != 0.0f) {
+        lo = min(lo, k);
+        hi = max(hi, k);
+      }
+    }
+  }
+  lo = wave_min(lo);
+  hi = wave_max(hi);
+  first = __builtin_amdgcn_readfirstlane(hi >= 0 ? lo : 0);
+  last = __builtin_amdgcn_readfirstlane(hi);
+}
+
+// RMSNorm + partial RoPE of one wave's 16 queries of one head into the
+// B-operand registers of S^T = K Q^T: lane (col, grp) ends with
+// Qn[q0 + col][grp*QS + s]. Goes through the wave's own LDS rows qw
+// (16 x (HDP + 4) floats): raw rows (16-byte loads along tokens when VEC),
+// normalized in registers, rotated pairs in LDS, read back. Queries that are
+// past L or dropped (q < start) get zeros.
+template <int HDP, bool VEC>
+__device__ __forceinline__ void jeff_q_prep(const JeffArgs &a, const float *Q, int q0, int start,
+                                            float *qw, float (&qreg)[HDP / 4]) {
+  constexpr int QS = HDP / 4, QP = HDP + 4;
+  const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+  const int L = a.L, hd = a.hd, rh = a.rot_half;
+  const int q = q0 + col;
+  const bool q_live = q < L && q >= start;
+  if constexpr (VEC) {
+    // Task (d, g): queries q0 + 4g .. +3 of feature d, one 16-byte load;
+    // features past hd read as 0.
+    const __amdgpu_buffer_rsrc_t rq = buffer_rsrc(Q, (uint32_t)((size_t)hd * L * 4));
+#pragma unroll
+    for (int i0 = 0; i0 < HDP * 4; i0 += 64 * 4) {
+      f32x4 x[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {  // HDP * 4 < 256 only at HDP = 32: clamp, skip below
+        const int e = min(i0 + lane + 64 * u, HDP * 4 - 1), d = e >> 2, g = e & 3;
+        x[u] = buffer_load4(rq, (int)(((size_t)d * L + 4 * g) * 4), q0 * 4);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int e = i0 + lane + 64 * u, d = e >> 2, g = e & 3;
+        if (HDP * 4 % 256 == 0 || e < HDP * 4) {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) qw[(4 * g + t) * QP + d] = x[u][t];
+        }
+      }
+    }
+  } else {
+    for (int e0 = 0; e0 < 16 * HDP; e0 += 64 * 8) {
+      float x[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int e = e0 + lane + 64 * u, d = e >> 4, t = e & 15;
+        x[u] = Q[min(q0 + t, L - 1) + (size_t)L * min(d, hd - 1)];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int e = e0 + lane + 64 * u, d = e >> 4, t = e & 15;
+        qw[t * QP + d] = d < hd ? x[u] : 0.0f;
+      }
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float *qs = qw + col * QP + grp * QS;
+  f32x4 xv[QS / 4], wv[QS / 4];
+  float ss = 0.0f;
+#pragma unroll
+  for (int c = 0; c < QS / 4; ++c) {
+    xv[c] = *reinterpret_cast<const f32x4 *>(qs + 4 * c);
+    ss += xv[c][0] * xv[c][0] + xv[c][1] * xv[c][1] + xv[c][2] * xv[c][2] + xv[c][3] * xv[c][3];
+  }
+  // norm weights: 16-byte loads of this lane's QS dims (clamped past hd)
+#pragma unroll
+  for (int c = 0; c < QS / 4; ++c) {
+    const int d = grp * QS + 4 * c;
+    if (d + 3 < hd) {
+      wv[c] = *reinterpret_cast<const f32x4 *>(a.q_norm + d);
+    } else {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) wv[c][t] = a.q_norm[min(d + t, hd - 1)];
+    }
+  }
+  ss += __shfl_xor(ss, 16);
+  ss += pair_sum(ss) - ss;  // lanes l and l ^ 32 hold the other two groups
+  const float scale = rms_scale(ss, hd, a.eps);
+#pragma unroll
+  for (int c = 0; c < QS / 4; ++c) {
+    f32x4 y;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int d = grp * QS + 4 * c + t;
+      y[t] = (q_live && d < hd) ? rms_apply(xv[c][t], scale, wv[c][t]) : 0.0f;
+    }
+    *reinterpret_cast<f32x4 *>(qs + 4 * c) = y;
+  }
+  if (a.cos_t != nullptr && rh > 0) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (int e0 = 0; e0 < 16 * rh; e0 += 64 * 8) {
+      float c[8], sn[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {  // clamped table loads, all in flight
+        const int e = min(e0 + lane + 64 * u, 16 * rh - 1);
+        const int qi = e / rh, i = e - qi * rh;
+        const int pos = min(max(q0 + qi - start, 0), L - 1);
+        c[u] = a.cos_t[(size_t)pos * rh + i];
+        sn[u] = a.sin_t[(size_t)pos * rh + i];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int e = e0 + lane + 64 * u;
+        const int qi = e / rh, i = e - qi * rh;
+        const int qq = q0 + qi;
+        if (e < 16 * rh && qq < L && qq >= start) {
+          const float x = qw[qi * QP + i], y = qw[qi * QP + i + rh];
+          qw[qi * QP + i] = rope_lo(x, y, c[u], sn[u]);
+          qw[qi * QP + i + rh] = rope_hi(x, y, c[u], sn[u]);
+        }
+      }
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+  for (int c = 0; c < QS / 4; ++c) {
+    const f32x4 y = *reinterpret_cast<const f32x4 *>(qs + 4 * c);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) qreg[4 * c + t] = y[t];
+  }
+}
+
+// o = O^T * inv (0 when nothing was kept), times the sigmoid gate, stored
+// feature-major: the wave writes its 16 x HDP block through its LDS rows ow
+// (16 x (HDP + 4) floats) so that gate loads and output stores run along
+// tokens, 16 bytes at a time, when VEC. Dropped queries (q < start) get 0.
+template <int HDP, bool VEC>
+__device__ __forceinline__ void jeff_store(const JeffArgs &a, const float *Gt, float *OUT, int q0,
+                                           int start, float *ow, const f32x4 (&O)[HDP / 16],
+                                           float inv) {
+  constexpr int NB = HDP / 16, QP = HDP + 4;
+  const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+  const int L = a.L, hd = a.hd;
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const f32x4 v = O[j] * inv;  // dims 16j + 4grp + 0..3 of query q0 + col
+    *reinterpret_cast<f32x4 *>(ow + col * QP + 16 * j + 4 * grp) = v;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if constexpr (VEC) {
+    const __amdgpu_buffer_rsrc_t rg = buffer_rsrc(Gt, (uint32_t)((size_t)hd * L * 4));
+    const __amdgpu_buffer_rsrc_t ro = buffer_rsrc(OUT, (uint32_t)((size_t)hd * L * 4));
+#pragma unroll
+    for (int i0 = 0; i0 < HDP * 4; i0 += 64 * 4) {
+      f32x4 g[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {  // clamped as in the Q prep
+        const int e = min(i0 + lane + 64 * u, HDP * 4 - 1), d = e >> 2, gq = e & 3;
+        g[u] = buffer_load4(rg, (int)(((size_t)d * L + 4 * gq) * 4), q0 * 4);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int e = min(i0 + lane + 64 * u, HDP * 4 - 1), d = e >> 2, gq = e & 3;
+        const int qa = q0 + 4 * gq;  // L % 4 == 0: the 4 queries are all in or all out
+        f32x4 o;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float x = ow[(4 * gq + t) * QP + d] * fast_sigmoid(g[u][t]);
+          o[t] = qa + t < start ? 0.0f : x;
+        }
+        if (qa < L && d < hd) buffer_store4(o, ro, (int)(((size_t)d * L + 4 * gq) * 4), q0 * 4);
+      }
+    }
+  } else {
+    for (int e0 = 0; e0 < 16 * HDP; e0 += 64 * 8) {
+      float g[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int e = e0 + lane + 64 * u, d = e >> 4, t = e & 15;
+        g[u] = Gt[min(q0 + t, L - 1) + (size_t)L * min(d, hd - 1)];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int e = e0 + lane + 64 * u, d = e >> 4, t = e & 15;
+        const int qq = q0 + t;
+        if (qq < L && d < hd)
+          OUT[qq + (size_t)L * d] = qq < start ? 0.0f : ow[t * QP + d] * fast_sigmoid(g[u]);
+      }
+    }
+  }
+}
+
 // Tile data for one 16-key tile, prefetched into registers: finished K rows
-// from the prep workspace (16-byte loads) and the V columns (16-byte loads
-// along tokens when VEC, else element loads). LDS holds K as [key][d] and V
-// as [d][key], V's layout in global memory.
+// from the prep workspace and V columns, all 16-byte buffer loads with a
+// fixed per-lane offset and a scalar tile offset (VEC), or element loads
+// with clamped indices. Keys past L read as 0 (K) or are zeroed at commit
+// (V). LDS holds K as [key][d] and V as [d][key], V's layout in memory.
 template <int HDP, bool VEC>
 struct JeffStage {
   static constexpr int KT = kJeffKeyTile;
   static constexpr int TASKS = KT * HDP / 4;      // 16-byte chunks of K (and of V)
-  static constexpr int KN = (TASKS + 255) / 256;  // K chunks per thread
-  static constexpr int VN = (TASKS + 255) / 256;  // V 4-key groups per thread
-  f32x4 k[KN], v[VN];
+  static constexpr int KN = (TASKS + 255) / 256;  // chunks per thread
+  f32x4 k[KN], v[KN];
+  __amdgpu_buffer_rsrc_t rk, rv;
+  int ok[KN], ov[KN];
 
-  __device__ __forceinline__ void fetch(const float *kp_tile, const float *V, int L, int hd,
-                                        int k0, int tid) {
-    // Unconditional loads with clamped indices (all in flight together);
-    // keys past L and features past hd are zeroed at commit time.
+  __device__ __forceinline__ void init(const float *KP, const float *V, int L, int hd, int tid) {
+    rk = buffer_rsrc(KP, (uint32_t)((size_t)L * HDP * 4));
+    rv = buffer_rsrc(V, (uint32_t)((size_t)hd * L * 4));
 #pragma unroll
     for (int i = 0; i < KN; ++i) {
-      const int e = min(tid + 256 * i, TASKS - 1);  // chunk of the contiguous KT x HDP tile
-      const int kk = min((4 * e) / HDP, L - 1 - k0);
-      k[i] = reinterpret_cast<const f32x4 *>(kp_tile)[kk * (HDP / 4) + e % (HDP / 4)];
-    }
-#pragma unroll
-    for (int i = 0; i < VN; ++i) {
       const int e = min(tid + 256 * i, TASKS - 1);
-      const int d = min(e / (KT / 4), hd - 1), g = e % (KT / 4);  // feature d, keys k0+4g..+3
-      const float *src = V + (size_t)L * d;
-      const int key = k0 + 4 * g;
-      if (VEC) {
-        v[i] = *reinterpret_cast<const f32x4 *>(src + min(key, L - 4));
-      } else {
+      ok[i] = e * 16;                                  // chunk e of the KT x HDP tile
+      const int d = e / (KT / 4), g = e % (KT / 4);    // feature d, keys 4g .. 4g+3
+      ov[i] = (int)(((size_t)d * L + 4 * g) * 4);
+    }
+  }
+
+  __device__ __forceinline__ void fetch(const float *KP, const float *V, int L, int hd, int k0,
+                                        int tid) {
+    if constexpr (VEC) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) v[i][t] = src[min(key + t, L - 1)];
+      for (int i = 0; i < KN; ++i) {
+        k[i] = buffer_load4(rk, ok[i], k0 * HDP * 4);
+        v[i] = buffer_load4(rv, ov[i], k0 * 4);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < KN; ++i) {
+        const int e = min(tid + 256 * i, TASKS - 1);
+        const int kk = min((4 * e) / HDP, L - 1 - k0);
+        k[i] = reinterpret_cast<const f32x4 *>(KP + (size_t)k0 * HDP)[kk * (HDP / 4) + e % (HDP / 4)];
+        const int d = min(e / (KT / 4), hd - 1), g = e % (KT / 4);
+        const float *src = V + (size_t)L * d;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) v[i][t] = src[min(k0 + 4 * g + t, L - 1)];
       }
     }
   }
 
-  __device__ __forceinline__ int commit(float *Ks, float *Vs, int tid, int k0, int L, int hd) {
-    constexpr int KS = HDP + 4;
-    constexpr int VS = KT + 4;
-    const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
-    int nonfinite = 0;
+  __device__ __forceinline__ void commit(float *Ks, float *Vs, int tid, int k0, int L, int hd) {
+    constexpr int KS = HDP + 4, VS = KT + 4;
+    const bool tail = k0 + KT > L;  // uniform: the row's last, partial tile
 #pragma unroll
     for (int i = 0; i < KN; ++i) {
       const int e = tid + 256 * i;
-      const int kk = (4 * e) / HDP, d = (4 * e) % HDP;
-      if (e < TASKS) *reinterpret_cast<f32x4 *>(&Ks[kk * KS + d]) = k0 + kk < L ? k[i] : z;
-    }
+      if (TASKS % 256 == 0 || e < TASKS) {  // blockDim is 256
+        const int kk = (4 * e) / HDP, dk = (4 * e) % HDP;
+        f32x4 kv = k[i];
+        const int d = e / (KT / 4), g = e % (KT / 4);
+        f32x4 vv = v[i];
+        if (!VEC || tail) {
 #pragma unroll
-    for (int i = 0; i < VN; ++i) {
-      const int e = tid + 256 * i;
-      const int d = e / (KT / 4), g = e % (KT / 4);
-      if (e >= TASKS) continue;
-      f32x4 x = v[i];
-      const int key = k0 + 4 * g;
-      if (VEC && key + 4 > L) {  // the clamped load was shifted back: realign
-        const int sh = key - (L - 4);
-        f32x4 y = z;
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-          if (t + sh < 4) y[t] = x[t + sh];
-        x = y;
+          for (int t = 0; t < 4; ++t) vv[t] = (d < hd && k0 + 4 * g + t < L) ? vv[t] : 0.0f;
+          if (k0 + kk >= L) kv = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        *reinterpret_cast<f32x4 *>(&Ks[kk * KS + dk]) = kv;
+        *reinterpret_cast<f32x4 *>(&Vs[d * VS + 4 * g]) = vv;
       }
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const bool live = d < hd && key + t < L;
-        const bool fin = __builtin_isfinite(x[t]);
-        nonfinite |= live && !fin;
-        x[t] = (live && fin) ? x[t] : 0.0f;
-      }
-      *reinterpret_cast<f32x4 *>(&Vs[d * VS + 4 * g]) = x;
     }
-    return nonfinite;
   }
 };
+
+template <int HDP, bool VEC>
+__device__ __noinline__ void jeff_redo_wave(const JeffArgs a, const float *__restrict__ kp, int row,
+                                            int head, int q0, int kt_begin, int kt_end, int start,
+                                            float *ws);
 
 template <int HDP, bool VEC>
 __global__ __launch_bounds__(256, 2) void jeff_attention_f32_kernel(const JeffArgs a,
@@ -275,13 +507,11 @@ __global__ __launch_bounds__(256, 2) void jeff_attention_f32_kernel(const JeffAr
   constexpr int KS = HDP + 4;       // K stored [key][d]
   constexpr int VS = KT + 4;        // V stored [d][key]: conflict-free 16-byte reads
   constexpr int KBUF = KT * KS, VBUF = HDP * VS;
-  // K and V double buffers; before the key loop the same bytes hold each
-  // wave's raw Q tile (16 queries x (HDP + 1)) for the Q prep.
-  static_assert(kWavesPerGroup * kJeffWaveQueries * (HDP + 1) <= 2 * (KBUF + VBUF), "Q scratch");
+  constexpr int QP = HDP + 4;       // per-wave Q / output rows before and after the walk
+  static_assert(kWavesPerGroup * kJeffWaveQueries * QP <= 2 * (KBUF + VBUF), "wave rows");
   __shared__ __attribute__((aligned(16))) float smem[2 * (KBUF + VBUF)];
-  float(*Ks)[KBUF] = reinterpret_cast<float(*)[KBUF]>(smem);
-  float(*Vs)[VBUF] = reinterpret_cast<float(*)[VBUF]>(smem + 2 * KBUF);
-  __shared__ int s_span[2];
+  auto Ks = [&](int i) { return smem + i * KBUF; };
+  auto Vs = [&](int i) { return smem + 2 * KBUF + i * VBUF; };
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 15, grp = lane >> 4;
@@ -289,28 +519,24 @@ __global__ __launch_bounds__(256, 2) void jeff_attention_f32_kernel(const JeffAr
   const int row = blockIdx.z;
   const int head = blockIdx.y * hg + wave % hg;
   const int kvh = min(head / a.groups, a.kv_heads - 1);
-  const int L = a.L, hd = a.hd, rh = a.rot_half;
+  const int L = a.L, hd = a.hd;
   const int QT = kJeffWaveQueries * qsubs;
   const int qa = blockIdx.x * QT;
-  const int q = qa + (wave / hg) * kJeffWaveQueries + col;
-  const bool qin = q < L;
+  const int q0 = qa + (wave / hg) * kJeffWaveQueries;
+  const int q = q0 + col;
   const float *maskr = a.mask + (size_t)row * L;
   const float *Q = static_cast<const float *>(a.q) + row * a.q_row + (size_t)head * hd * L;
   const float *Gt = static_cast<const float *>(a.gate) + row * a.q_row + (size_t)head * hd * L;
   const float *V = static_cast<const float *>(a.v) + row * a.kv_row + (size_t)kvh * hd * L;
   const float *KP = kp + ((size_t)row * a.kv_heads + kvh) * L * HDP;
   float *OUT = a.out + row * a.q_row + (size_t)head * hd * L;
-  const bool rope = a.cos_t != nullptr && rh > 0;
+  float *qw = smem + wave * (kJeffWaveQueries * QP);
 
-  // -------- active-key span; RoPE positions restart at `start` when trimming
-  if (tid == 0) {
-    s_span[0] = 0x7fffffff;
-    s_span[1] = -1;
-  }
-  __syncthreads();
-  scan_active(maskr, L, tid, lane, s_span);
-  __syncthreads();
-  const int first = s_span[0], last = s_span[1];
+  // -------- active-key span (each wave on its own); RoPE positions restart
+  // at `start` when trimming. Tiles past the group's last query are causal-
+  // ly dead.
+  int first, last;
+  wave_active_span(maskr, L, lane, first, last);
   const int start = (a.trim && last >= 0) ? first : 0;
   int kt_begin = 0, kt_end = 0;
   {
@@ -320,81 +546,19 @@ __global__ __launch_bounds__(256, 2) void jeff_attention_f32_kernel(const JeffAr
       kt_end = kl / KT + 1;
     }
   }
+  const bool q_live = q < L && q >= start;
 
-  // -------- Q: RMSNorm + partial RoPE into registers, in wave-local LDS
-  // phases (raw, normalized in place, rotated pairs) so that no long chain
-  // of global loads is in flight beside the registers the key loop needs.
-  // Lane (col, grp) ends with Qn[q][grp*QS + s], the B operand of step s.
   float qreg[QS];
-  const bool q_live = qin && q >= start;
-  {
-    constexpr int QP = HDP + 1;
-    float *qw = smem + wave * (kJeffWaveQueries * QP);
-    float *qs = qw + col * QP;
-    float ss = 0.0f;
-    const int qc = q_live ? q : 0;
-#pragma unroll
-    for (int s = 0; s < QS; ++s) {  // clamped, unconditional loads batch together
-      const int d = grp * QS + s;
-      const float x = Q[qc + (size_t)L * (d < hd ? d : hd - 1)];
-      const float y = (q_live && d < hd) ? x : 0.0f;
-      qs[d] = y;
-      ss += y * y;
-    }
-    ss += __shfl_xor(ss, 16);
-    ss += __shfl_xor(ss, 32);
-    const float scale = rms_scale(ss, hd, a.eps);
-#pragma unroll 16
-    for (int s = 0; s < QS; ++s) {
-      const int d = grp * QS + s;
-      const float wq = a.q_norm[min(d, hd - 1)];
-      const float y = rms_apply(qs[d], scale, wq);
-      qs[d] = d < hd ? y : 0.0f;
-    }
-    if (rope) {
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      const int q0 = qa + (wave / hg) * kJeffWaveQueries;
-      for (int e0 = 0; e0 < kJeffWaveQueries * rh; e0 += 64 * 8) {
-        float c[8], sn[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {  // clamped table loads, all in flight
-          const int e = min(e0 + lane + 64 * u, kJeffWaveQueries * rh - 1);
-          const int qi = e / rh, i = e - qi * rh;
-          const int pos = min(max(q0 + qi - start, 0), L - 1);
-          c[u] = a.cos_t[(size_t)pos * rh + i];
-          sn[u] = a.sin_t[(size_t)pos * rh + i];
-        }
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const int e = e0 + lane + 64 * u;
-          const int qi = e / rh, i = e - qi * rh;
-          const int qq = q0 + qi;
-          if (e < kJeffWaveQueries * rh && qq < L && qq >= start) {
-            const float x = qw[qi * QP + i], y = qw[qi * QP + i + rh];
-            qw[qi * QP + i] = rope_lo(x, y, c[u], sn[u]);
-            qw[qi * QP + i + rh] = rope_hi(x, y, c[u], sn[u]);
-          }
-        }
-      }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-    for (int s = 0; s < QS; ++s) qreg[s] = qs[grp * QS + s];
-  }
-  __syncthreads();  // the Q scratch becomes the K/V buffers
+  jeff_q_prep<HDP, VEC>(a, Q, q0, start, qw, qreg);
+  __syncthreads();  // the wave rows become the K/V buffers
 
   // Keep word for a 16-key tile: active key, key >= start, causal key <= query.
   // The mask value is fetched one tile ahead (mask_of) and turned into the
-  // word (keep_word) only when that tile comes up, so no wait on it stalls
-  // the tile prefetch issued next to it.
-  auto mask_of = [&](int kt) -> float { return maskr[min(kt * KT + (lane & 15), L - 1)]; };
+  // word (keep_word) only after that tile's barrier.
+  auto mask_of = [&](int kt) -> float { return maskr[min(kt * KT + col, L - 1)]; };
   auto keep_word = [&](int kt, float mv) -> uint32_t {
     const int k0 = kt * KT;
-    const int kc = k0 + (lane & 15);
+    const int kc = k0 + col;
     const bool act = kc < L && kc >= start && mv != 0.0f;
     const uint32_t abits = (uint32_t)__ballot(act) & 0xffffu;
     return q_live ? (abits & range_bits(0, q - k0)) : 0u;
@@ -405,32 +569,35 @@ __global__ __launch_bounds__(256, 2) void jeff_attention_f32_kernel(const JeffAr
   for (int j = 0; j < NB; ++j)
 #pragma unroll
     for (int r = 0; r < 4; ++r) O[j][r] = 0.0f;
-  float m = -INFINITY, l = 0.0f;
+  float m = kNoMax, l = 0.0f;
+  const float c1 = a.c1;
 
+  // -------- the walk (see the Laya kernel for the scheme): tile kt+1 is
+  // fetched before the products of tile kt and committed after them; one
+  // barrier per tile; lazily moved exponent reference; a wave whose kept
+  // scores sum to NaN or inf stops computing, and it or a wave whose O took
+  // a NaN or inf redoes its queries with the reference's exact semantics.
   JeffStage<HDP, VEC> st;
-  int nonfinite = 0;
+  st.init(KP, V, L, hd, tid);
   uint32_t w = 0u;
   float m_next = 0.0f;
   if (kt_begin < kt_end) {
     const float m0 = mask_of(kt_begin);
-    st.fetch(KP + (size_t)kt_begin * KT * HDP, V, L, hd, kt_begin * KT, tid);
-    nonfinite = st.commit(Ks[0], Vs[0], tid, kt_begin * KT, L, hd);
+    st.fetch(KP, V, L, hd, kt_begin * KT, tid);
+    st.commit(Ks(0), Vs(0), tid, kt_begin * KT, L, hd);
     w = keep_word(kt_begin, m0);
   }
-  int nf = __syncthreads_or(nonfinite);
-  int any_nf = 0;  // workgroup-uniform: some staged V value was NaN or inf
-
+  __syncthreads();
+  bool tainted = false;  // wave-uniform
+  int cur = 0;
   for (int kt = kt_begin; kt < kt_end; ++kt) {
-    const int cur = (kt - kt_begin) & 1;
     const bool more = kt + 1 < kt_end;
     if (more) {
       m_next = mask_of(kt + 1);
-      st.fetch(KP + (size_t)(kt + 1) * KT * HDP, V, L, hd, (kt + 1) * KT, tid);
+      st.fetch(KP, V, L, hd, (kt + 1) * KT, tid);
     }
-    const float *Kc = Ks[cur];
-    const float *Vc = Vs[cur];
-
-    if (__ballot(w != 0u) != 0) {
+    if (!tainted && __ballot(w != 0u) != 0) {
+      const float *Kc = Ks(cur);
       f32x4 s0, s1;  // two partial sums over alternate chunks of hd
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -448,108 +615,170 @@ __global__ __launch_bounds__(256, 2) void jeff_attention_f32_kernel(const JeffAr
 #pragma unroll
           for (int e = 0; e < 4; ++e) s0 = mfma_16x16x4(ka[e], qreg[4 * c + e], s0);
         }
-        if ((c & 3) == 3) __builtin_amdgcn_sched_barrier(0);
       }
       s0 += s1;
-      // masked softmax over the 16 keys (lane group g holds keys 4g + r)
-      float mx = -INFINITY;
+      // lane group g holds keys 4g + r of its query
+      if (__ballot(q_live && w != 0xffffu) != 0) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float x = ((w >> (4 * grp + r)) & 1u) ? s0[r] * a.c1 : -INFINITY;
-        s0[r] = x;
-        mx = fmaxf(mx, x);
+        for (int r = 0; r < 4; ++r) s0[r] = ((w >> (4 * grp + r)) & 1u) ? s0[r] : -INFINITY;
       }
+      float mx = fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3]));
       mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float mn = fmaxf(m, mx);
-      const float alpha = (m == mn) ? 1.0f : fast_exp2(m - mn);
+      mx = pair_max(mx);
+      const float mxs = mx * c1;
+      const bool need = mxs > m + kRescaleSlack;
+      const float mn = need ? mxs : m;
       float rs = 0.0f;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float e = __builtin_isfinite(s0[r]) ? fast_exp2(s0[r] - mn) : 0.0f;
-        s0[r] = e;
-        rs += e;
+        s0[r] = fast_exp2(__builtin_fmaf(s0[r], c1, -mn));
+        rs += s0[r];
       }
-      l = l * alpha + rs;
-      m = mn;
-      if (alpha != 1.0f) {
+      if (__ballot(q_live && !__builtin_isfinite(rs)) != 0) {
+        tainted = true;
+      } else {
+        if (__ballot(need) != 0) {
+          const float alpha = fast_exp2(m - mn);  // exactly 1 where the reference stays
 #pragma unroll
-        for (int j = 0; j < NB; ++j) O[j] *= alpha;
-      }
-      // V tiles are staged with NaN/inf replaced by 0, so this product is
-      // the exact sum over the finite values; the non-finite ones are folded
-      // in after the key loop.
-      // A operand of block j: V[key 4*grp + r][d = 16*j + col], one 16-byte read.
-      const float *v0 = &Vc[col * VS + 4 * grp];
+          for (int j = 0; j < NB; ++j) O[j] *= alpha;
+          l *= alpha;
+        }
+        l += rs;
+        m = mn;
+        // A operand of block j: V[key 4*grp + r][d = 16*j + col], one 16-byte read.
+        const float *v0 = &Vs(cur)[col * VS + 4 * grp];
 #pragma unroll
-      for (int j = 0; j < NB; ++j) {
-        const f32x4 vv = *reinterpret_cast<const f32x4 *>(v0 + j * 16 * VS);
+        for (int j = 0; j < NB; ++j) {
+          const f32x4 vv = *reinterpret_cast<const f32x4 *>(v0 + j * 16 * VS);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) O[j] = mfma_16x16x4(vv[r], s0[r], O[j]);
-        if ((j & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+          for (int r = 0; r < 4; ++r) O[j] = mfma_16x16x4(vv[r], s0[r], O[j]);
+        }
       }
     }
-    any_nf |= nf;
-    nonfinite = 0;
-    if (more) nonfinite = st.commit(Ks[cur ^ 1], Vs[cur ^ 1], tid, (kt + 1) * KT, L, hd);
-    nf = __syncthreads_or(nonfinite);
+    if (more) st.commit(Ks(cur ^ 1), Vs(cur ^ 1), tid, (kt + 1) * KT, L, hd);
+    __syncthreads();
     if (more) w = keep_word(kt + 1, m_next);
+    cur ^= 1;
   }
 
-  // -------- non-finite values of kept keys (rare): o = sum p*v over p != 0
-  // (lib.rs:746-748) is +-inf or NaN wherever such a value is kept. A kept
-  // key's p is never 0 here: q and k are RMS-normalized, so |score| stays
-  // far from exp's underflow. Flags per output: bit 0 NaN, 1 +inf, 2 -inf.
-  uint32_t special[NB];
+  // -------- careful redo (rare), out of line; every wave's LDS reads of the
+  // walk precede its last barrier, so each wave may now use its own rows.
+  bool bad = false;
 #pragma unroll
-  for (int j = 0; j < NB; ++j) special[j] = 0u;
-  if (any_nf) {
-    const int k_lo = kt_begin * KT, k_hi = min(kt_end * KT, L);
+  for (int j = 0; j < NB; ++j)
 #pragma unroll
-    for (int j = 0; j < NB; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int d = j * 16 + 4 * grp + r;
-        uint32_t f = 0u;
-        if (q_live && d < hd) {
-#pragma nounroll
-          for (int k = k_lo; k < k_hi && k <= q; ++k) {
-            if (k < start || maskr[k] == 0.0f) continue;
-            const float v = V[k + (size_t)L * d];
-            if (!__builtin_isfinite(v)) f |= __builtin_isnan(v) ? 1u : (v > 0.0f ? 2u : 4u);
-          }
-        }
-        special[j] |= f << (8 * r);
-      }
+    for (int r = 0; r < 4; ++r) bad |= !__builtin_isfinite(O[j][r]);
+  if (tainted || __ballot(q_live && bad) != 0) {
+    jeff_redo_wave<HDP, VEC>(a, kp, row, head, q0, kt_begin, kt_end, start, qw);
+    return;
   }
 
   // -------- o / sum (0 when nothing was kept), sigmoid gate, store
   float lt = l + __shfl_xor(l, 16);
-  lt += __shfl_xor(lt, 32);
+  lt = pair_sum(lt);
   const float inv = lt > 0.0f ? fast_rcp(lt) : 0.0f;
-  if (qin) {
-    const bool dropped = a.trim && q < start;
-    // Every gate load is issued before any is used (clamped, unconditional),
-    // so the epilogue waits on memory once rather than once per output.
-    f32x4 gv[NB];
+  jeff_store<HDP, VEC>(a, Gt, OUT, q0, start, qw, O, inv);
+}
+
+// The careful path for one wave's 16 queries of one head (rare: NaN or inf
+// among its kept scores or values), from global memory without barriers:
+// the reference's masked softmax with an exact running max (non-finite
+// scores weigh 0, a +inf score empties the row) and o = sum p*v over
+// p != 0 in key order (lib.rs:716-754), then the gate. Kept out of line so
+// that its registers never weigh on the walk. ws: the wave's LDS rows.
+template <int HDP, bool VEC>
+__device__ __noinline__ void jeff_redo_wave(const JeffArgs a, const float *__restrict__ kp, int row,
+                                            int head, int q0, int kt_begin, int kt_end, int start,
+                                            float *ws) {
+  constexpr int KT = kJeffKeyTile, QS = HDP / 4, NB = HDP / 16, PS = KT + 1;
+  const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+  const int L = a.L, hd = a.hd;
+  const int kvh = min(head / a.groups, a.kv_heads - 1);
+  const int q = q0 + col;
+  const bool q_live = q < L && q >= start;
+  const float *maskr = a.mask + (size_t)row * L;
+  const float *Q = static_cast<const float *>(a.q) + row * a.q_row + (size_t)head * hd * L;
+  const float *Gt = static_cast<const float *>(a.gate) + row * a.q_row + (size_t)head * hd * L;
+  const float *V = static_cast<const float *>(a.v) + row * a.kv_row + (size_t)kvh * hd * L;
+  const float *KP = kp + ((size_t)row * a.kv_heads + kvh) * L * HDP;
+  float *OUT = a.out + row * a.q_row + (size_t)head * hd * L;
+  float qreg[QS];
+  jeff_q_prep<HDP, VEC>(a, Q, q0, start, ws, qreg);
+  f32x4 O[NB];
+#pragma unroll
+  for (int j = 0; j < NB; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) O[j][r] = 0.0f;
+  float m = kNoMax, l = 0.0f;
+  float *Pw = ws;  // 16 keys x 17 floats, after the Q rows are consumed
+#pragma unroll 1
+  for (int kt = kt_begin; kt < kt_end; ++kt) {
+    const int k0 = kt * KT;
+    const int kc = k0 + col;
+    const bool act = kc < L && kc >= start && maskr[min(kc, L - 1)] != 0.0f;
+    const uint32_t abits = (uint32_t)__ballot(act) & 0xffffu;
+    const uint32_t w = q_live ? (abits & range_bits(0, q - k0)) : 0u;
+    if (__ballot(w != 0u) == 0) continue;
+    const float *krow = KP + (size_t)min(kc, L - 1) * HDP + grp * QS;
+    f32x4 s;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s[r] = 0.0f;
+#pragma unroll
+    for (int x = 0; x < QS; ++x) s = mfma_16x16x4(kc < L ? krow[x] : 0.0f, qreg[x], s);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float x = ((w >> (4 * grp + r)) & 1u) ? s[r] * a.c1 : -INFINITY;
+      s[r] = x;
+      mx = fmaxf(mx, x);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = pair_max(mx);
+    const float mn = fmaxf(m, mx);
+    const float alpha = (m == mn) ? 1.0f : fast_exp2(m - mn);
+    float rs = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float e = __builtin_isfinite(s[r]) ? fast_exp2(s[r] - mn) : 0.0f;
+      s[r] = e;
+      rs += e;
+    }
+    l = l * alpha + rs;
+    m = mn;
+    // alpha == 0: earlier probabilities are 0 against the new max, so their
+    // (possibly infinite) values drop out as in the reference.
 #pragma unroll
     for (int j = 0; j < NB; ++j)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int d = j * 16 + 4 * grp + r;
-        gv[j][r] = Gt[q + (size_t)L * (d < hd ? d : hd - 1)];
-      }
+      for (int r = 0; r < 4; ++r) O[j][r] = alpha == 0.0f ? 0.0f : O[j][r] * alpha;
+    __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int j = 0; j < NB; ++j)
+    for (int r = 0; r < 4; ++r) Pw[(4 * grp + r) * PS + col] = s[r];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll 1
+    for (int kk = 0; kk < KT; ++kk) {
+      const float pk = Pw[kk * PS + col];
+      if (pk == 0.0f) continue;  // only kept keys inside the row get here
+      const float *vcol = V + (k0 + kk);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int d = j * 16 + 4 * grp + r;
-        float o = O[j][r] * inv;
-        const uint32_t f = (special[j] >> (8 * r)) & 7u;
-        if (f) o = ((f & 1u) || f == 6u) ? __builtin_nanf("") : (f == 2u ? INFINITY : -INFINITY);
-        if (d < hd) OUT[q + (size_t)L * d] = dropped ? 0.0f : o * fast_sigmoid(gv[j][r]);
-      }
+      for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int d = 16 * j + 4 * grp + r;
+          if (d < hd) O[j][r] += pk * vcol[(size_t)L * d];
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
   }
+  float lt = l + __shfl_xor(l, 16);
+  lt = pair_sum(lt);
+  const float inv = lt > 0.0f ? fast_rcp(lt) : 0.0f;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  jeff_store<HDP, VEC>(a, Gt, OUT, q0, start, ws, O, inv);
 }
 
 // ---------------------------------------------------------- bf16 attention
@@ -905,8 +1134,13 @@ static hipError_t launch_jeff_f32_hd(const JeffArgs &a, int rows, float *kp, hip
   const int qsubs = kWavesPerGroup / a.heads_per_group;
   const int qt = kJeffWaveQueries * qsubs;
   dim3 grid((a.L + qt - 1) / qt, a.heads / a.heads_per_group, rows);
-  // 16-byte V loads along tokens need L % 4 == 0 and an aligned base.
-  const bool vec = a.L % 4 == 0 && (reinterpret_cast<uintptr_t>(a.v) & 15) == 0;
+  // 16-byte accesses along tokens need L % 4 == 0 and aligned bases; buffer
+  // offsets need one head's (hd, L) block and one kv head's K rows within
+  // 2 GiB.
+  const uintptr_t bases = reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.v) |
+                          reinterpret_cast<uintptr_t>(a.gate) | reinterpret_cast<uintptr_t>(a.out);
+  const bool vec = a.L % 4 == 0 && (bases & 15) == 0 &&
+                   (size_t)a.L * (size_t)HDP * 4 < ((size_t)1 << 31);
   if (vec)
     hipLaunchKernelGGL((jeff_attention_f32_kernel<HDP, true>), grid, dim3(256), 0, stream, a, kp);
   else

@@ -88,19 +88,6 @@ __device__ __forceinline__ f32x4 rot_hi(f32x4 x, f32x4 y, f32x4 c, f32x4 s) {
   return x * s + y * c;
 }
 
-// Raw buffer loads through an SGPR resource: the per-lane byte offset is
-// fixed for the whole walk, the tile base is a scalar offset, and any byte
-// at or past `bytes` reads as 0 (the hardware range check), so keys past the
-// row's end need no clamping or selects.
-constexpr int kBufferWord3 = 0x00020000;  // gfx9 raw buffer (no format, no swizzle)
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
-                                           kBufferWord3);
-}
-__device__ __forceinline__ f32x4 buffer_load4(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
-  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
-}
-
 // One K/V tile's global data held in registers between the prefetch (issued
 // before the previous tile's products) and the LDS commit (after them).
 //

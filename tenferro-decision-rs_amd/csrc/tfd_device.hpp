@@ -90,6 +90,23 @@ constexpr float kRescaleSlack = 8.0f;
 // Initial reference: finite, so exp2(fma(-inf, c1, -m)) is exp2(-inf) = 0.
 constexpr float kNoMax = -3.402823466e38f;
 
+// Raw buffer access through an SGPR resource: the per-lane byte offset can
+// stay fixed for a whole walk, the tile base is a scalar offset, and any byte
+// at or past `bytes` reads as 0 (stores there are dropped) by the hardware
+// range check.
+constexpr int kBufferWord3 = 0x00020000;  // gfx9 raw buffer (no format, no swizzle)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
+                                           kBufferWord3);
+}
+__device__ __forceinline__ f32x4 buffer_load4(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+__device__ __forceinline__ void buffer_store4(f32x4 v, __amdgpu_buffer_rsrc_t r, int voff,
+                                              int soff) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, v), r, voff, soff, 0);
+}
+
 __device__ __forceinline__ int wave_min(int v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o));
