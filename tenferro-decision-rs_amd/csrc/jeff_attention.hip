@@ -121,7 +121,7 @@ template <int HDP, typename OutT>
 __global__ __launch_bounds__(256) void jeff_k_prep_kernel(const JeffArgs a, OutT *__restrict__ kp) {
   constexpr int DP = HDP / 8;  // dims per thread: 8 threads per key
   constexpr int KS = HDP + 1;
-  constexpr int RT = (kKeyTile * (HDP / 2) + 255) / 256;  // RoPE pairs per thread, at most
+  constexpr int RT = (HDP / 2 + 7) / 8;  // RoPE pairs per thread, at most
   __shared__ float Kt[kKeyTile * KS];
   __shared__ float s_red[8 * kKeyTile];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -146,14 +146,14 @@ __global__ __launch_bounds__(256) void jeff_k_prep_kernel(const JeffArgs a, OutT
                : static_cast<const float *>(a.k)[at];
     wn[i] = a.k_norm[dc];
   }
+  // Thread (kk, part) rotates pairs i = part, part + 8, ... of key k0 + kk.
+  const size_t pos = (size_t)min(max(key - start, 0), L - 1) * rh;
   if (rope) {
 #pragma unroll
     for (int u = 0; u < RT; ++u) {
-      const int e = min(tid + 256 * u, kKeyTile * rh - 1);
-      const int k2 = e / rh, i = e - k2 * rh;
-      const int pos = min(max(k0 + k2 - start, 0), L - 1);
-      c[u] = a.cos_t[(size_t)pos * rh + i];
-      sn[u] = a.sin_t[(size_t)pos * rh + i];
+      const int i = min(part + 8 * u, rh - 1);
+      c[u] = a.cos_t[pos + i];
+      sn[u] = a.sin_t[pos + i];
     }
   }
   float ss = 0.0f;
@@ -180,12 +180,11 @@ __global__ __launch_bounds__(256) void jeff_k_prep_kernel(const JeffArgs a, OutT
     __syncthreads();
 #pragma unroll
     for (int u = 0; u < RT; ++u) {
-      const int e = tid + 256 * u;
-      const int k2 = e / rh, i = e - k2 * rh;
-      if (e < kKeyTile * rh && k0 + k2 < L) {
-        const float x = Kt[k2 * KS + i], y = Kt[k2 * KS + i + rh];
-        Kt[k2 * KS + i] = rope_lo(x, y, c[u], sn[u]);
-        Kt[k2 * KS + i + rh] = rope_hi(x, y, c[u], sn[u]);
+      const int i = part + 8 * u;
+      if (i < rh && kin) {
+        const float x = Kt[kk * KS + i], y = Kt[kk * KS + i + rh];
+        Kt[kk * KS + i] = rope_lo(x, y, c[u], sn[u]);
+        Kt[kk * KS + i + rh] = rope_hi(x, y, c[u], sn[u]);
       }
     }
   }
@@ -298,17 +297,11 @@ __device__ __forceinline__ void jeff_q_prep(const JeffArgs &a, const float *Q, i
     xv[c] = *reinterpret_cast<const f32x4 *>(qs + 4 * c);
     ss += xv[c][0] * xv[c][0] + xv[c][1] * xv[c][1] + xv[c][2] * xv[c][2] + xv[c][3] * xv[c][3];
   }
-  // norm weights: 16-byte loads of this lane's QS dims (clamped past hd)
+  // norm weights of this lane's QS dims: buffer loads (past hd they read 0
+  // or anything; those dims are zeroed below)
+  const __amdgpu_buffer_rsrc_t rn = buffer_rsrc(a.q_norm, (uint32_t)(hd * 4));
 #pragma unroll
-  for (int c = 0; c < QS / 4; ++c) {
-    const int d = grp * QS + 4 * c;
-    if (d + 3 < hd) {
-      wv[c] = *reinterpret_cast<const f32x4 *>(a.q_norm + d);
-    } else {
-#pragma unroll
-      for (int t = 0; t < 4; ++t) wv[c][t] = a.q_norm[min(d + t, hd - 1)];
-    }
-  }
+  for (int c = 0; c < QS / 4; ++c) wv[c] = buffer_load4(rn, (grp * QS + 4 * c) * 4, 0);
   ss += __shfl_xor(ss, 16);
   ss += pair_sum(ss) - ss;  // lanes l and l ^ 32 hold the other two groups
   const float scale = rms_scale(ss, hd, a.eps);
@@ -326,25 +319,26 @@ __device__ __forceinline__ void jeff_q_prep(const JeffArgs &a, const float *Q, i
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    for (int e0 = 0; e0 < 16 * rh; e0 += 64 * 8) {
-      float c[8], sn[8];
+    // Lane (col, grp) rotates pairs i = grp, grp + 4, ... of query q0 + col.
+    if (q_live) {
+      const size_t pos = (size_t)(q - start) * rh;
+      float *qr = qw + col * QP;
+      for (int i0 = grp; i0 < rh; i0 += 4 * 8) {
+        float c[8], sn[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {  // clamped table loads, all in flight
-        const int e = min(e0 + lane + 64 * u, 16 * rh - 1);
-        const int qi = e / rh, i = e - qi * rh;
-        const int pos = min(max(q0 + qi - start, 0), L - 1);
-        c[u] = a.cos_t[(size_t)pos * rh + i];
-        sn[u] = a.sin_t[(size_t)pos * rh + i];
-      }
+        for (int u = 0; u < 8; ++u) {  // clamped table loads, all in flight
+          const int i = min(i0 + 4 * u, rh - 1);
+          c[u] = a.cos_t[pos + i];
+          sn[u] = a.sin_t[pos + i];
+        }
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int e = e0 + lane + 64 * u;
-        const int qi = e / rh, i = e - qi * rh;
-        const int qq = q0 + qi;
-        if (e < 16 * rh && qq < L && qq >= start) {
-          const float x = qw[qi * QP + i], y = qw[qi * QP + i + rh];
-          qw[qi * QP + i] = rope_lo(x, y, c[u], sn[u]);
-          qw[qi * QP + i + rh] = rope_hi(x, y, c[u], sn[u]);
+        for (int u = 0; u < 8; ++u) {
+          const int i = i0 + 4 * u;
+          if (i < rh) {
+            const float x = qr[i], y = qr[i + rh];
+            qr[i] = rope_lo(x, y, c[u], sn[u]);
+            qr[i + rh] = rope_hi(x, y, c[u], sn[u]);
+          }
         }
       }
     }
@@ -427,11 +421,11 @@ __device__ __forceinline__ void jeff_store(const JeffArgs &a, const float *Gt, f
 // fixed per-lane offset and a scalar tile offset (VEC), or element loads
 // with clamped indices. Keys past L read as 0 (K) or are zeroed at commit
 // (V). LDS holds K as [key][d] and V as [d][key], V's layout in memory.
-template <int HDP, bool VEC>
+template <int HDP, bool VEC, int NT>
 struct JeffStage {
   static constexpr int KT = kJeffKeyTile;
-  static constexpr int TASKS = KT * HDP / 4;      // 16-byte chunks of K (and of V)
-  static constexpr int KN = (TASKS + 255) / 256;  // chunks per thread
+  static constexpr int TASKS = KT * HDP / 4;       // 16-byte chunks of K (and of V)
+  static constexpr int KN = (TASKS + NT - 1) / NT;  // chunks per thread (NT threads)
   f32x4 k[KN], v[KN];
   __amdgpu_buffer_rsrc_t rk, rv;
   int ok[KN], ov[KN];
@@ -441,7 +435,7 @@ struct JeffStage {
     rv = buffer_rsrc(V, (uint32_t)((size_t)hd * L * 4));
 #pragma unroll
     for (int i = 0; i < KN; ++i) {
-      const int e = min(tid + 256 * i, TASKS - 1);
+      const int e = min(tid + NT * i, TASKS - 1);
       ok[i] = e * 16;                                  // chunk e of the KT x HDP tile
       const int d = e / (KT / 4), g = e % (KT / 4);    // feature d, keys 4g .. 4g+3
       ov[i] = (int)(((size_t)d * L + 4 * g) * 4);
@@ -459,7 +453,7 @@ struct JeffStage {
     } else {
 #pragma unroll
       for (int i = 0; i < KN; ++i) {
-        const int e = min(tid + 256 * i, TASKS - 1);
+        const int e = min(tid + NT * i, TASKS - 1);
         const int kk = min((4 * e) / HDP, L - 1 - k0);
         k[i] = reinterpret_cast<const f32x4 *>(KP + (size_t)k0 * HDP)[kk * (HDP / 4) + e % (HDP / 4)];
         const int d = min(e / (KT / 4), hd - 1), g = e % (KT / 4);
@@ -475,8 +469,8 @@ struct JeffStage {
     const bool tail = k0 + KT > L;  // uniform: the row's last, partial tile
 #pragma unroll
     for (int i = 0; i < KN; ++i) {
-      const int e = tid + 256 * i;
-      if (TASKS % 256 == 0 || e < TASKS) {  // blockDim is 256
+      const int e = tid + NT * i;
+      if (TASKS % NT == 0 || e < TASKS) {  // blockDim is NT
         const int kk = (4 * e) / HDP, dk = (4 * e) % HDP;
         f32x4 kv = k[i];
         const int d = e / (KT / 4), g = e % (KT / 4);
@@ -498,9 +492,15 @@ __device__ __noinline__ void jeff_redo_wave(const JeffArgs a, const float *__res
                                             int head, int q0, int kt_begin, int kt_end, int start,
                                             float *ws);
 
+// One workgroup = 8 wavefronts (one workgroup per CU) sharing one kv head:
+// hg = heads_per_group query heads x (8 / hg) query tiles of 16. The query
+// tiles come in causal pairs (p, n - 1 - p), n = ceil(L / 16), so every
+// workgroup carries about the same number of key tiles; the walk covers the
+// group's span and a wave skips the tiles its own queries do not reach.
 template <int HDP, bool VEC>
-__global__ __launch_bounds__(256, 2) void jeff_attention_f32_kernel(const JeffArgs a,
-                                                                    const float *__restrict__ kp) {
+__global__ __launch_bounds__(kJeffF32Waves * 64, 1) void jeff_attention_f32_kernel(
+    const JeffArgs a, const float *__restrict__ kp) {
+  constexpr int NT = kJeffF32Waves * 64;
   constexpr int KT = kJeffKeyTile;  // 16 keys per tile
   constexpr int QS = HDP / 4;       // Q registers per lane (4 lane groups split hd)
   constexpr int NB = HDP / 16;      // 16-row blocks of O^T
@@ -508,22 +508,31 @@ __global__ __launch_bounds__(256, 2) void jeff_attention_f32_kernel(const JeffAr
   constexpr int VS = KT + 4;        // V stored [d][key]: conflict-free 16-byte reads
   constexpr int KBUF = KT * KS, VBUF = HDP * VS;
   constexpr int QP = HDP + 4;       // per-wave Q / output rows before and after the walk
-  static_assert(kWavesPerGroup * kJeffWaveQueries * QP <= 2 * (KBUF + VBUF), "wave rows");
-  __shared__ __attribute__((aligned(16))) float smem[2 * (KBUF + VBUF)];
+  constexpr int WROWS = kJeffF32Waves * kJeffWaveQueries * QP;
+  constexpr int SMEM = WROWS > 2 * (KBUF + VBUF) ? WROWS : 2 * (KBUF + VBUF);
+  __shared__ __attribute__((aligned(16))) float smem[SMEM];
   auto Ks = [&](int i) { return smem + i * KBUF; };
   auto Vs = [&](int i) { return smem + 2 * KBUF + i * VBUF; };
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform, in a scalar register
   const int col = lane & 15, grp = lane >> 4;
-  const int hg = a.heads_per_group, qsubs = kWavesPerGroup / hg;
+  const int hg = a.heads_per_group, S = kJeffF32Waves / hg;  // query tiles per workgroup
   const int row = blockIdx.z;
   const int head = blockIdx.y * hg + wave % hg;
   const int kvh = min(head / a.groups, a.kv_heads - 1);
   const int L = a.L, hd = a.hd;
-  const int QT = kJeffWaveQueries * qsubs;
-  const int qa = blockIdx.x * QT;
-  const int q0 = qa + (wave / hg) * kJeffWaveQueries;
+  const int nq = (L + kJeffWaveQueries - 1) / kJeffWaveQueries;
+  const int npairs = (nq + 1) / 2;
+  const int s_idx = wave / hg, pair = blockIdx.x * (S / 2) + s_idx / 2;
+  const bool hi_member = s_idx & 1;
+  const int qtile = hi_member ? nq - 1 - pair : pair;
+  // a wave with no query tile (past the pairs, or the middle tile's twin)
+  const bool wave_live = pair < npairs && (!hi_member || nq - 1 - pair != pair);
+  const int q0 = qtile * kJeffWaveQueries;
   const int q = q0 + col;
+  // the group's last query: the upper member of its lowest pair
+  const int q_last = min((nq - (int)blockIdx.x * (S / 2)) * kJeffWaveQueries, L) - 1;
   const float *maskr = a.mask + (size_t)row * L;
   const float *Q = static_cast<const float *>(a.q) + row * a.q_row + (size_t)head * hd * L;
   const float *Gt = static_cast<const float *>(a.gate) + row * a.q_row + (size_t)head * hd * L;
@@ -540,16 +549,16 @@ __global__ __launch_bounds__(256, 2) void jeff_attention_f32_kernel(const JeffAr
   const int start = (a.trim && last >= 0) ? first : 0;
   int kt_begin = 0, kt_end = 0;
   {
-    const int kl = min(last, min(qa + QT, L) - 1);
+    const int kl = min(last, q_last);
     if (last >= 0 && first <= kl) {
       kt_begin = first / KT;
       kt_end = kl / KT + 1;
     }
   }
-  const bool q_live = q < L && q >= start;
+  const bool q_live = wave_live && q < L && q >= start;
 
   float qreg[QS];
-  jeff_q_prep<HDP, VEC>(a, Q, q0, start, qw, qreg);
+  jeff_q_prep<HDP, VEC>(a, Q, wave_live ? q0 : 0, start, qw, qreg);
   __syncthreads();  // the wave rows become the K/V buffers
 
   // Keep word for a 16-key tile: active key, key >= start, causal key <= query.
@@ -577,7 +586,7 @@ __global__ __launch_bounds__(256, 2) void jeff_attention_f32_kernel(const JeffAr
   // barrier per tile; lazily moved exponent reference; a wave whose kept
   // scores sum to NaN or inf stops computing, and it or a wave whose O took
   // a NaN or inf redoes its queries with the reference's exact semantics.
-  JeffStage<HDP, VEC> st;
+  JeffStage<HDP, VEC, NT> st;
   st.init(KP, V, L, hd, tid);
   uint32_t w = 0u;
   float m_next = 0.0f;
@@ -668,6 +677,7 @@ __global__ __launch_bounds__(256, 2) void jeff_attention_f32_kernel(const JeffAr
   for (int j = 0; j < NB; ++j)
 #pragma unroll
     for (int r = 0; r < 4; ++r) bad |= !__builtin_isfinite(O[j][r]);
+  if (!wave_live) return;
   if (tainted || __ballot(q_live && bad) != 0) {
     jeff_redo_wave<HDP, VEC>(a, kp, row, head, q0, kt_begin, kt_end, start, qw);
     return;
@@ -879,7 +889,8 @@ __global__ __launch_bounds__(256, 2) void jeff_attention_bf16_kernel(const JeffA
   float *const qscr = reinterpret_cast<float *>(smem_raw);
   __shared__ int s_span[2];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform, in a scalar register
   const int col = lane & 15, grp = lane >> 4;
   const int hg = a.heads_per_group, qsubs = kWavesPerGroup / hg;
   const int row = blockIdx.z;
@@ -1131,9 +1142,12 @@ static hipError_t launch_jeff_f32_hd(const JeffArgs &a, int rows, float *kp, hip
   hipLaunchKernelGGL((jeff_k_prep_kernel<HDP, float>), pgrid, dim3(256), 0, stream, a, kp);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int qsubs = kWavesPerGroup / a.heads_per_group;
-  const int qt = kJeffWaveQueries * qsubs;
-  dim3 grid((a.L + qt - 1) / qt, a.heads / a.heads_per_group, rows);
+  // Query tiles of 16 in causal pairs, kJeffF32Waves / heads_per_group tiles
+  // (half as many pairs) per workgroup.
+  const int nq = (a.L + kJeffWaveQueries - 1) / kJeffWaveQueries;
+  const int pairs_per_group = kJeffF32Waves / a.heads_per_group / 2;
+  const int npairs = (nq + 1) / 2;
+  dim3 grid((npairs + pairs_per_group - 1) / pairs_per_group, a.heads / a.heads_per_group, rows);
   // 16-byte accesses along tokens need L % 4 == 0 and aligned bases; buffer
   // offsets need one head's (hd, L) block and one kv head's K rows within
   // 2 GiB.
@@ -1141,10 +1155,11 @@ static hipError_t launch_jeff_f32_hd(const JeffArgs &a, int rows, float *kp, hip
                           reinterpret_cast<uintptr_t>(a.gate) | reinterpret_cast<uintptr_t>(a.out);
   const bool vec = a.L % 4 == 0 && (bases & 15) == 0 &&
                    (size_t)a.L * (size_t)HDP * 4 < ((size_t)1 << 31);
+  const dim3 block(kJeffF32Waves * 64);
   if (vec)
-    hipLaunchKernelGGL((jeff_attention_f32_kernel<HDP, true>), grid, dim3(256), 0, stream, a, kp);
+    hipLaunchKernelGGL((jeff_attention_f32_kernel<HDP, true>), grid, block, 0, stream, a, kp);
   else
-    hipLaunchKernelGGL((jeff_attention_f32_kernel<HDP, false>), grid, dim3(256), 0, stream, a, kp);
+    hipLaunchKernelGGL((jeff_attention_f32_kernel<HDP, false>), grid, block, 0, stream, a, kp);
   return hipGetLastError();
 }
 

@@ -329,7 +329,8 @@ __global__ __launch_bounds__(256, laya_groups_per_cu<HDP>()) void laya_attention
   auto Ks = [&](int i) { return smem + i * (kKeyTile * KS); };
   auto Vs = [&](int i) { return smem + 2 * kKeyTile * KS + i * (kKeyTile * VS); };
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform, in a scalar register
   const int col = lane & 31, half = lane >> 5;
   const int head = blockIdx.y, b = blockIdx.z;
   const int L = a.L, hd = a.hd, hh = a.half, nkt = a.nkt;

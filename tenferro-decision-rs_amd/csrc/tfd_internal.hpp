@@ -15,6 +15,7 @@ constexpr int kWaveQueries = 32;
 constexpr int kWavesPerGroup = 4;   // 256 threads per workgroup
 constexpr int kLayaGroupQueries = kWaveQueries * kWavesPerGroup;
 constexpr int kJeffWaveQueries = 16;  // Jeff waves use the 16x16x4 MFMA
+constexpr int kJeffF32Waves = 8;      // Jeff f32 workgroup: 512 threads, one per CU
 constexpr int kJeffKeyTile = 16;      // keys per Jeff f32 tile
 
 enum LayaMaskMode : int {
