@@ -250,6 +250,24 @@ __device__ __forceinline__ void jeff_q_prep(const JeffArgs &a, const float *Q, i
   const int L = a.L, hd = a.hd, rh = a.rot_half;
   const int q = q0 + col;
   const bool q_live = q < L && q >= start;
+  // Issued first, so that they share the Q loads' round trip: this lane's
+  // norm weights (past hd they read 0 or anything; those dims are zeroed
+  // below) and the table entries of its first 8 RoPE pairs i = grp + 4u.
+  const __amdgpu_buffer_rsrc_t rn = buffer_rsrc(a.q_norm, (uint32_t)(hd * 4));
+  f32x4 wv[QS / 4];
+#pragma unroll
+  for (int c = 0; c < QS / 4; ++c) wv[c] = buffer_load4(rn, (grp * QS + 4 * c) * 4, 0);
+  const bool rope = a.cos_t != nullptr && rh > 0;
+  const size_t pos = (size_t)min(max(q - start, 0), L - 1) * rh;
+  float c8[8], s8[8];
+  if (rope) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = min(grp + 4 * u, rh - 1);
+      c8[u] = a.cos_t[pos + i];
+      s8[u] = a.sin_t[pos + i];
+    }
+  }
   if constexpr (VEC) {
     // Task (d, g): queries q0 + 4g .. +3 of feature d, one 16-byte load;
     // features past hd read as 0.
@@ -290,18 +308,13 @@ __device__ __forceinline__ void jeff_q_prep(const JeffArgs &a, const float *Q, i
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   float *qs = qw + col * QP + grp * QS;
-  f32x4 xv[QS / 4], wv[QS / 4];
+  f32x4 xv[QS / 4];
   float ss = 0.0f;
 #pragma unroll
   for (int c = 0; c < QS / 4; ++c) {
     xv[c] = *reinterpret_cast<const f32x4 *>(qs + 4 * c);
     ss += xv[c][0] * xv[c][0] + xv[c][1] * xv[c][1] + xv[c][2] * xv[c][2] + xv[c][3] * xv[c][3];
   }
-  // norm weights of this lane's QS dims: buffer loads (past hd they read 0
-  // or anything; those dims are zeroed below)
-  const __amdgpu_buffer_rsrc_t rn = buffer_rsrc(a.q_norm, (uint32_t)(hd * 4));
-#pragma unroll
-  for (int c = 0; c < QS / 4; ++c) wv[c] = buffer_load4(rn, (grp * QS + 4 * c) * 4, 0);
   ss += __shfl_xor(ss, 16);
   ss += pair_sum(ss) - ss;  // lanes l and l ^ 32 hold the other two groups
   const float scale = rms_scale(ss, hd, a.eps);
@@ -315,21 +328,21 @@ __device__ __forceinline__ void jeff_q_prep(const JeffArgs &a, const float *Q, i
     }
     *reinterpret_cast<f32x4 *>(qs + 4 * c) = y;
   }
-  if (a.cos_t != nullptr && rh > 0) {
+  if (rope) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // Lane (col, grp) rotates pairs i = grp, grp + 4, ... of query q0 + col.
+    // Lane (col, grp) rotates pairs i = grp, grp + 4, ... of query q0 + col;
+    // the first 8 with the entries loaded up front.
     if (q_live) {
-      const size_t pos = (size_t)(q - start) * rh;
       float *qr = qw + col * QP;
       for (int i0 = grp; i0 < rh; i0 += 4 * 8) {
         float c[8], sn[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {  // clamped table loads, all in flight
+        for (int u = 0; u < 8; ++u) {
           const int i = min(i0 + 4 * u, rh - 1);
-          c[u] = a.cos_t[pos + i];
-          sn[u] = a.sin_t[pos + i];
+          c[u] = i0 == grp ? c8[u] : a.cos_t[pos + i];
+          sn[u] = i0 == grp ? s8[u] : a.sin_t[pos + i];
         }
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
@@ -365,27 +378,29 @@ __device__ __forceinline__ void jeff_store(const JeffArgs &a, const float *Gt, f
   constexpr int NB = HDP / 16, QP = HDP + 4;
   const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
   const int L = a.L, hd = a.hd;
-#pragma unroll
-  for (int j = 0; j < NB; ++j) {
-    const f32x4 v = O[j] * inv;  // dims 16j + 4grp + 0..3 of query q0 + col
-    *reinterpret_cast<f32x4 *>(ow + col * QP + 16 * j + 4 * grp) = v;
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   if constexpr (VEC) {
+    // The gate loads go out before O is written to LDS.
     const __amdgpu_buffer_rsrc_t rg = buffer_rsrc(Gt, (uint32_t)((size_t)hd * L * 4));
     const __amdgpu_buffer_rsrc_t ro = buffer_rsrc(OUT, (uint32_t)((size_t)hd * L * 4));
+    constexpr int NG = (HDP * 4 + 63) / 64;
+    f32x4 g[NG];
 #pragma unroll
-    for (int i0 = 0; i0 < HDP * 4; i0 += 64 * 4) {
-      f32x4 g[4];
+    for (int u = 0; u < NG; ++u) {  // clamped as in the Q prep
+      const int e = min(lane + 64 * u, HDP * 4 - 1), d = e >> 2, gq = e & 3;
+      g[u] = buffer_load4(rg, (int)(((size_t)d * L + 4 * gq) * 4), q0 * 4);
+    }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {  // clamped as in the Q prep
-        const int e = min(i0 + lane + 64 * u, HDP * 4 - 1), d = e >> 2, gq = e & 3;
-        g[u] = buffer_load4(rg, (int)(((size_t)d * L + 4 * gq) * 4), q0 * 4);
-      }
+    for (int j = 0; j < NB; ++j) {
+      const f32x4 v = O[j] * inv;  // dims 16j + 4grp + 0..3 of query q0 + col
+      *reinterpret_cast<f32x4 *>(ow + col * QP + 16 * j + 4 * grp) = v;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    {
+      const int i0 = 0;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < NG; ++u) {
         const int e = min(i0 + lane + 64 * u, HDP * 4 - 1), d = e >> 2, gq = e & 3;
         const int qa = q0 + 4 * gq;  // L % 4 == 0: the 4 queries are all in or all out
         f32x4 o;
@@ -398,6 +413,14 @@ __device__ __forceinline__ void jeff_store(const JeffArgs &a, const float *Gt, f
       }
     }
   } else {
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const f32x4 v = O[j] * inv;  // dims 16j + 4grp + 0..3 of query q0 + col
+      *reinterpret_cast<f32x4 *>(ow + col * QP + 16 * j + 4 * grp) = v;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     for (int e0 = 0; e0 < 16 * HDP; e0 += 64 * 8) {
       float g[8];
 #pragma unroll
@@ -518,13 +541,29 @@ __global__ __launch_bounds__(kJeffF32Waves * 64, 1) void jeff_attention_f32_kern
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform, in a scalar register
   const int col = lane & 15, grp = lane >> 4;
   const int hg = a.heads_per_group, S = kJeffF32Waves / hg;  // query tiles per workgroup
-  const int row = blockIdx.z;
-  const int head = blockIdx.y * hg + wave % hg;
+  // XCD-aware order: the dispatcher hands workgroup p to XCD p % 8, each XCD
+  // with its own L2. Workgroups sharing one (row, kv head) -- its K/V -- are
+  // given ids p = 8*i + c for one c, so they land on one XCD; consecutive
+  // groups go to consecutive XCDs.
+  int bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
+  {
+    const int nx = gridDim.x, ngroups = gridDim.y * gridDim.z;
+    const int p = blockIdx.x + nx * (blockIdx.y + gridDim.y * blockIdx.z);
+    if (ngroups % 8 == 0) {
+      const int c = p % 8, i = p / 8;  // i-th workgroup of XCD c
+      const int g = 8 * (i / nx) + c;  // (row, kv group) index
+      bx = i % nx;
+      by = g % gridDim.y;
+      bz = g / gridDim.y;
+    }
+  }
+  const int row = bz;
+  const int head = by * hg + wave % hg;
   const int kvh = min(head / a.groups, a.kv_heads - 1);
   const int L = a.L, hd = a.hd;
   const int nq = (L + kJeffWaveQueries - 1) / kJeffWaveQueries;
   const int npairs = (nq + 1) / 2;
-  const int s_idx = wave / hg, pair = blockIdx.x * (S / 2) + s_idx / 2;
+  const int s_idx = wave / hg, pair = bx * (S / 2) + s_idx / 2;
   const bool hi_member = s_idx & 1;
   const int qtile = hi_member ? nq - 1 - pair : pair;
   // a wave with no query tile (past the pairs, or the middle tile's twin)
@@ -532,7 +571,7 @@ __global__ __launch_bounds__(kJeffF32Waves * 64, 1) void jeff_attention_f32_kern
   const int q0 = qtile * kJeffWaveQueries;
   const int q = q0 + col;
   // the group's last query: the upper member of its lowest pair
-  const int q_last = min((nq - (int)blockIdx.x * (S / 2)) * kJeffWaveQueries, L) - 1;
+  const int q_last = min((nq - bx * (S / 2)) * kJeffWaveQueries, L) - 1;
   const float *maskr = a.mask + (size_t)row * L;
   const float *Q = static_cast<const float *>(a.q) + row * a.q_row + (size_t)head * hd * L;
   const float *Gt = static_cast<const float *>(a.gate) + row * a.q_row + (size_t)head * hd * L;
@@ -557,6 +596,14 @@ __global__ __launch_bounds__(kJeffF32Waves * 64, 1) void jeff_attention_f32_kern
   }
   const bool q_live = wave_live && q < L && q >= start;
 
+  // The first tile's loads go out before the Q prep and land during it.
+  JeffStage<HDP, VEC, NT> st;
+  st.init(KP, V, L, hd, tid);
+  float m0 = 0.0f;
+  if (kt_begin < kt_end) {
+    m0 = maskr[min(kt_begin * KT + col, L - 1)];
+    st.fetch(KP, V, L, hd, kt_begin * KT, tid);
+  }
   float qreg[QS];
   jeff_q_prep<HDP, VEC>(a, Q, wave_live ? q0 : 0, start, qw, qreg);
   __syncthreads();  // the wave rows become the K/V buffers
@@ -586,13 +633,9 @@ __global__ __launch_bounds__(kJeffF32Waves * 64, 1) void jeff_attention_f32_kern
   // barrier per tile; lazily moved exponent reference; a wave whose kept
   // scores sum to NaN or inf stops computing, and it or a wave whose O took
   // a NaN or inf redoes its queries with the reference's exact semantics.
-  JeffStage<HDP, VEC, NT> st;
-  st.init(KP, V, L, hd, tid);
   uint32_t w = 0u;
   float m_next = 0.0f;
   if (kt_begin < kt_end) {
-    const float m0 = mask_of(kt_begin);
-    st.fetch(KP, V, L, hd, kt_begin * KT, tid);
     st.commit(Ks(0), Vs(0), tid, kt_begin * KT, L, hd);
     w = keep_word(kt_begin, m0);
   }
