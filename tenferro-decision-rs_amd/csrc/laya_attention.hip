@@ -6,16 +6,18 @@
 // (1111-1136), out = sum p*v with p == 0 never multiplying a value (1143-1151),
 // NaN for a query that keeps no key (1025-1033, 1143-1151).
 //
-// One workgroup = 4 wavefronts = 128 queries of one (batch, head). Each
-// wavefront owns 32 queries and walks 32-key tiles:
-//   S^T (32 keys x 32 queries) = K_tile * Q^T      (hd/2 MFMA 32x32x2)
-//   O^T (hd x 32 queries)     += V_tile^T * P^T     (hd/32 x 16 MFMA 32x32x2)
-// Computing S^T rather than S puts each lane's 16 probabilities exactly where
+// One workgroup = 4 wavefronts = 64 queries of one (batch, head). Each
+// wavefront owns 16 queries and walks 32-key tiles as two 16-key blocks:
+//   S^T (16 keys x 16 queries) = K_blk * Q^T       (hd/4 MFMA 16x16x4 per block)
+//   O^T (hd x 16 queries)     += V_tile^T * P^T     (hd/16 x 8 MFMA 16x16x4)
+// Computing S^T rather than S puts each lane's 8 probabilities exactly where
 // the B operand of the P.V product wants them, so no shuffles sit between the
 // two products. Q (rotated) stays in registers for the whole walk; K (rotated
 // while staged) and V tiles go through LDS and are shared by the 4 waves.
 // Key tiles outside the workgroup's key span are never visited; a wave whose
-// 32 queries keep nothing in a tile skips its MFMAs.
+// 16 queries keep nothing in a tile skips its MFMAs. Small workgroups (four
+// per CU) keep the per-tile critical path short and the work per CU even
+// when rows differ in length.
 #include "tfd_device.hpp"
 #include "tfd_internal.hpp"
 
@@ -89,26 +91,33 @@ __device__ __forceinline__ f32x4 rot_hi(f32x4 x, f32x4 y, f32x4 c, f32x4 s) {
 }
 
 // One K/V tile's global data held in registers between the prefetch (issued
-// before the previous tile's products) and the LDS commit (after them).
+// before the previous tile's products) and the LDS commit (after them). LDS
+// holds K as [key][d] (row stride KS) and V transposed, [d][key] (row stride
+// VS), so that the P.V product reads four consecutive keys of one feature
+// with one 16-byte read.
 //
 // VEC (hd == HDP, hd % 8 == 0, 16-byte aligned rows, the batch row within
 // 2 GiB): buffer loads; a K task is one (key, chunk c) with its RoPE partner
 // chunk c + half/4 (and, with ROPE, the table chunks); a V task is one
-// (key, chunk). Keys at or past L read as 0. Otherwise (any hd) the commit
-// loads and rotates element by element and the prefetch is empty.
+// (key pair, chunk), written as four 8-byte [d][key, key + 1] pairs. Keys at
+// or past L read as 0. Otherwise (any hd) the commit loads and rotates
+// element by element and the prefetch is empty.
 template <int HDP, bool VEC, bool ROPE>
 struct LayaStage {
+  static constexpr int KS = HDP + 4;        // conflict-free 16-byte row reads
+  static constexpr int VS = kKeyTile + 8;   // 4 rows = 32 banks: conflict-free pair writes
+  static constexpr int KBUF = kKeyTile * KS, VBUF = HDP * VS;
   static constexpr int KTASKS = kKeyTile * HDP / 8;
-  static constexpr int VTASKS = kKeyTile * HDP / 4;
+  static constexpr int VTASKS = (kKeyTile / 2) * (HDP / 4);
   static constexpr int KN = VEC ? (KTASKS + 255) / 256 : 1;
   static constexpr int VN = VEC ? (VTASKS + 255) / 256 : 1;
   static constexpr int CN = ROPE ? KN : 1;
   f32x4 ka[KN], kb[KN], c[CN], s[CN];
-  f32x4 v[VN];
+  f32x4 v0[VN], v1[VN];
   // Resources and per-lane byte offsets, fixed for the walk.
   __amdgpu_buffer_rsrc_t rk, rv, rc, rs;
   int ok[KN], oc[KN], ov[VN];
-  int hh4, tok4, hh4k;
+  int hh4, tok4;
 
   __device__ __forceinline__ void init(const LayaArgs &a, const float *xb, size_t tok, int tid) {
     if constexpr (VEC) {
@@ -130,12 +139,11 @@ struct LayaStage {
 #pragma unroll
       for (int i = 0; i < VN; ++i) {
         const int task = min(tid + 256 * i, VTASKS - 1);
-        const int kk = task / (HDP / 4), ch = task % (HDP / 4);
-        ov[i] = (int)(((size_t)kk * tok + 4 * ch) * 4);
+        const int p = task % (kKeyTile / 2), ch = task / (kKeyTile / 2);
+        ov[i] = (int)(((size_t)(2 * p) * tok + 4 * ch) * 4);
       }
       hh4 = hh * 4;
       tok4 = (int)(tok * 4);
-      hh4k = hh * 4 * kKeyTile;
     }
   }
 
@@ -152,14 +160,16 @@ struct LayaStage {
         }
       }
 #pragma unroll
-      for (int i = 0; i < VN; ++i) v[i] = buffer_load4(rv, ov[i], sk);
+      for (int i = 0; i < VN; ++i) {
+        v0[i] = buffer_load4(rv, ov[i], sk);
+        v1[i] = buffer_load4(rv, ov[i], sk + tok4);
+      }
     }
   }
 
-  // Writes the tile to LDS (K rotated).
+  // Writes the tile to LDS (K rotated, V transposed).
   __device__ __forceinline__ void commit(const LayaArgs &a, const float *xb, size_t tok, int k0,
                                          int tid, float *Ks, float *Vs) {
-    constexpr int KS = HDP + 4, VS = HDP + 8;
     if constexpr (VEC) {
       const int hh = a.half;
 #pragma unroll
@@ -180,8 +190,12 @@ struct LayaStage {
       for (int i = 0; i < VN; ++i) {
         const int task = tid + 256 * i;
         if (VTASKS % 256 == 0 || task < VTASKS) {
-          const int kk = task / (HDP / 4), ch = task % (HDP / 4);
-          *reinterpret_cast<f32x4 *>(&Vs[kk * VS + 4 * ch]) = v[i];
+          const int p = task % (kKeyTile / 2), ch = task / (kKeyTile / 2);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float2 pr = {v0[i][e], v1[i][e]};
+            *reinterpret_cast<float2 *>(&Vs[(4 * ch + e) * VS + 2 * p]) = pr;
+          }
         }
       }
     } else {
@@ -198,7 +212,7 @@ struct LayaStage {
           vv = row[2 * a.d + dd];
         }
         Ks[kk * KS + dd] = kv;
-        Vs[kk * VS + dd] = vv;
+        Vs[dd * VS + kk] = vv;
       }
     }
   }
@@ -206,18 +220,18 @@ struct LayaStage {
 
 // ------------------------------------------------------------------- kernel
 
-// The careful path for one wave's 32 queries (rare: NaN or inf among its
+// The careful path for one wave's 16 queries (rare: NaN or inf among its
 // kept scores or values), recomputed from global memory without barriers
 // and written to out: the reference's masked softmax with an exact running
 // max (non-finite scores weigh 0, a +inf score empties the row,
 // lib.rs:1111-1136) and key-by-key accumulation that skips zero
 // probabilities (lib.rs:1143-1151). Kept out of line so that its registers
-// never weigh on the walk. Pw: 32 x 33 floats of LDS owned by the wave.
+// never weigh on the walk. Pw: 32 x 17 floats of LDS owned by the wave.
 template <int HDP, int MODE, bool ROPE>
 __device__ __noinline__ void laya_redo_wave(const LayaArgs a, int b, int head, int q0,
                                             int kt_begin, int kt_end, float *Pw) {
-  constexpr int QS = HDP / 2, NB = HDP / 32, PS = kKeyTile + 1;
-  const int lane = threadIdx.x & 63, col = lane & 31, half = lane >> 5;
+  constexpr int QS = HDP / 4, NB = HDP / 16, PS = 17;
+  const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
   const int L = a.L, hd = a.hd, hh = a.half, nkt = a.nkt;
   const int q = q0 + col;
   const bool qin = q < L;
@@ -230,15 +244,15 @@ __device__ __noinline__ void laya_redo_wave(const LayaArgs a, int b, int head, i
     const float *cr = ROPE ? a.cos_t + (size_t)qq * hh : nullptr;
     const float *sr = ROPE ? a.sin_t + (size_t)qq * hh : nullptr;
 #pragma unroll
-    for (int x = 0; x < QS; ++x) qreg[x] = qin ? rope_elem(row, half * QS + x, hd, hh, cr, sr) : 0.0f;
+    for (int x = 0; x < QS; ++x) qreg[x] = qin ? rope_elem(row, grp * QS + x, hd, hh, cr, sr) : 0.0f;
   }
   bool q_valid = false;
   if (MODE == kMaskStruct) q_valid = qin && a.valid[(size_t)b * L + qq] != 0;
-  f32x16 O[NB];
+  f32x4 O[NB];
 #pragma unroll
   for (int j = 0; j < NB; ++j)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) O[j][r] = 0.0f;
+    for (int r = 0; r < 4; ++r) O[j][r] = 0.0f;
   float m = kNoMax, l = 0.0f;
 #pragma unroll 1
   for (int kt = kt_begin; kt < kt_end; ++kt) {
@@ -248,7 +262,7 @@ __device__ __noinline__ void laya_redo_wave(const LayaArgs a, int b, int head, i
       const uint32_t x = a.bits[((size_t)b * nkt + kt) * L + qq];
       wk = qin ? x : 0u;
     } else {
-      const int key = k0 + col;
+      const int key = k0 + (lane & 31);
       const bool kv = key < L && a.valid[(size_t)b * L + min(key, L - 1)] != 0;
       const uint32_t vbits = (uint32_t)__ballot(kv);
       if (qin) {
@@ -257,28 +271,38 @@ __device__ __noinline__ void laya_redo_wave(const LayaArgs a, int b, int head, i
       }
     }
     if (__ballot(wk != 0u) == 0) continue;
-    const int key = k0 + col;
-    const int kc = min(key, L - 1);
-    const float *krow = xb + (size_t)kc * tok + a.d;
-    const float *cr = ROPE ? a.cos_t + (size_t)kc * hh : nullptr;
-    const float *sr = ROPE ? a.sin_t + (size_t)kc * hh : nullptr;
-    f32x16 p;
+    f32x4 sb[2];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) p[r] = 0.0f;
+    for (int blk = 0; blk < 2; ++blk) {
+      const int key = k0 + 16 * blk + col;
+      const int kc = min(key, L - 1);
+      const float *krow = xb + (size_t)kc * tok + a.d;
+      const float *cr = ROPE ? a.cos_t + (size_t)kc * hh : nullptr;
+      const float *sr = ROPE ? a.sin_t + (size_t)kc * hh : nullptr;
+      f32x4 p = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int x = 0; x < QS; ++x) {
-      const float kx = rope_elem(krow, half * QS + x, hd, hh, cr, sr);
-      p = mfma_32x32x2(key < L ? kx : 0.0f, qreg[x], p);
+      for (int x = 0; x < QS; ++x) {
+        const float kx = rope_elem(krow, grp * QS + x, hd, hh, cr, sr);
+        p = mfma_16x16x4(key < L ? kx : 0.0f, qreg[x], p);
+      }
+      sb[blk] = p;
     }
-    const float alpha = softmax_tile(p, wk, half, a.c1, m, l);
+    const float alpha = softmax_tile16(sb[0], sb[1], wk, grp, a.c1, m, l);
     // alpha == 0: every earlier probability is 0 against the new max, so
     // earlier (possibly infinite) values drop out as in the reference.
 #pragma unroll
     for (int j = 0; j < NB; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) O[j][r] = alpha == 0.0f ? 0.0f : O[j][r] * alpha;
+      for (int r = 0; r < 4; ++r) O[j][r] = alpha == 0.0f ? 0.0f : O[j][r] * alpha;
+    __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int r = 0; r < 16; ++r) Pw[acc_row(r, half) * PS + col] = p[r];
+    for (int r = 0; r < 4; ++r) {
+      Pw[(4 * grp + r) * PS + col] = sb[0][r];
+      Pw[(16 + 4 * grp + r) * PS + col] = sb[1][r];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll 1
     for (int kk = 0; kk < kKeyTile; ++kk) {
       const float pk = Pw[kk * PS + col];
@@ -287,77 +311,82 @@ __device__ __noinline__ void laya_redo_wave(const LayaArgs a, int b, int head, i
 #pragma unroll
       for (int j = 0; j < NB; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int dd = j * 32 + acc_row(r, half);
+        for (int r = 0; r < 4; ++r) {
+          const int dd = 16 * j + 4 * grp + r;
           if (dd < hd) O[j][r] += pk * vrow[dd];
         }
     }
+    __builtin_amdgcn_wave_barrier();
   }
-  const float lt = pair_sum(l);
+  const float lt = pair_sum(pair16_sum(l));
   const float inv = lt > 0.0f ? fast_rcp(lt) : __builtin_nanf("");
   if (qin) {
     float *orow = a.out + ((size_t)b * L + q) * a.d + (size_t)head * hd;
 #pragma unroll
     for (int j = 0; j < NB; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int dd = j * 32 + acc_row(r, half);
+      for (int r = 0; r < 4; ++r) {
+        const int dd = 16 * j + 4 * grp + r;
         if (dd < hd) orow[dd] = O[j][r] * inv;
       }
   }
 }
 
-// Occupancy target: three workgroups (12 waves) per CU where the registers
-// allow it. On gfx950 the f32 MFMAs and the vector ALU share the SIMD (they
-// never run at the same time), so the walk keeps its vector work per tile
-// small and relies on other waves to cover memory and barrier waits.
+// Occupancy target: four workgroups (16 waves) per CU where LDS and
+// registers allow it. On gfx950 the f32 MFMAs and the vector ALU share the
+// SIMD (they never run at the same time), so the walk keeps its vector work
+// per tile small and relies on other waves to cover memory and barrier
+// waits.
 template <int HDP>
 constexpr int laya_groups_per_cu() {
-  return HDP <= 64 ? 3 : 2;
+  return HDP <= 64 ? 4 : 2;
 }
 
 template <int HDP, int MODE, bool VEC, bool ROPE>
 __global__ __launch_bounds__(256, laya_groups_per_cu<HDP>()) void laya_attention_kernel(
     const LayaArgs a) {
-  constexpr int KS = HDP + 4;  // K row stride (floats): 16-byte rows, conflict-free b128 reads
-  constexpr int VS = HDP + 8;  // V row stride: the two lane halves read rows 4 apart
-  constexpr int QS = HDP / 2;  // Q registers per lane
-  constexpr int NB = HDP / 32; // 32-row blocks of O^T
+  using Stage = LayaStage<HDP, VEC, ROPE>;
+  constexpr int KS = Stage::KS, VS = Stage::VS;
+  constexpr int QS = HDP / 4;   // Q registers per lane (4 lane groups split hd)
+  constexpr int NB = HDP / 16;  // 16-row blocks of O^T
   constexpr int GQ = kLayaGroupQueries;
-  // K buffers then V buffers, one block (reused after the walk).
-  __shared__ __attribute__((aligned(16))) float smem[2 * kKeyTile * (KS + VS)];
-  auto Ks = [&](int i) { return smem + i * (kKeyTile * KS); };
-  auto Vs = [&](int i) { return smem + 2 * kKeyTile * KS + i * (kKeyTile * VS); };
+  __shared__ __attribute__((aligned(16))) float smem[2 * (Stage::KBUF + Stage::VBUF)];
+  auto Ks = [&](int i) { return smem + i * Stage::KBUF; };
+  auto Vs = [&](int i) { return smem + 2 * Stage::KBUF + i * Stage::VBUF; };
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform, in a scalar register
-  const int col = lane & 31, half = lane >> 5;
+  const int col = lane & 15, grp = lane >> 4;
   const int head = blockIdx.y, b = blockIdx.z;
   const int L = a.L, hd = a.hd, hh = a.half, nkt = a.nkt;
   const int qg0 = blockIdx.x * GQ;
-  const int q = qg0 + wave * kWaveQueries + col;
+  const int q0w = qg0 + wave * kLayaWaveQueries;
+  const int q = q0w + col;
   const bool qin = q < L;
   const size_t tok = 3 * (size_t)a.d;
   const float *xb = a.qkv + (size_t)b * L * tok + (size_t)head * hd;
 
-  // -------- Q: rotated, in registers. Lane (col, half) holds
-  // Q[q][half*QS + s] for s < QS, the B operand of step s. The loads are
+  // -------- Q: rotated, in registers. Lane (col, grp) holds
+  // Q[q][grp*QS + x] for x < QS, the B operand of step x. The loads are
   // issued first so that they overlap the span scan.
   float qreg[QS];
-  f32x4 qlo[VEC ? QS / 4 : 1], qhi[VEC ? QS / 4 : 1], qcs[VEC && ROPE ? QS / 4 : 1],
+  f32x4 qown[VEC ? QS / 4 : 1], qpar[VEC && ROPE ? QS / 4 : 1], qcs[VEC && ROPE ? QS / 4 : 1],
       qsn[VEC && ROPE ? QS / 4 : 1];
   const int qq = qin ? q : 0;
+  const int d0 = grp * QS;
+  const bool qlo = d0 < hh;  // VEC: lane groups 0, 1 hold the low half of the row
   if constexpr (VEC) {
-    // hd == HDP: this lane's half of the row and its RoPE partner half are
-    // the two halves of the row; 16-byte loads, all in flight together.
+    // hd == HDP: this lane's quarter of the row and (with RoPE) its partner
+    // quarter half a row away; 16-byte loads, all in flight together.
     const float *row = xb + (size_t)qq * tok;
+    const int dp = qlo ? d0 + hh : d0 - hh, ci = qlo ? d0 : dp;
 #pragma unroll
     for (int c = 0; c < QS / 4; ++c) {
-      qlo[c] = reinterpret_cast<const f32x4 *>(row)[c];
-      qhi[c] = reinterpret_cast<const f32x4 *>(row + QS)[c];
+      qown[c] = reinterpret_cast<const f32x4 *>(row + d0)[c];
       if constexpr (ROPE) {
-        qcs[c] = reinterpret_cast<const f32x4 *>(a.cos_t + (size_t)qq * hh)[c];
-        qsn[c] = reinterpret_cast<const f32x4 *>(a.sin_t + (size_t)qq * hh)[c];
+        qpar[c] = reinterpret_cast<const f32x4 *>(row + dp)[c];
+        qcs[c] = reinterpret_cast<const f32x4 *>(a.cos_t + (size_t)qq * hh + ci)[c];
+        qsn[c] = reinterpret_cast<const f32x4 *>(a.sin_t + (size_t)qq * hh + ci)[c];
       }
     }
   }
@@ -368,23 +397,19 @@ __global__ __launch_bounds__(256, laya_groups_per_cu<HDP>()) void laya_attention
   // skips the products of tiles its queries keep nothing of.
   int kt_begin = 0, kt_end = 0;
   if (MODE == kMaskBits) {
+    // The workgroup's 64 queries are exactly tile-map group qg0 / 64.
     const int ng = (L + 63) / 64, g0 = qg0 / 64;
-    const uint8_t *anyb = a.any + (size_t)b * nkt * ng;
+    const uint8_t *anyb = a.any + (size_t)b * nkt * ng + g0;
     int lo = 0x7fffffff, hi = -1;
     for (int k0 = 0; k0 < nkt; k0 += 64 * 4) {
-      uint8_t f[4][GQ / 64];
+      uint8_t f[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u)  // clamped loads, all in flight together
-#pragma unroll
-        for (int g = 0; g < GQ / 64; ++g)
-          f[u][g] = anyb[(size_t)min(k0 + lane + 64 * u, nkt - 1) * ng + min(g0 + g, ng - 1)];
+        f[u] = anyb[(size_t)min(k0 + lane + 64 * u, nkt - 1) * ng];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int kt = k0 + lane + 64 * u;
-        bool some = false;
-#pragma unroll
-        for (int g = 0; g < GQ / 64; ++g) some |= g0 + g < ng && f[u][g] != 0;
-        if (kt < nkt && some) {
+        if (kt < nkt && f[u] != 0) {
           lo = min(lo, kt);
           hi = max(hi, kt);
         }
@@ -402,14 +427,9 @@ __global__ __launch_bounds__(256, laya_groups_per_cu<HDP>()) void laya_attention
     // window and no padded query in the group the window bounds the span;
     // otherwise it runs from the first to the last valid key of the row.
     const uint8_t *vb = a.valid + (size_t)b * L;
-    int padded = 0;
-#pragma unroll
-    for (int u = 0; u < GQ / 64; ++u) {
-      const int qx = qg0 + lane + 64 * u;
-      const uint8_t x = vb[min(qx, L - 1)];
-      padded |= qx < L && x == 0;
-    }
-    padded = __ballot(padded) != 0;
+    const int qx = qg0 + lane;
+    const uint8_t xv = vb[min(qx, L - 1)];
+    const bool padded = __ballot(qx < L && xv == 0) != 0;
     int kf = 0, kl = -1;
     if (a.window >= 0 && !padded) {
       kf = max(0, qg0 - a.window);
@@ -446,9 +466,9 @@ __global__ __launch_bounds__(256, laya_groups_per_cu<HDP>()) void laya_attention
   if constexpr (VEC) {
 #pragma unroll
     for (int c = 0; c < QS / 4; ++c) {
-      f32x4 v = half ? qhi[c] : qlo[c];
+      f32x4 v = qown[c];
       if constexpr (ROPE)
-        v = half ? rot_hi(qlo[c], qhi[c], qcs[c], qsn[c]) : rot_lo(qlo[c], qhi[c], qcs[c], qsn[c]);
+        v = qlo ? rot_lo(qown[c], qpar[c], qcs[c], qsn[c]) : rot_hi(qpar[c], qown[c], qcs[c], qsn[c]);
 #pragma unroll
       for (int e = 0; e < 4; ++e) qreg[4 * c + e] = qin ? v[e] : 0.0f;
     }
@@ -457,8 +477,7 @@ __global__ __launch_bounds__(256, laya_groups_per_cu<HDP>()) void laya_attention
     const float *cr = ROPE ? a.cos_t + (size_t)qq * hh : nullptr;
     const float *sr = ROPE ? a.sin_t + (size_t)qq * hh : nullptr;
 #pragma unroll
-    for (int s = 0; s < QS; ++s)
-      qreg[s] = qin ? rope_elem(row, half * QS + s, hd, hh, cr, sr) : 0.0f;
+    for (int x = 0; x < QS; ++x) qreg[x] = qin ? rope_elem(row, d0 + x, hd, hh, cr, sr) : 0.0f;
   }
   bool q_valid = false;
   if (MODE == kMaskStruct) {
@@ -473,7 +492,7 @@ __global__ __launch_bounds__(256, laya_groups_per_cu<HDP>()) void laya_attention
   auto mask_of = [&](int kt) -> uint32_t {
     if (MODE == kMaskBits)
       return a.bits[((size_t)b * nkt + min(kt, nkt - 1)) * L + min(q, L - 1)];
-    return a.valid[(size_t)b * L + min(kt * kKeyTile + col, L - 1)];
+    return a.valid[(size_t)b * L + min(kt * kKeyTile + (lane & 31), L - 1)];
   };
   auto keep_word = [&](int kt, uint32_t x) -> uint32_t {
     uint32_t w = 0u;
@@ -481,7 +500,7 @@ __global__ __launch_bounds__(256, laya_groups_per_cu<HDP>()) void laya_attention
       w = qin ? x : 0u;
     } else {
       const int k0 = kt * kKeyTile;
-      const int key = k0 + col;
+      const int key = k0 + (lane & 31);
       const bool kv = key < L && x != 0;
       const uint32_t vbits = (uint32_t)__ballot(kv);  // lanes 0..31 = keys of the tile
       if (qin) {
@@ -492,34 +511,18 @@ __global__ __launch_bounds__(256, laya_groups_per_cu<HDP>()) void laya_attention
     return w;
   };
 
-  f32x16 O[NB];
+  f32x4 O[NB];
 #pragma unroll
   for (int j = 0; j < NB; ++j)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) O[j][r] = 0.0f;
-  float m = kNoMax, l = 0.0f;
+    for (int r = 0; r < 4; ++r) O[j][r] = 0.0f;
+  float m = kNoMax, l = 0.0f;  // l: this lane's share of the row sum
   const float c1 = a.c1;
-
-  // S^T of one staged tile: K rows from LDS against the Q registers.
-  auto scores = [&](const float *Kc) {
-    f32x16 s;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) s[r] = 0.0f;
-    const f32x4 *krow = reinterpret_cast<const f32x4 *>(&Kc[col * KS + half * QS]);
-#pragma unroll
-    for (int c = 0; c < QS / 4; ++c) {
-      const f32x4 kv = krow[c];
-      s = mfma_32x32x2(kv[0], qreg[4 * c + 0], s);
-      s = mfma_32x32x2(kv[1], qreg[4 * c + 1], s);
-      s = mfma_32x32x2(kv[2], qreg[4 * c + 2], s);
-      s = mfma_32x32x2(kv[3], qreg[4 * c + 3], s);
-    }
-    return s;
-  };
 
   // -------- the walk: tile kt+1 is fetched into registers before the
   // products of tile kt and committed to the other LDS buffer after them;
-  // one barrier per tile.
+  // one barrier per tile. A 32-key tile is two S^T blocks: sb[0] holds keys
+  // 4*grp + r, sb[1] keys 16 + 4*grp + r of query col.
   //
   // Exponents are fma(s, c1, -m) against a reference m that only moves when
   // a tile max exceeds it by more than kRescaleSlack. Non-finite inputs are
@@ -527,7 +530,7 @@ __global__ __launch_bounds__(256, laya_groups_per_cu<HDP>()) void laya_attention
   // computing (it still stages tiles and meets the barriers), a NaN or inf
   // value reaches O and stays there, and either way the wave redoes its
   // queries with the reference's exact semantics after the walk.
-  LayaStage<HDP, VEC, ROPE> st;
+  Stage st;
   st.init(a, xb, tok, tid);
   uint32_t w = 0u, m_next = 0u;
   if (kt_begin < kt_end) {
@@ -546,23 +549,41 @@ __global__ __launch_bounds__(256, laya_groups_per_cu<HDP>()) void laya_attention
       st.fetch((kt + 1) * kKeyTile);
     }
     if (!tainted && __ballot(w != 0u) != 0) {  // wave-uniform
-      f32x16 s = scores(Ks(cur));
+      // S^T: K rows from LDS against the Q registers, two independent chains.
+      f32x4 s0 = {0.0f, 0.0f, 0.0f, 0.0f}, s1 = {0.0f, 0.0f, 0.0f, 0.0f};
+      {
+        const float *Kc = Ks(cur);
+        const f32x4 *k0p = reinterpret_cast<const f32x4 *>(&Kc[col * KS + d0]);
+        const f32x4 *k1p = reinterpret_cast<const f32x4 *>(&Kc[(16 + col) * KS + d0]);
+#pragma unroll
+        for (int c = 0; c < QS / 4; ++c) {
+          const f32x4 x0 = k0p[c], x1 = k1p[c];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            s0 = mfma_16x16x4(x0[e], qreg[4 * c + e], s0);
+            s1 = mfma_16x16x4(x1[e], qreg[4 * c + e], s1);
+          }
+        }
+      }
       if (__ballot(qin && w != 0xffffffffu) != 0) {
         // A tile some query of the wave keeps only in part: mask it.
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s[r] = ((w >> acc_row(r, half)) & 1u) ? s[r] : -INFINITY;
+        for (int r = 0; r < 4; ++r) {
+          s0[r] = ((w >> (4 * grp + r)) & 1u) ? s0[r] : -INFINITY;
+          s1[r] = ((w >> (16 + 4 * grp + r)) & 1u) ? s1[r] : -INFINITY;
+        }
       }
-      float mx = s[0];
-#pragma unroll
-      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
-      const float mxs = pair_max(mx) * c1;
+      float mx = fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])),
+                       fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3])));
+      const float mxs = pair_max(pair16_max(mx)) * c1;
       const bool need = mxs > m + kRescaleSlack;
       const float mn = need ? mxs : m;
       float rs = 0.0f;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        s[r] = fast_exp2(__builtin_fmaf(s[r], c1, -mn));
-        rs += s[r];
+      for (int r = 0; r < 4; ++r) {
+        s0[r] = fast_exp2(__builtin_fmaf(s0[r], c1, -mn));
+        s1[r] = fast_exp2(__builtin_fmaf(s1[r], c1, -mn));
+        rs += s0[r] + s1[r];
       }
       if (__ballot(qin && !__builtin_isfinite(rs)) != 0) {
         tainted = true;
@@ -575,12 +596,18 @@ __global__ __launch_bounds__(256, laya_groups_per_cu<HDP>()) void laya_attention
         }
         l += rs;
         m = mn;
-        const float *Vc = Vs(cur);
+        // A operand of block j: V[key 4*grp + r (+16)][d = 16*j + col], one
+        // 16-byte read per 4 keys.
+        const float *vb = &Vs(cur)[col * VS + 4 * grp];
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
+        for (int j = 0; j < NB; ++j) {
+          const f32x4 va = *reinterpret_cast<const f32x4 *>(vb + j * 16 * VS);
+          const f32x4 vc = *reinterpret_cast<const f32x4 *>(vb + j * 16 * VS + 16);
 #pragma unroll
-          for (int j = 0; j < NB; ++j)
-            O[j] = mfma_32x32x2(Vc[acc_row(r, half) * VS + j * 32 + col], s[r], O[j]);
+          for (int r = 0; r < 4; ++r) O[j] = mfma_16x16x4(va[r], s0[r], O[j]);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) O[j] = mfma_16x16x4(vc[r], s1[r], O[j]);
+        }
       }
     }
     if (more) st.commit(a, xb, tok, (kt + 1) * kKeyTile, tid, Ks(cur ^ 1), Vs(cur ^ 1));
@@ -596,36 +623,30 @@ __global__ __launch_bounds__(256, laya_groups_per_cu<HDP>()) void laya_attention
 #pragma unroll
   for (int j = 0; j < NB; ++j)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) bad |= !__builtin_isfinite(O[j][r]);
+    for (int r = 0; r < 4; ++r) bad |= !__builtin_isfinite(O[j][r]);
   if (tainted || __ballot(qin && bad) != 0) {
-    laya_redo_wave<HDP, MODE, ROPE>(a, b, head, qg0 + wave * kWaveQueries, kt_begin, kt_end,
-                                    smem + wave * kKeyTile * (kKeyTile + 1));
+    laya_redo_wave<HDP, MODE, ROPE>(a, b, head, q0w, kt_begin, kt_end,
+                                    smem + wave * kKeyTile * 17);
     return;
   }
 
   // -------- normalize and store: out[feat + d + hidden*(q + L*b)]
   // 0/0 gives NaN for a query that kept nothing, as the reference does.
-  const float lt = pair_sum(l);
+  const float lt = pair_sum(pair16_sum(l));
   const float inv = lt > 0.0f ? fast_rcp(lt) : __builtin_nanf("");
   if (qin) {
     float *orow = a.out + ((size_t)b * L + q) * a.d + (size_t)head * hd;
     if constexpr (VEC) {
-      // Accumulators 4g..4g+3 are dims j*32 + 8g + 4*half + 0..3: one
-      // 16-byte store each.
+      // Block j holds dims 16j + 4*grp + 0..3: one 16-byte store each.
 #pragma unroll
       for (int j = 0; j < NB; ++j)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const f32x4 v = {O[j][4 * g] * inv, O[j][4 * g + 1] * inv, O[j][4 * g + 2] * inv,
-                           O[j][4 * g + 3] * inv};
-          *reinterpret_cast<f32x4 *>(orow + j * 32 + 8 * g + 4 * half) = v;
-        }
+        *reinterpret_cast<f32x4 *>(orow + 16 * j + 4 * grp) = O[j] * inv;
     } else {
 #pragma unroll
       for (int j = 0; j < NB; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int dd = j * 32 + acc_row(r, half);
+        for (int r = 0; r < 4; ++r) {
+          const int dd = 16 * j + 4 * grp + r;
           if (dd < hd) orow[dd] = O[j][r] * inv;
         }
     }

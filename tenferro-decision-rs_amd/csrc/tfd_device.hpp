@@ -81,6 +81,19 @@ __device__ __forceinline__ float pair_sum(float x) {
                                                   false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
+// The same over the lane pair (l, l ^ 16), with one v_permlane16_swap (odd
+// 16-lane rows of the first operand trade places with even rows of the
+// second).
+__device__ __forceinline__ float pair16_max(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair16_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 // Online softmax with a lazily moved reference: exponents are taken against
 // a reference m (log2 units) that only moves when a tile's max exceeds it by

@@ -8,12 +8,11 @@
 
 namespace tfd {
 
-// Keys per tile and queries per wave in every attention kernel: one 32x32
-// MFMA output block covers (32 keys) x (32 queries).
+// Keys per tile of the Laya and Jeff bf16 kernels.
 constexpr int kKeyTile = 32;
-constexpr int kWaveQueries = 32;
-constexpr int kWavesPerGroup = 4;   // 256 threads per workgroup
-constexpr int kLayaGroupQueries = kWaveQueries * kWavesPerGroup;
+constexpr int kWavesPerGroup = 4;     // 256 threads per workgroup
+constexpr int kLayaWaveQueries = 16;  // Laya waves use the 16x16x4 MFMA
+constexpr int kLayaGroupQueries = kLayaWaveQueries * kWavesPerGroup;
 constexpr int kJeffWaveQueries = 16;  // Jeff waves use the 16x16x4 MFMA
 constexpr int kJeffF32Waves = 8;      // Jeff f32 workgroup: 512 threads, one per CU
 constexpr int kJeffKeyTile = 16;      // keys per Jeff f32 tile
