@@ -99,21 +99,22 @@ __device__ __forceinline__ f32x4 rot_hi(f32x4 x, f32x4 y, f32x4 c, f32x4 s) {
 // VEC (hd == HDP, hd % 8 == 0, 16-byte aligned rows, the batch row within
 // 2 GiB): buffer loads; a K task is one (key, chunk c) with its RoPE partner
 // chunk c + half/4 (and, with ROPE, the table chunks); a V task is one
-// (key pair, chunk), written as four 8-byte [d][key, key + 1] pairs. Keys at
-// or past L read as 0. Otherwise (any hd) the commit loads and rotates
-// element by element and the prefetch is empty.
+// feature of four consecutive keys, four 4-byte loads (a wave reads whole
+// key rows) that land as one 16-byte [d][key .. key + 3] LDS row piece.
+// Keys at or past L read as 0. Otherwise (any hd) the commit loads and
+// rotates element by element and the prefetch is empty.
 template <int HDP, bool VEC, bool ROPE>
 struct LayaStage {
   static constexpr int KS = HDP + 4;        // conflict-free 16-byte row reads
-  static constexpr int VS = kKeyTile + 8;   // 4 rows = 32 banks: conflict-free pair writes
+  static constexpr int VS = kKeyTile + 4;   // 16 lanes of 16-byte row pieces: conflict-free
   static constexpr int KBUF = kKeyTile * KS, VBUF = HDP * VS;
   static constexpr int KTASKS = kKeyTile * HDP / 8;
-  static constexpr int VTASKS = (kKeyTile / 2) * (HDP / 4);
+  static constexpr int VTASKS = (kKeyTile / 4) * HDP;
   static constexpr int KN = VEC ? (KTASKS + 255) / 256 : 1;
   static constexpr int VN = VEC ? (VTASKS + 255) / 256 : 1;
   static constexpr int CN = ROPE ? KN : 1;
   f32x4 ka[KN], kb[KN], c[CN], s[CN];
-  f32x4 v0[VN], v1[VN];
+  f32x4 v[VN];
   // Resources and per-lane byte offsets, fixed for the walk.
   __amdgpu_buffer_rsrc_t rk, rv, rc, rs;
   int ok[KN], oc[KN], ov[VN];
@@ -139,8 +140,8 @@ struct LayaStage {
 #pragma unroll
       for (int i = 0; i < VN; ++i) {
         const int task = min(tid + 256 * i, VTASKS - 1);
-        const int p = task % (kKeyTile / 2), ch = task / (kKeyTile / 2);
-        ov[i] = (int)(((size_t)(2 * p) * tok + 4 * ch) * 4);
+        const int dd = task % HDP, kq = task / HDP;
+        ov[i] = (int)(((size_t)(4 * kq) * tok + dd) * 4);
       }
       hh4 = hh * 4;
       tok4 = (int)(tok * 4);
@@ -160,10 +161,9 @@ struct LayaStage {
         }
       }
 #pragma unroll
-      for (int i = 0; i < VN; ++i) {
-        v0[i] = buffer_load4(rv, ov[i], sk);
-        v1[i] = buffer_load4(rv, ov[i], sk + tok4);
-      }
+      for (int i = 0; i < VN; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[i][e] = buffer_load1(rv, ov[i], sk + e * tok4);
     }
   }
 
@@ -190,12 +190,8 @@ struct LayaStage {
       for (int i = 0; i < VN; ++i) {
         const int task = tid + 256 * i;
         if (VTASKS % 256 == 0 || task < VTASKS) {
-          const int p = task % (kKeyTile / 2), ch = task / (kKeyTile / 2);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float2 pr = {v0[i][e], v1[i][e]};
-            *reinterpret_cast<float2 *>(&Vs[(4 * ch + e) * VS + 2 * p]) = pr;
-          }
+          const int dd = task % HDP, kq = task / HDP;
+          *reinterpret_cast<f32x4 *>(&Vs[dd * VS + 4 * kq]) = v[i];
         }
       }
     } else {
@@ -366,9 +362,30 @@ __global__ __launch_bounds__(256, laya_groups_per_cu<HDP>()) void laya_attention
   const size_t tok = 3 * (size_t)a.d;
   const float *xb = a.qkv + (size_t)b * L * tok + (size_t)head * hd;
 
+  // -------- key span of the workgroup: the tiles [kt_begin, kt_end) that
+  // hold a key some query of the workgroup may keep (it may be a superset; a
+  // wave skips the products of tiles its queries keep nothing of). Every
+  // wave computes it on its own from ballots (identical scalar results, no
+  // barrier). Its bytes are read before anything else, so that waiting for
+  // them never waits for the Q rows issued after them.
+  int kt_begin = 0, kt_end = 0;
+  uint8_t f0[4];
+  const int ng = (L + 63) / 64;
+  const uint8_t *anyb = a.any + (size_t)b * nkt * ng + qg0 / 64;  // kMaskBits
+  const uint8_t *vb = a.valid + (size_t)b * L;                     // kMaskStruct
+  bool padded = false;
+  if (MODE == kMaskBits) {
+    // The workgroup's 64 queries are exactly tile-map group qg0 / 64.
+#pragma unroll
+    for (int u = 0; u < 4; ++u) f0[u] = anyb[(size_t)min(lane + 64 * u, nkt - 1) * ng];
+  } else {
+    const int qx = qg0 + lane;
+    const uint8_t xv = vb[min(qx, L - 1)];
+    padded = __ballot(qx < L && xv == 0) != 0;
+  }
+
   // -------- Q: rotated, in registers. Lane (col, grp) holds
-  // Q[q][grp*QS + x] for x < QS, the B operand of step x. The loads are
-  // issued first so that they overlap the span scan.
+  // Q[q][grp*QS + x] for x < QS, the B operand of step x.
   float qreg[QS];
   f32x4 qown[VEC ? QS / 4 : 1], qpar[VEC && ROPE ? QS / 4 : 1], qcs[VEC && ROPE ? QS / 4 : 1],
       qsn[VEC && ROPE ? QS / 4 : 1];
@@ -391,32 +408,25 @@ __global__ __launch_bounds__(256, laya_groups_per_cu<HDP>()) void laya_attention
     }
   }
 
-  // -------- key span of the workgroup, computed by every wave on its own
-  // (identical results, no barrier): the tiles [kt_begin, kt_end) that hold
-  // a key some query of the workgroup may keep. It may be a superset; a wave
-  // skips the products of tiles its queries keep nothing of.
-  int kt_begin = 0, kt_end = 0;
+  // Lowest / highest set lane index of a ballot over 64 items starting at k0.
+  int lo = 0x7fffffff, hi = -1;
+  auto span_add = [&](uint64_t mk, int k0) {
+    if (mk != 0) {
+      lo = min(lo, k0 + (int)__builtin_ctzll(mk));
+      hi = max(hi, k0 + 63 - (int)__builtin_clzll(mk));
+    }
+  };
   if (MODE == kMaskBits) {
-    // The workgroup's 64 queries are exactly tile-map group qg0 / 64.
-    const int ng = (L + 63) / 64, g0 = qg0 / 64;
-    const uint8_t *anyb = a.any + (size_t)b * nkt * ng + g0;
-    int lo = 0x7fffffff, hi = -1;
-    for (int k0 = 0; k0 < nkt; k0 += 64 * 4) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) span_add(__ballot(lane + 64 * u < nkt && f0[u] != 0), 64 * u);
+    for (int k0 = 64 * 4; k0 < nkt; k0 += 64 * 4) {  // L > 8192 only
       uint8_t f[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u)  // clamped loads, all in flight together
-        f[u] = anyb[(size_t)min(k0 + lane + 64 * u, nkt - 1) * ng];
+      for (int u = 0; u < 4; ++u) f[u] = anyb[(size_t)min(k0 + lane + 64 * u, nkt - 1) * ng];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int kt = k0 + lane + 64 * u;
-        if (kt < nkt && f[u] != 0) {
-          lo = min(lo, kt);
-          hi = max(hi, kt);
-        }
-      }
+      for (int u = 0; u < 4; ++u)
+        span_add(__ballot(k0 + lane + 64 * u < nkt && f[u] != 0), k0 + 64 * u);
     }
-    lo = wave_min(lo);
-    hi = wave_max(hi);
     if (hi >= 0) {
       kt_begin = lo;
       kt_end = hi + 1;
@@ -426,42 +436,50 @@ __global__ __launch_bounds__(256, laya_groups_per_cu<HDP>()) void laya_attention
     // valid keys of its window, a padded query every valid key. With a
     // window and no padded query in the group the window bounds the span;
     // otherwise it runs from the first to the last valid key of the row.
-    const uint8_t *vb = a.valid + (size_t)b * L;
-    const int qx = qg0 + lane;
-    const uint8_t xv = vb[min(qx, L - 1)];
-    const bool padded = __ballot(qx < L && xv == 0) != 0;
     int kf = 0, kl = -1;
     if (a.window >= 0 && !padded) {
       kf = max(0, qg0 - a.window);
       kl = min(L - 1, min(qg0 + GQ - 1, L - 1) + a.window);
     } else {
-      int lo = 0x7fffffff, hi = -1;
       for (int k0 = 0; k0 < L; k0 += 64 * 8) {
         uint8_t v[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) v[u] = vb[min(k0 + lane + 64 * u, L - 1)];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const int k = k0 + lane + 64 * u;
-          if (k < L && v[u]) {
-            lo = min(lo, k);
-            hi = max(hi, k);
-          }
-        }
+        for (int u = 0; u < 8; ++u)
+          span_add(__ballot(k0 + lane + 64 * u < L && v[u] != 0), k0 + 64 * u);
       }
-      kf = wave_min(lo);
-      kl = wave_max(hi);
+      kf = lo;
+      kl = hi;
     }
     if (kl >= 0 && kf <= kl) {
       kt_begin = kf / kKeyTile;
       kt_end = kl / kKeyTile + 1;
     }
   }
-
-  // The reductions above leave the same value in every lane; say so, so that
-  // the walk's counters and scalar offsets stay in scalar registers.
+  // Ballot results are uniform already; say so for the walk's scalar
+  // counters and offsets.
   kt_begin = __builtin_amdgcn_readfirstlane(kt_begin);
   kt_end = __builtin_amdgcn_readfirstlane(kt_end);
+
+  // This lane's keep word for key tile kt (bit j: key 32*kt + j). The raw
+  // word or validity byte is fetched one tile ahead (mask_of) and turned
+  // into the word (keep_word) only after that tile's barrier, so waiting on
+  // it never stalls the tile prefetch issued beside it.
+  auto mask_of = [&](int kt) -> uint32_t {
+    if (MODE == kMaskBits)
+      return a.bits[((size_t)b * nkt + min(kt, nkt - 1)) * L + min(q, L - 1)];
+    return a.valid[(size_t)b * L + min(kt * kKeyTile + (lane & 31), L - 1)];
+  };
+
+  // The first tile's loads go out before the Q rotation waits for its rows.
+  Stage st;
+  st.init(a, xb, tok, tid);
+  uint32_t m0 = 0u;
+  if (kt_begin < kt_end) {
+    m0 = mask_of(kt_begin);
+    st.fetch(kt_begin * kKeyTile);
+  }
 
   if constexpr (VEC) {
 #pragma unroll
@@ -485,15 +503,6 @@ __global__ __launch_bounds__(256, laya_groups_per_cu<HDP>()) void laya_attention
     q_valid = qin && x != 0;
   }
 
-  // This lane's keep word for key tile kt (bit j: key 32*kt + j). The raw
-  // word or validity byte is fetched one tile ahead (mask_of) and turned
-  // into the word (keep_word) only after that tile's barrier, so waiting on
-  // it never stalls the tile prefetch issued beside it.
-  auto mask_of = [&](int kt) -> uint32_t {
-    if (MODE == kMaskBits)
-      return a.bits[((size_t)b * nkt + min(kt, nkt - 1)) * L + min(q, L - 1)];
-    return a.valid[(size_t)b * L + min(kt * kKeyTile + (lane & 31), L - 1)];
-  };
   auto keep_word = [&](int kt, uint32_t x) -> uint32_t {
     uint32_t w = 0u;
     if (MODE == kMaskBits) {
@@ -521,21 +530,21 @@ __global__ __launch_bounds__(256, laya_groups_per_cu<HDP>()) void laya_attention
 
   // -------- the walk: tile kt+1 is fetched into registers before the
   // products of tile kt and committed to the other LDS buffer after them;
-  // one barrier per tile. A 32-key tile is two S^T blocks: sb[0] holds keys
-  // 4*grp + r, sb[1] keys 16 + 4*grp + r of query col.
+  // one barrier per tile. A 32-key tile is two S^T blocks: s0 holds keys
+  // 4*grp + r, s1 keys 16 + 4*grp + r of query col.
   //
-  // Exponents are fma(s, c1, -m) against a reference m that only moves when
-  // a tile max exceeds it by more than kRescaleSlack. Non-finite inputs are
-  // kept off this path: a wave whose kept scores sum to NaN or inf stops
-  // computing (it still stages tiles and meets the barriers), a NaN or inf
-  // value reaches O and stays there, and either way the wave redoes its
+  // Exponents are exp2(fma(s, c1, -m)) against a reference m (log2 units)
+  // that moves only when needed: a tile is first exponentiated against the
+  // current m, and only if some lane's 8 terms sum to more than 2^11 (or to
+  // NaN / inf: every term is then checked for a max more than kRescaleSlack
+  // above m) is the tile max taken, m moved to it and the accumulators
+  // rescaled. Terms stay below 2^11; O / l is unchanged. Non-finite inputs
+  // are kept off this path: a wave whose kept scores sum to NaN or inf
+  // stops computing (it still stages tiles and meets the barriers), a NaN or
+  // inf value reaches O and stays there, and either way the wave redoes its
   // queries with the reference's exact semantics after the walk.
-  Stage st;
-  st.init(a, xb, tok, tid);
   uint32_t w = 0u, m_next = 0u;
   if (kt_begin < kt_end) {
-    const uint32_t m0 = mask_of(kt_begin);
-    st.fetch(kt_begin * kKeyTile);
     st.commit(a, xb, tok, kt_begin * kKeyTile, tid, Ks(0), Vs(0));
     w = keep_word(kt_begin, m0);
   }
@@ -573,29 +582,43 @@ __global__ __launch_bounds__(256, laya_groups_per_cu<HDP>()) void laya_attention
           s1[r] = ((w >> (16 + 4 * grp + r)) & 1u) ? s1[r] : -INFINITY;
         }
       }
-      float mx = fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])),
-                       fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3])));
-      const float mxs = pair_max(pair16_max(mx)) * c1;
-      const bool need = mxs > m + kRescaleSlack;
-      const float mn = need ? mxs : m;
+      f32x4 e0, e1;
       float rs = 0.0f;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        s0[r] = fast_exp2(__builtin_fmaf(s0[r], c1, -mn));
-        s1[r] = fast_exp2(__builtin_fmaf(s1[r], c1, -mn));
-        rs += s0[r] + s1[r];
+        e0[r] = fast_exp2(__builtin_fmaf(s0[r], c1, -m));
+        e1[r] = fast_exp2(__builtin_fmaf(s1[r], c1, -m));
+        rs += e0[r] + e1[r];
       }
-      if (__ballot(qin && !__builtin_isfinite(rs)) != 0) {
-        tainted = true;
-      } else {
-        if (__ballot(need) != 0) {
+      bool ok = true;
+      if (__ballot(qin && !(rs <= kLazyLimit)) != 0) {
+        // Move the reference where the tile max exceeds it by more than the
+        // slack (the first tile always: m starts at kNoMax).
+        const float mx = fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])),
+                               fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3])));
+        const float mxs = pair_max(pair16_max(mx)) * c1;
+        const bool need = mxs > m + kRescaleSlack;
+        const float mn = need ? mxs : m;
+        rs = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          e0[r] = fast_exp2(__builtin_fmaf(s0[r], c1, -mn));
+          e1[r] = fast_exp2(__builtin_fmaf(s1[r], c1, -mn));
+          rs += e0[r] + e1[r];
+        }
+        if (__ballot(qin && !__builtin_isfinite(rs)) != 0) {
+          tainted = true;
+          ok = false;
+        } else {
           const float alpha = fast_exp2(m - mn);  // exactly 1 where the reference stays
 #pragma unroll
           for (int j = 0; j < NB; ++j) O[j] *= alpha;
           l *= alpha;
+          m = mn;
         }
+      }
+      if (ok) {
         l += rs;
-        m = mn;
         // A operand of block j: V[key 4*grp + r (+16)][d = 16*j + col], one
         // 16-byte read per 4 keys.
         const float *vb = &Vs(cur)[col * VS + 4 * grp];
@@ -604,9 +627,9 @@ __global__ __launch_bounds__(256, laya_groups_per_cu<HDP>()) void laya_attention
           const f32x4 va = *reinterpret_cast<const f32x4 *>(vb + j * 16 * VS);
           const f32x4 vc = *reinterpret_cast<const f32x4 *>(vb + j * 16 * VS + 16);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) O[j] = mfma_16x16x4(va[r], s0[r], O[j]);
+          for (int r = 0; r < 4; ++r) O[j] = mfma_16x16x4(va[r], e0[r], O[j]);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) O[j] = mfma_16x16x4(vc[r], s1[r], O[j]);
+          for (int r = 0; r < 4; ++r) O[j] = mfma_16x16x4(vc[r], e1[r], O[j]);
         }
       }
     }

@@ -102,6 +102,9 @@ __device__ __forceinline__ float pair16_sum(float x) {
 constexpr float kRescaleSlack = 8.0f;
 // Initial reference: finite, so exp2(fma(-inf, c1, -m)) is exp2(-inf) = 0.
 constexpr float kNoMax = -3.402823466e38f;
+// A lane whose 8 terms of a tile, taken against the current reference, sum
+// to at most this (2^11 = 8 * 2^kRescaleSlack) needs no new reference.
+constexpr float kLazyLimit = 2048.0f;
 
 // Raw buffer access through an SGPR resource: the per-lane byte offset can
 // stay fixed for a whole walk, the tile base is a scalar offset, and any byte
@@ -114,6 +117,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, 
 }
 __device__ __forceinline__ f32x4 buffer_load4(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
   return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+__device__ __forceinline__ float buffer_load1(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
 }
 __device__ __forceinline__ void buffer_store4(f32x4 v, __amdgpu_buffer_rsrc_t r, int voff,
                                               int soff) {
