@@ -111,14 +111,53 @@ __device__ __forceinline__ int wave_first_active(const float *maskr, int L, int 
   return __builtin_amdgcn_readfirstlane(lo == 0x7fffffff ? 0 : lo);
 }
 
+// Row span of the mask, computed by one wave on its own (no barrier): first
+// and last active key (mask != 0), or (0, -1) for a row with none.
+__device__ __forceinline__ void wave_active_span(const float *maskr, int L, int lane, int &first,
+                                                 int &last) {
+  int lo = 0x7fffffff, hi = -1;
+  for (int k0 = 0; k0 < L; k0 += 64 * 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = maskr[min(k0 + lane + 64 * u, L - 1)];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int k = k0 + lane + 64 * u;
+      if (k < L && v[u] != 0.0f) {
+        lo = min(lo, k);
+        hi = max(hi, k);
+      }
+    }
+  }
+  lo = wave_min(lo);
+  hi = wave_max(hi);
+  first = __builtin_amdgcn_readfirstlane(hi >= 0 ? lo : 0);
+  last = __builtin_amdgcn_readfirstlane(hi);
+}
+
 // RMSNorm (lib.rs:676-691) and partial RoPE (692-709) of every key of one
 // (row, kv head) once per call, so attention workgroups stage finished keys.
 // One workgroup = 32 keys; output kp[row][kvh][key][HDP] (zero-padded past
 // hd), written in whole 16-byte chunks. Out: f32, or bf16 (RNE) for the
 // bf16 attention kernel. Every global load (keys, norm weights, RoPE table)
 // is issued before the first is used.
-template <int HDP, typename OutT>
-__global__ __launch_bounds__(256) void jeff_k_prep_kernel(const JeffArgs a, OutT *__restrict__ kp) {
+//
+// SPLIT (f32, HDP = 256, for the split-head kernel): each (row, kv head)
+// holds Lp = L rounded up to 16 keys, as blocks of 16 keys x 64 features
+// (tile kt, wave slice w) of 4 KB, each four 1 KB runs c: run c, 16-byte
+// chunk 16g + col is key 16kt + col, features 64w + 16c + 4g .. + 3. A
+// wave's load of run c is then one contiguous 1 KB read. Keys L .. Lp - 1
+// are written as zeros.
+__device__ __forceinline__ size_t split_kp_offset(int key, int d) {
+  const int kt = key >> 4, col = key & 15;
+  const int w = d >> 6, c = (d >> 4) & 3, g = (d >> 2) & 3, e = d & 3;
+  return ((size_t)(kt * 4 + w) * 4 + c) * 256 + (g * 16 + col) * 4 + e;
+}
+
+template <int HDP, typename OutT, bool SPLIT = false>
+__global__ __launch_bounds__(256) void jeff_k_prep_kernel(const JeffArgs a, OutT *__restrict__ kp,
+                                                          int *__restrict__ spans = nullptr,
+                                                          uint32_t *__restrict__ kbits = nullptr) {
   constexpr int DP = HDP / 8;  // dims per thread: 8 threads per key
   constexpr int KS = HDP + 1;
   constexpr int RT = (HDP / 2 + 7) / 8;  // RoPE pairs per thread, at most
@@ -135,6 +174,30 @@ __global__ __launch_bounds__(256) void jeff_k_prep_kernel(const JeffArgs a, OutT
   const bool kin = key < L;
   const bool rope = a.cos_t != nullptr && rh > 0;
   const int start = a.trim ? wave_first_active(a.mask + (size_t)row * L, L, lane) : 0;
+  if (SPLIT && blockIdx.x == 0 && blockIdx.y == 0 && tid < 64) {
+    // The row's active keys (mask != 0) for the split-head kernel: one bit
+    // per key (zero past L) and the (first, last) span, (0, -1) for a row
+    // with none.
+    const float *maskr = a.mask + (size_t)row * L;
+    uint32_t *bits = kbits + (size_t)row * ((L + 31) / 32);
+    int lo = 0x7fffffff, hi = -1;
+    for (int b0 = 0; b0 < L; b0 += 64) {
+      const float mv = maskr[min(b0 + lane, L - 1)];
+      const uint64_t bm = __ballot(b0 + lane < L && mv != 0.0f);
+      if (lane == 0) {
+        bits[b0 / 32] = (uint32_t)bm;
+        if (b0 + 32 < L) bits[b0 / 32 + 1] = (uint32_t)(bm >> 32);
+      }
+      if (bm != 0) {
+        lo = min(lo, b0 + (int)__builtin_ctzll(bm));
+        hi = max(hi, b0 + 63 - (int)__builtin_clzll(bm));
+      }
+    }
+    if (lane == 0) {
+      spans[2 * row] = hi >= 0 ? lo : 0;
+      spans[2 * row + 1] = hi;
+    }
+  }
 
   float xs[DP], wn[DP], c[RT], sn[RT];
 #pragma unroll
@@ -189,6 +252,20 @@ __global__ __launch_bounds__(256) void jeff_k_prep_kernel(const JeffArgs a, OutT
     }
   }
   __syncthreads();
+  if constexpr (SPLIT) {
+    static_assert(HDP == 256 && sizeof(OutT) == 4, "split layout: f32, HDP 256");
+    const int Lp = (L + 15) & ~15;
+    OutT *unit = kp + ((size_t)row * a.kv_heads + kvh) * (size_t)Lp * HDP;
+    const int nkeys = min(kKeyTile, Lp - k0);  // keys past L: zeros
+    for (int e = tid; e < nkeys * (HDP / 4); e += 256) {
+      const int k2 = e / (HDP / 4), d0 = (e % (HDP / 4)) * 4;
+      const float *src = &Kt[k2 * KS + d0];
+      const bool in = k0 + k2 < L;
+      const f32x4 o = in ? f32x4{src[0], src[1], src[2], src[3]} : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      *reinterpret_cast<f32x4 *>(unit + split_kp_offset(k0 + k2, d0)) = o;
+    }
+    return;
+  }
   OutT *dst = kp + (((size_t)row * a.kv_heads + kvh) * L + k0) * HDP;
   const int nkeys = min(kKeyTile, L - k0);
   constexpr int CH = 16 / (int)sizeof(OutT);  // elements per 16-byte chunk
@@ -211,30 +288,6 @@ __global__ __launch_bounds__(256) void jeff_k_prep_kernel(const JeffArgs a, OutT
 }
 
 // ----------------------------------------------------------- f32 attention
-
-// Row span of the mask, computed by one wave on its own (no barrier): first
-// and last active key (mask != 0), or (0, -1) for a row with none.
-__device__ __forceinline__ void wave_active_span(const float *maskr, int L, int lane, int &first,
-                                                 int &last) {
-  int lo = 0x7fffffff, hi = -1;
-  for (int k0 = 0; k0 < L; k0 += 64 * 8) {
-    float v[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = maskr[min(k0 + lane + 64 * u, L - 1)];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int k = k0 + lane + 64 * u;
-      if (k < L && v[u] != 0.0f) {
-        lo = min(lo, k);
-        hi = max(hi, k);
-      }
-    }
-  }
-  lo = wave_min(lo);
-  hi = wave_max(hi);
-  first = __builtin_amdgcn_readfirstlane(hi >= 0 ? lo : 0);
-  last = __builtin_amdgcn_readfirstlane(hi);
-}
 
 // RMSNorm + partial RoPE of one wave's 16 queries of one head into the
 // B-operand registers of S^T = K Q^T: lane (col, grp) ends with
@@ -510,7 +563,9 @@ struct JeffStage {
   }
 };
 
-template <int HDP, bool VEC>
+// TAG gives each calling kernel its own copy, compiled to that kernel's
+// register budget; TAG 1 (the split-head kernel) reads the split K layout.
+template <int HDP, bool VEC, int TAG = 0>
 __device__ __noinline__ void jeff_redo_wave(const JeffArgs a, const float *__restrict__ kp, int row,
                                             int head, int q0, int kt_begin, int kt_end, int start,
                                             float *ws);
@@ -739,7 +794,7 @@ __global__ __launch_bounds__(kJeffF32Waves * 64, 1) void jeff_attention_f32_kern
 // scores weigh 0, a +inf score empties the row) and o = sum p*v over
 // p != 0 in key order (lib.rs:716-754), then the gate. Kept out of line so
 // that its registers never weigh on the walk. ws: the wave's LDS rows.
-template <int HDP, bool VEC>
+template <int HDP, bool VEC, int TAG>
 __device__ __noinline__ void jeff_redo_wave(const JeffArgs a, const float *__restrict__ kp, int row,
                                             int head, int q0, int kt_begin, int kt_end, int start,
                                             float *ws) {
@@ -753,7 +808,9 @@ __device__ __noinline__ void jeff_redo_wave(const JeffArgs a, const float *__res
   const float *Q = static_cast<const float *>(a.q) + row * a.q_row + (size_t)head * hd * L;
   const float *Gt = static_cast<const float *>(a.gate) + row * a.q_row + (size_t)head * hd * L;
   const float *V = static_cast<const float *>(a.v) + row * a.kv_row + (size_t)kvh * hd * L;
-  const float *KP = kp + ((size_t)row * a.kv_heads + kvh) * L * HDP;
+  constexpr bool SPLIT = TAG == 1;
+  const size_t Lu = SPLIT ? (size_t)((L + 15) & ~15) : (size_t)L;
+  const float *KP = kp + ((size_t)row * a.kv_heads + kvh) * Lu * HDP;
   float *OUT = a.out + row * a.q_row + (size_t)head * hd * L;
   float qreg[QS];
   jeff_q_prep<HDP, VEC>(a, Q, q0, start, ws, qreg);
@@ -772,12 +829,16 @@ __device__ __noinline__ void jeff_redo_wave(const JeffArgs a, const float *__res
     const uint32_t abits = (uint32_t)__ballot(act) & 0xffffu;
     const uint32_t w = q_live ? (abits & range_bits(0, q - k0)) : 0u;
     if (__ballot(w != 0u) == 0) continue;
-    const float *krow = KP + (size_t)min(kc, L - 1) * HDP + grp * QS;
+    const int kcl = min(kc, L - 1);
+    const float *krow = KP + (size_t)kcl * HDP + grp * QS;
     f32x4 s;
 #pragma unroll
     for (int r = 0; r < 4; ++r) s[r] = 0.0f;
 #pragma unroll
-    for (int x = 0; x < QS; ++x) s = mfma_16x16x4(kc < L ? krow[x] : 0.0f, qreg[x], s);
+    for (int x = 0; x < QS; ++x) {
+      const float kx = SPLIT ? KP[split_kp_offset(kcl, grp * QS + x)] : krow[x];
+      s = mfma_16x16x4(kc < L ? kx : 0.0f, qreg[x], s);
+    }
     float mx = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -832,6 +893,395 @@ __device__ __noinline__ void jeff_redo_wave(const JeffArgs a, const float *__res
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   jeff_store<HDP, VEC>(a, Gt, OUT, q0, start, ws, O, inv);
+}
+
+// ------------------------------------------------- f32 attention, split head
+
+// One workgroup = 4 wavefronts = one (row, head, 16-query tile). Wave w owns
+// features [w*DS, (w+1)*DS) of the head (DS = HDP/4 = 64) in both products:
+//   S^T_w (16 keys x 16 queries) = K[keys, slice w] Q[queries, slice w]^T  (16 MFMA 16x16x4)
+//   S^T = sum over w of S^T_w, exchanged through LDS, one barrier per tile
+//   O^T[slice w] += V[slice w]^T P^T                                       (16 MFMA 16x16x4)
+// so a query tile's key walk runs on four SIMDs at once, and the longest
+// tiles (the last query tiles of full rows) no longer bound the kernel.
+// Every wave holds the same scores and runs the same softmax, so all control
+// flow is workgroup-uniform.
+//
+// Memory: K comes from the prep workspace in the split layout (each wave's
+// run of a tile is one contiguous 1 KB read), V columns straight from V, one
+// tile ahead, into registers. Q, the gate and the output move along tokens
+// 16 bytes at a time and are transposed in the wave's own LDS rows, so a
+// wave issues four vector memory instructions per tensor. The row's key span
+// and active-key bits come from the prep (scalar loads).
+//
+// Workgroups are numbered from the last query tile down, so the longest
+// causal walks start first; within one query tile, the workgroups of one
+// (row, kv head) share an id residue mod 8 (one XCD, one L2) when the counts
+// allow it.
+template <int HDP>
+__global__ __launch_bounds__(256, 3) void jeff_split_f32_kernel(const JeffArgs a,
+                                                                const float *__restrict__ kp,
+                                                                const int *__restrict__ spans,
+                                                                const uint32_t *__restrict__ kbits,
+                                                                int rows) {
+  static_assert(HDP == 256, "split-head kernel: four 64-feature slices");
+  constexpr int DS = HDP / 4;    // features per wave
+  constexpr int QS = DS / 4;     // Q registers per lane: MFMA steps per tile
+  constexpr int NB = DS / 16;    // 16-feature blocks of O^T per wave
+  constexpr int KT = kJeffKeyTile;
+  constexpr int QW = DS + 4;     // wave rows [query][feature] for Q
+  constexpr int OW = 16 + 4;     // wave rows [feature][query] for the output
+  constexpr int WROWS = DS * OW > 16 * QW ? DS * OW : 16 * QW;
+  constexpr int QP = HDP + 4;    // whole-tile Q rows (RoPE widths other than 16, 32)
+  constexpr int WAREA = 4 * WROWS > 16 * QP ? 4 * WROWS : 16 * QP;
+  constexpr int SX = 2 * 4 * 64 * 4;  // score exchange: 2 buffers x 4 waves x 64 lanes x f32x4
+  __shared__ __attribute__((aligned(16))) float smem[WAREA + SX];
+  __shared__ float s_ssq[4 * 16];
+  __shared__ __attribute__((aligned(16))) float s_inv[4 * 16];
+  __shared__ int s_bad;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15, grp = lane >> 4;
+  const int L = a.L, hd = a.hd, heads = a.heads, G = a.groups;
+
+  // -------- work item
+  const int nq = (L + 15) / 16;
+  const int units = rows * heads;
+  const int p = blockIdx.x;
+  const int qt = nq - 1 - p / units;
+  int u = p % units, row, head;
+  if (units % 8 == 0 && (rows * a.kv_heads) % 8 == 0) {
+    const int x = u % 8, i = u / 8;
+    const int kvu = x + 8 * (i / G);  // (row, kv head) unit of XCD x
+    row = kvu / a.kv_heads;
+    head = (kvu % a.kv_heads) * G + i % G;
+  } else {
+    row = u / heads;
+    head = u % heads;
+  }
+  const int kvh = min(head / G, a.kv_heads - 1);
+  const int q0 = qt * 16, q = q0 + col;
+  const float *Q = static_cast<const float *>(a.q) + row * a.q_row + (size_t)head * hd * L;
+  const float *Gt = static_cast<const float *>(a.gate) + row * a.q_row + (size_t)head * hd * L;
+  const float *V = static_cast<const float *>(a.v) + row * a.kv_row + (size_t)kvh * hd * L;
+  const int Lp = (L + 15) & ~15;
+  const float *KP = kp + ((size_t)row * a.kv_heads + kvh) * (size_t)Lp * HDP;
+  const uint32_t *rbits = kbits + (size_t)row * ((L + 31) / 32);
+  float *OUT = a.out + row * a.q_row + (size_t)head * hd * L;
+  float *ww = smem + wave * WROWS;  // this wave's rows
+
+  // This lane's features in both products: step (c, e) of the 16x16x4 MFMA
+  // chain uses feature d0 + 16c + e (the prep workspace's run order).
+  const int d0 = wave * DS + 4 * grp;
+  // Along-token tasks of the wave's slice (Q, gate, output): task t is
+  // feature wave*DS + (lane >> 2) + 16t, tokens q0 + 4*(lane & 3) .. + 3.
+  const int tdl = lane >> 2, tg4 = lane & 3;
+
+  // -------- loads that need nothing: the row's key span, the diagonal key
+  // tile (the walk runs from it down to the row's first active key).
+  // K: key k0 + col, features d0 + 16c .. + 3 = run c of the tile's block
+  // for this wave, chunk lane (zero past hd and past L). V: V[wave*DS + 16j
+  // + col][k0 + 4*grp .. + 3].
+  const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(KP, (uint32_t)((size_t)Lp * HDP * 4));
+  const __amdgpu_buffer_rsrc_t rv = buffer_rsrc(V, (uint32_t)((size_t)hd * L * 4));
+  const int okk = wave * 4096 + lane * 16;
+  const int ovv = ((wave * DS + col) * L + 4 * grp) * 4;
+  f32x4 kc[QS / 4], vc[NB], kn[QS / 4], vn[NB];
+  auto fetch = [&](int k0, f32x4 (&kr)[QS / 4], f32x4 (&vr)[NB]) {
+    k0 = __builtin_amdgcn_readfirstlane(k0);  // uniform: scalar offsets, no waterfall
+#pragma unroll
+    for (int c = 0; c < QS / 4; ++c) kr[c] = buffer_load4(rk, okk + 1024 * c, k0 * HDP * 4);
+#pragma unroll
+    for (int j = 0; j < NB; ++j) vr[j] = buffer_load4(rv, ovv + j * 16 * L * 4, k0 * 4);
+  };
+  const int first = spans[2 * row], last = spans[2 * row + 1];
+  fetch(qt * KT, kc, vc);
+  const int start = (a.trim && last >= 0) ? first : 0;
+  const bool q_live = q < L && q >= start;
+  const int q_last = min(q0 + 15, L - 1);
+  int kt_begin = 0, kt_end = 0;
+  {
+    const int kl = min(last, q_last);
+    if (last >= 0 && first <= kl && q_last >= start) {
+      kt_begin = first / KT;
+      kt_end = kl / KT + 1;
+    }
+  }
+  kt_begin = __builtin_amdgcn_readfirstlane(kt_begin);
+  kt_end = __builtin_amdgcn_readfirstlane(kt_end);
+
+  const __amdgpu_buffer_rsrc_t rg = buffer_rsrc(Gt, (uint32_t)((size_t)hd * L * 4));
+  const __amdgpu_buffer_rsrc_t ro = buffer_rsrc(OUT, (uint32_t)((size_t)hd * L * 4));
+  const __amdgpu_buffer_rsrc_t rq = buffer_rsrc(Q, (uint32_t)((size_t)hd * L * 4));
+  const int otask = ((wave * DS + tdl) * L + 4 * tg4) * 4;  // byte offset of task 0
+  f32x4 gv[NB];
+  auto load_gate = [&]() {
+#pragma unroll
+    for (int t = 0; t < NB; ++t) gv[t] = buffer_load4(rg, otask + t * 16 * L * 4, q0 * 4);
+  };
+  // o * sigmoid(gate) (lib.rs:755-758) for task t, o = O^T * inv; 0 for a
+  // dropped query (q < start). L % 4 == 0: a task's 4 tokens are all in or
+  // all out.
+  auto store_task = [&](int t, f32x4 o) {
+    const int qa = q0 + 4 * tg4, d = wave * DS + tdl + 16 * t;
+    f32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = qa + i < start ? 0.0f : o[i] * fast_sigmoid(gv[t][i]);
+    if (qa < L && d < hd) buffer_store4(r, ro, otask + t * 16 * L * 4, q0 * 4);
+  };
+  if (kt_begin >= kt_end) {
+    // No key at or before these queries: o = 0 (lib.rs:739-743).
+    load_gate();
+#pragma unroll
+    for (int t = 0; t < NB; ++t) store_task(t, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+    return;
+  }
+
+  // -------- Q: the wave's slice along tokens, transposed through its LDS
+  // rows into this lane's B operands (feature d0 + 16c + e of query q0 +
+  // col; features past hd read as 0); its norm weights and, where the RoPE
+  // partners sit in the same lane (rot/2 = 16 or 32: partner of step (c, e)
+  // is (c + rot/32, e)), its table entries.
+  const int rh = a.rot_half;
+  const bool rope = a.cos_t != nullptr && rh > 0;
+  const bool lane_rope = rh == 16 || rh == 32;
+  f32x4 qx[NB];
+#pragma unroll
+  for (int t = 0; t < NB; ++t) qx[t] = buffer_load4(rq, otask + t * 16 * L * 4, q0 * 4);
+  const __amdgpu_buffer_rsrc_t rn = buffer_rsrc(a.q_norm, (uint32_t)(hd * 4));
+  f32x4 wv[QS / 4];
+#pragma unroll
+  for (int c = 0; c < QS / 4; ++c) wv[c] = buffer_load4(rn, (d0 + 16 * c) * 4, 0);
+  f32x4 tc[2], ts[2];  // wave 0, lane_rope: table entries of pairs i = 4*grp + 16c + e, c < rh/16
+  if (rope && lane_rope && wave == 0) {
+    const size_t pos = (size_t)min(max(q - start, 0), L - 1) * rh;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int i = min(4 * grp + 16 * c, rh - 4);
+      tc[c] = *reinterpret_cast<const f32x4 *>(a.cos_t + pos + i);
+      ts[c] = *reinterpret_cast<const f32x4 *>(a.sin_t + pos + i);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < NB; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ww[(4 * tg4 + i) * QW + tdl + 16 * t] = qx[t][i];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float qv[QS];
+#pragma unroll
+  for (int c = 0; c < QS / 4; ++c) {
+    const f32x4 y = *reinterpret_cast<const f32x4 *>(ww + col * QW + 4 * grp + 16 * c);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) qv[4 * c + e] = y[e];
+  }
+
+  // -------- RMSNorm (lib.rs:676-691): the sum of squares over the four
+  // waves' slices through LDS, then partial RoPE (692-709).
+  if (tid == 0) s_bad = 0;
+  float ss = 0.0f;
+#pragma unroll
+  for (int c = 0; c < QS / 4; ++c)
+    ss += qv[4 * c] * qv[4 * c] + qv[4 * c + 1] * qv[4 * c + 1] + qv[4 * c + 2] * qv[4 * c + 2] +
+          qv[4 * c + 3] * qv[4 * c + 3];
+  ss = pair_sum(pair16_sum(ss));
+  if (grp == 0) s_ssq[wave * 16 + col] = ss;
+  __syncthreads();
+  const float tot = s_ssq[col] + s_ssq[16 + col] + s_ssq[32 + col] + s_ssq[48 + col];
+  const float scale = rms_scale(tot, hd, a.eps);
+  float qreg[QS];
+#pragma unroll
+  for (int c = 0; c < QS / 4; ++c)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int d = d0 + 16 * c + e;
+      qreg[4 * c + e] = (q_live && d < hd) ? rms_apply(qv[4 * c + e], scale, wv[c][e]) : 0.0f;
+    }
+  if (rope && lane_rope) {
+    if (wave == 0 && q_live) {
+      const int pc = rh / 16;  // register-block offset of the partner
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+        if (c < pc) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float x = qreg[4 * c + e], y = qreg[4 * (c + pc) + e];
+            qreg[4 * c + e] = rope_lo(x, y, tc[c][e], ts[c][e]);
+            qreg[4 * (c + pc) + e] = rope_hi(x, y, tc[c][e], ts[c][e]);
+          }
+        }
+    }
+  } else if (rope) {
+    // Any other rotary width: rotate the normalized rows of the whole tile
+    // in LDS (the wave rows are free again).
+    float *Qs = smem;
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < QS / 4; ++c)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) Qs[col * QP + d0 + 16 * c + e] = qreg[4 * c + e];
+    __syncthreads();
+    const int qi = tid & 15, qa = q0 + qi;
+    if (qa < L && qa >= start) {
+      const size_t pq = (size_t)(qa - start) * rh;
+      float *qr = Qs + qi * QP;
+      for (int i = tid >> 4; i < rh; i += 16) {
+        const float x = qr[i], y = qr[i + rh];
+        const float c = a.cos_t[pq + i], sn = a.sin_t[pq + i];
+        qr[i] = rope_lo(x, y, c, sn);
+        qr[i + rh] = rope_hi(x, y, c, sn);
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < QS / 4; ++c)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) qreg[4 * c + e] = Qs[col * QP + d0 + 16 * c + e];
+    __syncthreads();  // the tile rows become wave rows again
+  }
+  f32x4 *sx = reinterpret_cast<f32x4 *>(smem + WAREA);
+
+  // Keep word of a 16-key tile for query col: active key (the prep's bits:
+  // mask != 0, zero past L), key <= query (lib.rs:716). Keys before `start`
+  // are inactive by definition of start.
+  auto keep_word = [&](int kt) -> uint32_t {
+    const uint32_t abits = (rbits[kt >> 1] >> (16 * (kt & 1))) & 0xffffu;
+    return q_live ? (abits & range_bits(0, q - kt * KT)) : 0u;
+  };
+
+  f32x4 O[NB];
+#pragma unroll
+  for (int j = 0; j < NB; ++j) O[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float m = kNoMax, l = 0.0f;  // l: this lane's share of the row sum
+  const float c1 = a.c1;
+
+  // -------- the walk, from the last key tile down (exponents against a
+  // lazily moved reference, as in the Laya kernel; the order of the keys
+  // only moves rounding). A workgroup whose kept scores sum to NaN or inf
+  // stops computing; it, or one whose O took a NaN or inf, redoes the tile
+  // with the reference's exact semantics afterwards. The gate loads go out
+  // with the last tile.
+  const int kt_hi = kt_end - 1;
+  if (kt_hi != qt) fetch(kt_hi * KT, kc, vc);  // the span ends before the diagonal
+  uint32_t w = keep_word(kt_hi);
+  bool tainted = false;  // workgroup-uniform
+  int xb = 0;            // exchange buffer
+  for (int kt = kt_hi; kt >= kt_begin; --kt) {
+    const bool more = kt > kt_begin;
+    if (more)
+      fetch((kt - 1) * KT, kn, vn);
+    else
+      load_gate();
+    if (kt * KT + KT > L) {  // the row's last, partial tile: V past L is another feature's
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) vc[j][t] = kt * KT + 4 * grp + t < L ? vc[j][t] : 0.0f;
+    }
+    if (!tainted && __ballot(w != 0u) != 0) {  // workgroup-uniform: every wave has the same w
+      f32x4 s0 = {0.0f, 0.0f, 0.0f, 0.0f}, s1 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int c = 0; c < QS / 4; ++c) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (c & 1)
+            s1 = mfma_16x16x4(kc[c][e], qreg[4 * c + e], s1);
+          else
+            s0 = mfma_16x16x4(kc[c][e], qreg[4 * c + e], s0);
+        }
+      }
+      sx[(xb * 4 + wave) * 64 + lane] = s0 + s1;
+      __syncthreads();
+      f32x4 s = sx[(xb * 4 + 0) * 64 + lane];
+#pragma unroll
+      for (int v = 1; v < 4; ++v) s += sx[(xb * 4 + v) * 64 + lane];
+      xb ^= 1;
+      // lane group g holds keys 4g + r of its query
+      if (__ballot(q_live && w != 0xffffu) != 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s[r] = ((w >> (4 * grp + r)) & 1u) ? s[r] : -INFINITY;
+      }
+      f32x4 ex;
+      float rs = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        ex[r] = fast_exp2(__builtin_fmaf(s[r], c1, -m));
+        rs += ex[r];
+      }
+      bool ok = true;
+      if (__ballot(q_live && !(rs <= kLazyLimit)) != 0) {
+        const float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+        const float mxs = pair_max(pair16_max(mx)) * c1;
+        const bool need = mxs > m + kRescaleSlack;
+        const float mn = need ? mxs : m;
+        rs = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          ex[r] = fast_exp2(__builtin_fmaf(s[r], c1, -mn));
+          rs += ex[r];
+        }
+        if (__ballot(q_live && !__builtin_isfinite(rs)) != 0) {
+          tainted = true;
+          ok = false;
+        } else {
+          const float alpha = fast_exp2(m - mn);  // exactly 1 where the reference stays
+#pragma unroll
+          for (int j = 0; j < NB; ++j) O[j] *= alpha;
+          l *= alpha;
+          m = mn;
+        }
+      }
+      if (ok) {
+        l += rs;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int j = 0; j < NB; ++j) O[j] = mfma_16x16x4(vc[j][r], ex[r], O[j]);
+      }
+    }
+    if (more) {
+#pragma unroll
+      for (int c = 0; c < QS / 4; ++c) kc[c] = kn[c];
+#pragma unroll
+      for (int j = 0; j < NB; ++j) vc[j] = vn[j];
+      w = keep_word(kt - 1);
+    }
+  }
+
+  // -------- careful redo (rare): the scores (shared) or this wave's O went
+  // non-finite; one wave redoes the whole tile from global memory.
+  bool bad = false;
+#pragma unroll
+  for (int j = 0; j < NB; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) bad |= !__builtin_isfinite(O[j][r]);
+  if (__ballot(q_live && bad) != 0 && lane == 0) s_bad = 1;
+  __syncthreads();
+  if (tainted || s_bad != 0) {
+    if (wave == 0) jeff_redo_wave<HDP, true, 1>(a, kp, row, head, q0, kt_begin, kt_end, start, smem);
+    return;
+  }
+
+  // -------- o / sum (0 when nothing was kept), sigmoid gate, store: O^T
+  // through the wave's rows [feature][query] so that each task stores 4
+  // tokens of one feature.
+  const float lt = pair_sum(pair16_sum(l));
+  if (grp == 0) s_inv[wave * 16 + col] = lt > 0.0f ? fast_rcp(lt) : 0.0f;
+#pragma unroll
+  for (int j = 0; j < NB; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) ww[(16 * j + 4 * grp + r) * OW + col] = O[j][r];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const f32x4 inv4 = *reinterpret_cast<const f32x4 *>(s_inv + wave * 16 + 4 * tg4);
+#pragma unroll
+  for (int t = 0; t < NB; ++t) {
+    const f32x4 o = *reinterpret_cast<const f32x4 *>(ww + (tdl + 16 * t) * OW + 4 * tg4);
+    store_task(t, o * inv4);
+  }
 }
 
 // ---------------------------------------------------------- bf16 attention
@@ -1179,12 +1629,18 @@ __global__ __launch_bounds__(256, 2) void jeff_attention_bf16_kernel(const JeffA
 
 // ----------------------------------------------------------------- launchers
 
+// Workspace: the prepared keys (per row and kv head, keys rounded up to 16
+// for the split-head kernel's padded blocks), then one (first, last) key
+// span per row and the rows' active-key bits (32 keys per word).
+static size_t jeff_kp_main_bytes(const JeffArgs &a, int rows, int hd_pad, bool bf16) {
+  const size_t Lp = ((size_t)a.L + 15) & ~(size_t)15;
+  const size_t b = (size_t)rows * a.kv_heads * Lp * hd_pad * (bf16 ? 2 : 4);
+  return (b + 255) & ~(size_t)255;
+}
+
 template <int HDP>
 static hipError_t launch_jeff_f32_hd(const JeffArgs &a, int rows, float *kp, hipStream_t stream) {
   dim3 pgrid((a.L + kKeyTile - 1) / kKeyTile, a.kv_heads, rows);
-  hipLaunchKernelGGL((jeff_k_prep_kernel<HDP, float>), pgrid, dim3(256), 0, stream, a, kp);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
   // Query tiles of 16 in causal pairs, kJeffF32Waves / heads_per_group tiles
   // (half as many pairs) per workgroup.
   const int nq = (a.L + kJeffWaveQueries - 1) / kJeffWaveQueries;
@@ -1197,7 +1653,27 @@ static hipError_t launch_jeff_f32_hd(const JeffArgs &a, int rows, float *kp, hip
   const uintptr_t bases = reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.v) |
                           reinterpret_cast<uintptr_t>(a.gate) | reinterpret_cast<uintptr_t>(a.out);
   const bool vec = a.L % 4 == 0 && (bases & 15) == 0 &&
-                   (size_t)a.L * (size_t)HDP * 4 < ((size_t)1 << 31);
+                   ((size_t)a.L + 15) * (size_t)HDP * 4 < ((size_t)1 << 31);
+  if constexpr (HDP == 256) {
+    // Buffer offsets of the split kernel: one head's (hd, L) block and one
+    // kv head's padded K blocks within 2 GiB (checked above, L + 15 < 2^21).
+    if (vec) {
+      int *spans = reinterpret_cast<int *>(reinterpret_cast<char *>(kp) +
+                                           jeff_kp_main_bytes(a, rows, HDP, false));
+      uint32_t *kbits = reinterpret_cast<uint32_t *>(spans + 2 * rows);
+      hipLaunchKernelGGL((jeff_k_prep_kernel<HDP, float, true>), pgrid, dim3(256), 0, stream, a,
+                         kp, spans, kbits);
+      hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return e;
+      const dim3 sgrid(nq * rows * a.heads);
+      hipLaunchKernelGGL((jeff_split_f32_kernel<HDP>), sgrid, dim3(256), 0, stream, a, kp, spans,
+                         kbits, rows);
+      return hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((jeff_k_prep_kernel<HDP, float>), pgrid, dim3(256), 0, stream, a, kp);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
   const dim3 block(kJeffF32Waves * 64);
   if (vec)
     hipLaunchKernelGGL((jeff_attention_f32_kernel<HDP, true>), grid, block, 0, stream, a, kp);
@@ -1219,7 +1695,8 @@ hipError_t launch_jeff_attention_f32(const JeffArgs &a, int rows, int hd_pad, vo
 }
 
 size_t jeff_kp_bytes(const JeffArgs &a, int rows, int hd_pad, bool bf16) {
-  return (size_t)rows * a.kv_heads * a.L * hd_pad * (bf16 ? 2 : 4);
+  return jeff_kp_main_bytes(a, rows, hd_pad, bf16) + (size_t)rows * 2 * sizeof(int) +
+         (size_t)rows * ((a.L + 31) / 32) * sizeof(uint32_t);
 }
 
 template <int HDP>

@@ -121,6 +121,9 @@ __device__ __forceinline__ f32x4 buffer_load4(__amdgpu_buffer_rsrc_t r, int voff
 __device__ __forceinline__ float buffer_load1(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
 }
+__device__ __forceinline__ void buffer_store1(float v, __amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, voff, soff, 0);
+}
 __device__ __forceinline__ void buffer_store4(f32x4 v, __amdgpu_buffer_rsrc_t r, int voff,
                                               int soff) {
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, v), r, voff, soff, 0);

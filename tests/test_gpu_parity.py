@@ -292,10 +292,10 @@ def test_jeff_masked_nonfinite_values_and_empty_rows(gpu_ctx):
     assert np.all(out[:, :3] == 0.0)  # no active key at or before these queries
 
 
-@pytest.mark.parametrize("hd", [16, 256])
-def test_jeff_kept_nonfinite_values_propagate(gpu_ctx, hd):
+@pytest.mark.parametrize("hd,length", [(16, 50), (256, 50), (256, 52)])
+def test_jeff_kept_nonfinite_values_propagate(gpu_ctx, hd, length):
     """Kept inf / NaN values reach exactly the outputs whose p is non-zero."""
-    length, heads = 50, 2
+    heads = 2
     q, k, v, g, qn, kn, mask = jeff_case(9, length, heads, hd, heads, False)
     mask[:4] = 0.0
     V = v.reshape(heads * hd, length)
@@ -311,6 +311,54 @@ def test_jeff_kept_nonfinite_values_propagate(gpu_ctx, hd):
     assert np.array_equal(np.isneginf(got), np.isneginf(want))
     fin = np.isfinite(want)
     assert np.abs(got[fin] - want[fin]).max() <= F32_TOL
+
+
+@pytest.mark.parametrize("length", [4, 16, 20, 48, 68, 132, 256])
+def test_jeff_split_head_rows_match_oracle(gpu_ctx, length):
+    """hd 256 with L % 4 == 0 (the split-head kernel): GQA rows with left
+    padding, an interior hole and a fully padded row, with and without
+    trimming."""
+    rows, heads, kv, hd, rot = 3, 4, 2, 256, 64
+    rng = Lcg(length + 1000)
+    W, KW = heads * hd, kv * hd
+    q = rng.normal(rows * length * W).astype(np.float32)
+    g = rng.normal(rows * length * W).astype(np.float32)
+    k = rng.normal(rows * length * KW).astype(np.float32)
+    v = rng.normal(rows * length * KW).astype(np.float32)
+    qn = (rng.normal(hd) * 0.1).astype(np.float32)
+    kn = (rng.normal(hd) * 0.1).astype(np.float32)
+    mask = np.ones(rows * length, np.float32)
+    mask[length // 2] = 0.0                        # row 0: interior hole
+    mask[length:length + length // 3 + 1] = 0.0    # row 1: left padding
+    mask[2 * length:] = 0.0                        # row 2: nothing active
+    for trim in (False, True):
+        want = oracle.jeff_rows(q, k, v, g, qn, kn, mask, rows, length, heads, kv, hd, rot,
+                                1e7, 1e-6, trim_leading=trim)
+        got = te.jeff_full_attention_rows(q, k, v, g, qn, kn, mask, rows, length, heads, kv, hd,
+                                          rot, 1e7, 1e-6, trim_leading=trim, ctx=gpu_ctx)
+        assert_close(got, want, F32_TOL)
+
+
+@pytest.mark.parametrize("where", ["k_nan", "k_inf", "q_nan"])
+def test_jeff_split_head_nonfinite_scores(gpu_ctx, where):
+    """NaN / inf scores on the split-head kernel's path (hd 256, L % 4 == 0)
+    match the reference's NaN / inf pattern and finite values."""
+    length, heads, hd = 52, 2, 256
+    q, k, v, g, qn, kn, mask = jeff_case(11, length, heads, hd, heads, False)
+    mask[:3] = 0.0
+    K = k.reshape(heads * hd, length)
+    Q = q.reshape(heads * hd, length)
+    if where == "k_nan":
+        K[7, 20] = np.nan      # kept from query 20 on
+        K[9, 1] = np.nan       # masked key: must not leak
+    elif where == "k_inf":
+        K[hd + 3, 30] = np.inf
+    else:
+        Q[5, 40] = np.nan
+    want = oracle.jeff_full_attention(q, k, v, g, qn, kn, mask, length, heads, hd, 64, 1e7, 1e-6)
+    got = np.asarray(te.jeff_full_attention(q, k, v, g, qn, kn, mask, heads, hd, 64, 1e7, 1e-6,
+                                            q_shape=(length, heads * hd), ctx=gpu_ctx))
+    assert_same_nonfinite(got, want, F32_TOL)
 
 
 def test_jeff_c4_full_gqa_and_dropin(gpu_ctx):
