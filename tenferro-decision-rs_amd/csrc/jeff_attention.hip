@@ -135,29 +135,27 @@ __device__ __forceinline__ void wave_active_span(const float *maskr, int L, int 
   last = __builtin_amdgcn_readfirstlane(hi);
 }
 
-// RMSNorm (lib.rs:676-691) and partial RoPE (692-709) of every key of one
-// (row, kv head) once per call, so attention workgroups stage finished keys.
-// One workgroup = 32 keys; output kp[row][kvh][key][HDP] (zero-padded past
-// hd), written in whole 16-byte chunks. Out: f32, or bf16 (RNE) for the
-// bf16 attention kernel. Every global load (keys, norm weights, RoPE table)
-// is issued before the first is used.
-//
-// SPLIT (f32, HDP = 256, for the split-head kernel): each (row, kv head)
-// holds Lp = L rounded up to 16 keys, as blocks of 16 keys x 64 features
-// (tile kt, wave slice w) of 4 KB, each four 1 KB runs c: run c, 16-byte
-// chunk 16g + col is key 16kt + col, features 64w + 16c + 4g .. + 3. A
-// wave's load of run c is then one contiguous 1 KB read. Keys L .. Lp - 1
-// are written as zeros.
+// Split layout (f32, HDP = 256, for the split-head kernel): each (row, kv
+// head) holds Lp = L rounded up to 16 keys, as blocks of 16 keys x 64
+// features (tile kt, wave slice w) of 4 KB, each four 1 KB runs c: run c,
+// 16-byte chunk 16g + col is key 16kt + col, features 64w + 16c + 4g .. + 3.
+// A wave's load of run c is then one contiguous 1 KB read. Keys L .. Lp - 1
+// hold zeros.
 __device__ __forceinline__ size_t split_kp_offset(int key, int d) {
   const int kt = key >> 4, col = key & 15;
   const int w = d >> 6, c = (d >> 4) & 3, g = (d >> 2) & 3, e = d & 3;
   return ((size_t)(kt * 4 + w) * 4 + c) * 256 + (g * 16 + col) * 4 + e;
 }
 
-template <int HDP, typename OutT, bool SPLIT = false>
-__global__ __launch_bounds__(256) void jeff_k_prep_kernel(const JeffArgs a, OutT *__restrict__ kp,
-                                                          int *__restrict__ spans = nullptr,
-                                                          uint32_t *__restrict__ kbits = nullptr) {
+// RMSNorm (lib.rs:676-691) and partial RoPE (692-709) of every key of one
+// (row, kv head) once per call, so attention workgroups stage finished keys.
+// One workgroup = 32 keys; output kp[row][kvh][key][HDP] (zero-padded past
+// hd), written in whole 16-byte chunks. Out: f32, or bf16 (RNE) for the
+// bf16 attention kernel. Every global load (keys, norm weights, RoPE table)
+// is issued before the first is used.
+
+template <int HDP, typename OutT>
+__global__ __launch_bounds__(256) void jeff_k_prep_kernel(const JeffArgs a, OutT *__restrict__ kp) {
   constexpr int DP = HDP / 8;  // dims per thread: 8 threads per key
   constexpr int KS = HDP + 1;
   constexpr int RT = (HDP / 2 + 7) / 8;  // RoPE pairs per thread, at most
@@ -174,31 +172,6 @@ __global__ __launch_bounds__(256) void jeff_k_prep_kernel(const JeffArgs a, OutT
   const bool kin = key < L;
   const bool rope = a.cos_t != nullptr && rh > 0;
   const int start = a.trim ? wave_first_active(a.mask + (size_t)row * L, L, lane) : 0;
-  if (SPLIT && blockIdx.x == 0 && blockIdx.y == 0 && tid < 64) {
-    // The row's active keys (mask != 0) for the split-head kernel: one bit
-    // per key (zero past L) and the (first, last) span, (0, -1) for a row
-    // with none.
-    const float *maskr = a.mask + (size_t)row * L;
-    uint32_t *bits = kbits + (size_t)row * ((L + 31) / 32);
-    int lo = 0x7fffffff, hi = -1;
-    for (int b0 = 0; b0 < L; b0 += 64) {
-      const float mv = maskr[min(b0 + lane, L - 1)];
-      const uint64_t bm = __ballot(b0 + lane < L && mv != 0.0f);
-      if (lane == 0) {
-        bits[b0 / 32] = (uint32_t)bm;
-        if (b0 + 32 < L) bits[b0 / 32 + 1] = (uint32_t)(bm >> 32);
-      }
-      if (bm != 0) {
-        lo = min(lo, b0 + (int)__builtin_ctzll(bm));
-        hi = max(hi, b0 + 63 - (int)__builtin_clzll(bm));
-      }
-    }
-    if (lane == 0) {
-      spans[2 * row] = hi >= 0 ? lo : 0;
-      spans[2 * row + 1] = hi;
-    }
-  }
-
   float xs[DP], wn[DP], c[RT], sn[RT];
 #pragma unroll
   for (int i = 0; i < DP; ++i) {
@@ -252,20 +225,6 @@ __global__ __launch_bounds__(256) void jeff_k_prep_kernel(const JeffArgs a, OutT
     }
   }
   __syncthreads();
-  if constexpr (SPLIT) {
-    static_assert(HDP == 256 && sizeof(OutT) == 4, "split layout: f32, HDP 256");
-    const int Lp = (L + 15) & ~15;
-    OutT *unit = kp + ((size_t)row * a.kv_heads + kvh) * (size_t)Lp * HDP;
-    const int nkeys = min(kKeyTile, Lp - k0);  // keys past L: zeros
-    for (int e = tid; e < nkeys * (HDP / 4); e += 256) {
-      const int k2 = e / (HDP / 4), d0 = (e % (HDP / 4)) * 4;
-      const float *src = &Kt[k2 * KS + d0];
-      const bool in = k0 + k2 < L;
-      const f32x4 o = in ? f32x4{src[0], src[1], src[2], src[3]} : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      *reinterpret_cast<f32x4 *>(unit + split_kp_offset(k0 + k2, d0)) = o;
-    }
-    return;
-  }
   OutT *dst = kp + (((size_t)row * a.kv_heads + kvh) * L + k0) * HDP;
   const int nkeys = min(kKeyTile, L - k0);
   constexpr int CH = 16 / (int)sizeof(OutT);  // elements per 16-byte chunk
@@ -284,6 +243,159 @@ __global__ __launch_bounds__(256) void jeff_k_prep_kernel(const JeffArgs a, OutT
       const f32x4 o = {src[0], src[1], src[2], src[3]};
       *reinterpret_cast<f32x4 *>(dst + (size_t)k2 * HDP + d0) = o;
     }
+  }
+}
+
+// K prep for the split-head kernel (f32, HDP = 256): one workgroup = one
+// 16-key tile of one (row, kv head), written in the split layout above. K
+// arrives along keys (16-byte loads, four per thread) and is transposed
+// through LDS; thread (key tid & 15, part tid >> 4) then owns features
+// 16*part .. + 15 of its key: RMSNorm (lib.rs:676-691) with the sum of
+// squares reduced over parts by lane swaps and LDS, partial RoPE (692-709)
+// in registers when the partner feature i + rot/2 sits in the same lane
+// (rot/2 = 32: part p pairs with part p + 2, lane + 32), else through LDS.
+// Workgroups with blockIdx.x == 0 and kv head 0 also write the row's
+// active-key bits and key span.
+__global__ __launch_bounds__(256) void jeff_k_prep_split_kernel(const JeffArgs a,
+                                                                float *__restrict__ kp,
+                                                                int *__restrict__ spans,
+                                                                uint32_t *__restrict__ kbits) {
+  constexpr int HDP = 256, KS = HDP + 4;
+  __shared__ __attribute__((aligned(16))) float Kt[16 * KS];
+  __shared__ float s_red[4 * 16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int row = blockIdx.z, kvh = blockIdx.y, kt = blockIdx.x;
+  const int L = a.L, hd = a.hd, rh = a.rot_half;
+  const int k0 = kt * 16;
+  const float *maskr = a.mask + (size_t)row * L;
+  const float *K = static_cast<const float *>(a.k) + row * a.kv_row + (size_t)kvh * hd * L;
+
+  // Raw tile along keys: task (feature d, keys k0 + 4*g4 .. + 3), L % 4 == 0;
+  // features past hd and keys past L read as 0.
+  const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(K, (uint32_t)((size_t)hd * L * 4));
+  f32x4 x[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int e = tid + 256 * t, d = e >> 2, g4 = e & 3;
+    x[t] = buffer_load4(rk, (d * L + 4 * g4) * 4, k0 * 4);
+  }
+  const int key = k0 + (tid & 15), part = tid >> 4;
+  const bool kin = key < L;
+  const __amdgpu_buffer_rsrc_t rn = buffer_rsrc(a.k_norm, (uint32_t)(hd * 4));
+  f32x4 wn[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) wn[c] = buffer_load4(rn, (16 * part + 4 * c) * 4, 0);
+  const bool rope = a.cos_t != nullptr && rh > 0;
+  const int start = a.trim ? wave_first_active(maskr, L, lane) : 0;
+  const size_t pos = (size_t)min(max(key - start, 0), L - 1) * rh;
+  f32x4 tc[4], ts[4];  // rot/2 == 32, wave 0: pairs i = 16*(part & 1) + 4c + e
+  if (rope && rh == 32 && wave == 0) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      tc[c] = *reinterpret_cast<const f32x4 *>(a.cos_t + pos + 16 * (part & 1) + 4 * c);
+      ts[c] = *reinterpret_cast<const f32x4 *>(a.sin_t + pos + 16 * (part & 1) + 4 * c);
+    }
+  }
+
+  if (kt == 0 && kvh == 0 && wave == 0) {
+    // The row's active keys: one bit per key (zero past L) and the (first,
+    // last) span, (0, -1) for a row with none.
+    uint32_t *bits = kbits + (size_t)row * ((L + 31) / 32);
+    int lo = 0x7fffffff, hi = -1;
+    for (int b0 = 0; b0 < L; b0 += 64 * 8) {
+      float mv[8];
+#pragma unroll
+      for (int v = 0; v < 8; ++v) mv[v] = maskr[min(b0 + 64 * v + lane, L - 1)];
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        const int kb = b0 + 64 * v;
+        const uint64_t bm = __ballot(kb + lane < L && mv[v] != 0.0f);
+        if (lane == 0 && kb < L) {
+          bits[kb / 32] = (uint32_t)bm;
+          if (kb + 32 < L) bits[kb / 32 + 1] = (uint32_t)(bm >> 32);
+        }
+        if (bm != 0) {
+          lo = min(lo, kb + (int)__builtin_ctzll(bm));
+          hi = max(hi, kb + 63 - (int)__builtin_clzll(bm));
+        }
+      }
+    }
+    if (lane == 0) {
+      spans[2 * row] = hi >= 0 ? lo : 0;
+      spans[2 * row + 1] = hi;
+    }
+  }
+
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int e = tid + 256 * t, d = e >> 2, g4 = e & 3;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) Kt[(4 * g4 + i) * KS + d] = x[t][i];
+  }
+  __syncthreads();
+  float kv[16];
+  float ss = 0.0f;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const f32x4 y = *reinterpret_cast<const f32x4 *>(&Kt[(tid & 15) * KS + 16 * part + 4 * c]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      kv[4 * c + e] = kin ? y[e] : 0.0f;
+      ss += kv[4 * c + e] * kv[4 * c + e];
+    }
+  }
+  ss = pair_sum(pair16_sum(ss));  // the wave's four parts of this key
+  if (lane < 16) s_red[wave * 16 + lane] = ss;
+  __syncthreads();
+  const int kk = tid & 15;
+  const float tot = s_red[kk] + s_red[16 + kk] + s_red[32 + kk] + s_red[48 + kk];
+  const float scale = rms_scale(tot, hd, a.eps);
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int d = 16 * part + 4 * c + e;
+      kv[4 * c + e] = (kin && d < hd) ? rms_apply(kv[4 * c + e], scale, wn[c][e]) : 0.0f;
+    }
+  if (rope && rh == 32) {
+    // Part p < 2 holds pairs i = 16p + j, part p + 2 (lane + 32, same wave)
+    // their partners i + 32.
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      // r[1] holds lanes 32..63 in both halves, r[0] lanes 0..31: the
+      // partner of lane l < 32 is r[1], of lane l >= 32 r[0].
+      const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(kv[j]), __float_as_uint(kv[j]),
+                                                      false, false);
+      const float other = __uint_as_float(lane < 32 ? r[1] : r[0]);
+      const float xl = part < 2 ? kv[j] : other, yh = part < 2 ? other : kv[j];
+      if (kin && wave == 0) {
+        const float cc = tc[j >> 2][j & 3], sn = ts[j >> 2][j & 3];
+        kv[j] = part < 2 ? rope_lo(xl, yh, cc, sn) : rope_hi(xl, yh, cc, sn);
+      }
+    }
+  } else if (rope) {
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 16; ++j) Kt[kk * KS + 16 * part + j] = kv[j];
+    __syncthreads();
+    if (kin) {
+      for (int i = part; i < rh; i += 16) {
+        const float xl = Kt[kk * KS + i], yh = Kt[kk * KS + i + rh];
+        const float cc = a.cos_t[pos + i], sn = a.sin_t[pos + i];
+        Kt[kk * KS + i] = rope_lo(xl, yh, cc, sn);
+        Kt[kk * KS + i + rh] = rope_hi(xl, yh, cc, sn);
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 16; ++j) kv[j] = Kt[kk * KS + 16 * part + j];
+  }
+  const int Lp = (L + 15) & ~15;
+  float *unit = kp + ((size_t)row * a.kv_heads + kvh) * (size_t)Lp * HDP;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const f32x4 o = {kv[4 * c], kv[4 * c + 1], kv[4 * c + 2], kv[4 * c + 3]};
+    *reinterpret_cast<f32x4 *>(unit + split_kp_offset(key, 16 * part + 4 * c)) = o;
   }
 }
 
@@ -995,6 +1107,13 @@ __global__ __launch_bounds__(256, 3) void jeff_split_f32_kernel(const JeffArgs a
 #pragma unroll
     for (int j = 0; j < NB; ++j) vr[j] = buffer_load4(rv, ovv + j * 16 * L * 4, k0 * 4);
   };
+  // The Q tile's HBM round trip starts with the item (wasted only for a
+  // tile with no key, which never reads it).
+  const __amdgpu_buffer_rsrc_t rq = buffer_rsrc(Q, (uint32_t)((size_t)hd * L * 4));
+  const int otask = ((wave * DS + tdl) * L + 4 * tg4) * 4;  // byte offset of task 0
+  f32x4 qx[NB];
+#pragma unroll
+  for (int t = 0; t < NB; ++t) qx[t] = buffer_load4(rq, otask + t * 16 * L * 4, q0 * 4);
   const int first = spans[2 * row], last = spans[2 * row + 1];
   fetch(qt * KT, kc, vc);
   const int start = (a.trim && last >= 0) ? first : 0;
@@ -1013,8 +1132,6 @@ __global__ __launch_bounds__(256, 3) void jeff_split_f32_kernel(const JeffArgs a
 
   const __amdgpu_buffer_rsrc_t rg = buffer_rsrc(Gt, (uint32_t)((size_t)hd * L * 4));
   const __amdgpu_buffer_rsrc_t ro = buffer_rsrc(OUT, (uint32_t)((size_t)hd * L * 4));
-  const __amdgpu_buffer_rsrc_t rq = buffer_rsrc(Q, (uint32_t)((size_t)hd * L * 4));
-  const int otask = ((wave * DS + tdl) * L + 4 * tg4) * 4;  // byte offset of task 0
   f32x4 gv[NB];
   auto load_gate = [&]() {
 #pragma unroll
@@ -1046,9 +1163,6 @@ __global__ __launch_bounds__(256, 3) void jeff_split_f32_kernel(const JeffArgs a
   const int rh = a.rot_half;
   const bool rope = a.cos_t != nullptr && rh > 0;
   const bool lane_rope = rh == 16 || rh == 32;
-  f32x4 qx[NB];
-#pragma unroll
-  for (int t = 0; t < NB; ++t) qx[t] = buffer_load4(rq, otask + t * 16 * L * 4, q0 * 4);
   const __amdgpu_buffer_rsrc_t rn = buffer_rsrc(a.q_norm, (uint32_t)(hd * 4));
   f32x4 wv[QS / 4];
 #pragma unroll
@@ -1145,9 +1259,11 @@ __global__ __launch_bounds__(256, 3) void jeff_split_f32_kernel(const JeffArgs a
 
   // Keep word of a 16-key tile for query col: active key (the prep's bits:
   // mask != 0, zero past L), key <= query (lib.rs:716). Keys before `start`
-  // are inactive by definition of start.
-  auto keep_word = [&](int kt) -> uint32_t {
-    const uint32_t abits = (rbits[kt >> 1] >> (16 * (kt & 1))) & 0xffffu;
+  // are inactive by definition of start. The bits word is loaded one tile
+  // ahead (bits_of) and turned into the word after that tile's products.
+  auto bits_of = [&](int kt) -> uint32_t { return rbits[kt >> 1]; };
+  auto keep_word = [&](int kt, uint32_t word) -> uint32_t {
+    const uint32_t abits = (word >> (16 * (kt & 1))) & 0xffffu;
     return q_live ? (abits & range_bits(0, q - kt * KT)) : 0u;
   };
 
@@ -1165,15 +1281,18 @@ __global__ __launch_bounds__(256, 3) void jeff_split_f32_kernel(const JeffArgs a
   // with the last tile.
   const int kt_hi = kt_end - 1;
   if (kt_hi != qt) fetch(kt_hi * KT, kc, vc);  // the span ends before the diagonal
-  uint32_t w = keep_word(kt_hi);
+  uint32_t w = keep_word(kt_hi, bits_of(kt_hi));
   bool tainted = false;  // workgroup-uniform
   int xb = 0;            // exchange buffer
   for (int kt = kt_hi; kt >= kt_begin; --kt) {
     const bool more = kt > kt_begin;
-    if (more)
+    uint32_t bnext = 0u;
+    if (more) {
+      bnext = bits_of(kt - 1);
       fetch((kt - 1) * KT, kn, vn);
-    else
+    } else {
       load_gate();
+    }
     if (kt * KT + KT > L) {  // the row's last, partial tile: V past L is another feature's
 #pragma unroll
       for (int j = 0; j < NB; ++j)
@@ -1246,7 +1365,7 @@ __global__ __launch_bounds__(256, 3) void jeff_split_f32_kernel(const JeffArgs a
       for (int c = 0; c < QS / 4; ++c) kc[c] = kn[c];
 #pragma unroll
       for (int j = 0; j < NB; ++j) vc[j] = vn[j];
-      w = keep_word(kt - 1);
+      w = keep_word(kt - 1, bnext);
     }
   }
 
@@ -1661,8 +1780,8 @@ static hipError_t launch_jeff_f32_hd(const JeffArgs &a, int rows, float *kp, hip
       int *spans = reinterpret_cast<int *>(reinterpret_cast<char *>(kp) +
                                            jeff_kp_main_bytes(a, rows, HDP, false));
       uint32_t *kbits = reinterpret_cast<uint32_t *>(spans + 2 * rows);
-      hipLaunchKernelGGL((jeff_k_prep_kernel<HDP, float, true>), pgrid, dim3(256), 0, stream, a,
-                         kp, spans, kbits);
+      const dim3 sp((a.L + 15) / 16, a.kv_heads, rows);
+      hipLaunchKernelGGL(jeff_k_prep_split_kernel, sp, dim3(256), 0, stream, a, kp, spans, kbits);
       hipError_t e = hipGetLastError();
       if (e != hipSuccess) return e;
       const dim3 sgrid(nq * rows * a.heads);

@@ -398,6 +398,7 @@ int jeff_run(tfd_ctx *c, const char *op, bool bf16, size_t rows, size_t length, 
   a.groups = (int)(heads / kv_heads);
   a.heads_per_group = (a.groups % 4 == 0) ? 4 : (a.groups % 2 == 0) ? 2 : 1;
   a.trim = (flags & TFD_TRIM_LEADING) ? 1 : 0;
+  a.cus = c->cus;
   a.eps = bits_to_f32(eps_bits);
   a.c1 = (1.0f / sqrtf((float)head_dim)) * kLog2e;
   a.q_row = qn / rows;

@@ -44,6 +44,7 @@ struct JeffArgs {
   int L, heads, kv_heads, hd, rot_half, groups;
   int heads_per_group;           // query heads sharing one workgroup (1, 2 or 4)
   int trim;                      // TFD_TRIM_LEADING semantics
+  int cus;                       // compute units of the device (grid shapes)
   float c1;                      // (1/sqrt(hd)) * log2(e)
   float eps;
   size_t q_row, kv_row;          // elements per row: L*heads*hd and L*kv_heads*hd
