@@ -27,9 +27,9 @@ namespace tfd {
 
 // Packs the (L, L, B) byte keep tensor into one 32-bit word per
 // (batch, key tile, query): bit j set when key 32*kt + j is kept. Also
-// writes the tile map: byte (b*nkt + kt)*ng + g is 1 when any of queries
-// 64g..64g+63 keeps a key of tile kt (ng = ceil(L/64)), from which the
-// attention workgroups read their key spans.
+// writes the tile map: byte (b*ng + g)*laya_map_row(nkt) + kt is 1 when any
+// of queries 64g..64g+63 keeps a key of tile kt (ng = ceil(L/64)); the
+// attention workgroups read their group's row with scalar loads.
 __global__ __launch_bounds__(256) void laya_keep_bits_kernel(const uint8_t *__restrict__ keep,
                                                              uint32_t *__restrict__ bits,
                                                              uint8_t *__restrict__ any, int L,
@@ -53,7 +53,8 @@ __global__ __launch_bounds__(256) void laya_keep_bits_kernel(const uint8_t *__re
   // A wave is 64 consecutive queries starting at a multiple of 64; its lane
   // 0 is active whenever the wave is.
   const bool some = __ballot(w != 0u) != 0;
-  if ((threadIdx.x & 63) == 0) any[((size_t)b * nkt + kt) * ((L + 63) / 64) + q / 64] = some;
+  if ((threadIdx.x & 63) == 0)
+    any[((size_t)b * ((L + 63) / 64) + q / 64) * laya_map_row(nkt) + kt] = some;
 }
 
 // ------------------------------------------------------------------ helpers
@@ -369,16 +370,12 @@ __global__ __launch_bounds__(256, laya_groups_per_cu<HDP>()) void laya_attention
   // barrier). Its bytes are read before anything else, so that waiting for
   // them never waits for the Q rows issued after them.
   int kt_begin = 0, kt_end = 0;
-  uint8_t f0[4];
   const int ng = (L + 63) / 64;
-  const uint8_t *anyb = a.any + (size_t)b * nkt * ng + qg0 / 64;  // kMaskBits
-  const uint8_t *vb = a.valid + (size_t)b * L;                     // kMaskStruct
+  // kMaskBits: the workgroup's 64 queries are exactly tile-map group qg0 / 64.
+  const uint8_t *anyb = a.any + ((size_t)b * ng + qg0 / 64) * laya_map_row(nkt);
+  const uint8_t *vb = a.valid + (size_t)b * L;  // kMaskStruct
   bool padded = false;
-  if (MODE == kMaskBits) {
-    // The workgroup's 64 queries are exactly tile-map group qg0 / 64.
-#pragma unroll
-    for (int u = 0; u < 4; ++u) f0[u] = anyb[(size_t)min(lane + 64 * u, nkt - 1) * ng];
-  } else {
+  if (MODE != kMaskBits) {
     const int qx = qg0 + lane;
     const uint8_t xv = vb[min(qx, L - 1)];
     padded = __ballot(qx < L && xv == 0) != 0;
@@ -417,15 +414,22 @@ __global__ __launch_bounds__(256, laya_groups_per_cu<HDP>()) void laya_attention
     }
   };
   if (MODE == kMaskBits) {
+    // The group's row of the tile map, 64 flags (16 words) per scalar load.
+    const uint32_t *anyw = reinterpret_cast<const uint32_t *>(anyb);
+    for (int t0 = 0; t0 < nkt; t0 += 64) {
+      uint32_t x[16];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) span_add(__ballot(lane + 64 * u < nkt && f0[u] != 0), 64 * u);
-    for (int k0 = 64 * 4; k0 < nkt; k0 += 64 * 4) {  // L > 8192 only
-      uint8_t f[4];
+      for (int i = 0; i < 16; ++i) x[i] = anyw[t0 / 4 + i];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) f[u] = anyb[(size_t)min(k0 + lane + 64 * u, nkt - 1) * ng];
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-        span_add(__ballot(k0 + lane + 64 * u < nkt && f[u] != 0), k0 + 64 * u);
+      for (int i = 0; i < 16; ++i) {
+        const int t = t0 + 4 * i;  // flags t .. t + 3, one per byte
+        uint32_t v = x[i];
+        if (t + 4 > nkt) v = t >= nkt ? 0u : v & ((1u << (8 * (nkt - t))) - 1u);
+        if (v != 0u) {
+          lo = min(lo, t + (int)__builtin_ctz(v) / 8);
+          hi = max(hi, t + (31 - (int)__builtin_clz(v)) / 8);
+        }
+      }
     }
     if (hi >= 0) {
       kt_begin = lo;

@@ -323,7 +323,8 @@ int laya_run(tfd_ctx *c, const char *op, const float *qkv, const uint8_t *keep,
     // Workspace: the packed words, then the per-(tile, 64-query group) map.
     size_t words = 0, groups = 0;
     if (!mul_ok((size_t)a.nkt * batch, length, &words) ||
-        !mul_ok((size_t)a.nkt * batch, (length + 63) / 64, &groups) || words > SIZE_MAX / 8)
+        !mul_ok((size_t)tfd::laya_map_row(a.nkt) * batch, (length + 63) / 64, &groups) ||
+        words > SIZE_MAX / 8)
       return invalid(c, op, "shape", "attention dimensions overflow");
     const size_t map_off = (sizeof(uint32_t) * words + 255) & ~(size_t)255;
     if ((rc = reserve(c, c->bits, map_off + groups))) return rc;

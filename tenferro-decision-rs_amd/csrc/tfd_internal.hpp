@@ -17,6 +17,10 @@ constexpr int kJeffWaveQueries = 16;  // Jeff waves use the 16x16x4 MFMA
 constexpr int kJeffF32Waves = 8;      // Jeff f32 workgroup: 512 threads, one per CU
 constexpr int kJeffKeyTile = 16;      // keys per Jeff f32 tile
 
+// Bytes per 64-query group in the Laya tile map: nkt flags rounded up to
+// whole 64-byte scalar loads.
+__host__ __device__ constexpr int laya_map_row(int nkt) { return (nkt + 63) & ~63; }
+
 enum LayaMaskMode : int {
   kMaskBits = 0,    // general (L, L, B) keep tensor, pre-packed into 32-key words
   kMaskStruct = 1,  // valid (L, B) + window (build_mask semantics)
@@ -25,8 +29,8 @@ enum LayaMaskMode : int {
 struct LayaArgs {
   const float *qkv;      // (3d, L, B)
   const uint32_t *bits;  // kMaskBits: word (b*nkt + kt)*L + q, bit j = key 32*kt + j kept
-  const uint8_t *any;    // kMaskBits: byte (b*nkt + kt)*ceil(L/64) + q/64, tile kt kept by any
-                         // query of that 64-query group
+  const uint8_t *any;    // kMaskBits: byte (b*ceil(L/64) + q/64)*laya_map_row(nkt) + kt, tile
+                         // kt kept by any query of that 64-query group
   const uint8_t *valid;  // kMaskStruct: (L, B)
   const float *cos_t;    // (L, half) or nullptr (no RoPE)
   const float *sin_t;
