@@ -678,9 +678,16 @@ struct JeffStage {
 // TAG gives each calling kernel its own copy, compiled to that kernel's
 // register budget; TAG 1 (the split-head kernel) reads the split K layout.
 template <int HDP, bool VEC, int TAG = 0>
-__device__ __noinline__ void jeff_redo_wave(const JeffArgs a, const float *__restrict__ kp, int row,
-                                            int head, int q0, int kt_begin, int kt_end, int start,
-                                            float *ws);
+__device__ __noinline__ void jeff_redo_wave(const JeffArgs *ap, const float *__restrict__ kp,
+                                            int row, int head, int q0, int kt_begin, int kt_end,
+                                            int start, float *ws);
+
+// The calling kernel's JeffArgs (its first parameter, at offset 0 of the
+// kernel argument segment), for the out-of-line redo: passing the struct by
+// value would make every wave copy it to scratch on entry.
+__device__ __forceinline__ const JeffArgs *kernel_jeff_args() {
+  return (const JeffArgs *)__builtin_amdgcn_kernarg_segment_ptr();
+}
 
 // One workgroup = 8 wavefronts (one workgroup per CU) sharing one kv head:
 // hg = heads_per_group query heads x (8 / hg) query tiles of 16. The query
@@ -889,7 +896,7 @@ __global__ __launch_bounds__(kJeffF32Waves * 64, 1) void jeff_attention_f32_kern
     for (int r = 0; r < 4; ++r) bad |= !__builtin_isfinite(O[j][r]);
   if (!wave_live) return;
   if (tainted || __ballot(q_live && bad) != 0) {
-    jeff_redo_wave<HDP, VEC>(a, kp, row, head, q0, kt_begin, kt_end, start, qw);
+    jeff_redo_wave<HDP, VEC>(kernel_jeff_args(), kp, row, head, q0, kt_begin, kt_end, start, qw);
     return;
   }
 
@@ -907,9 +914,10 @@ __global__ __launch_bounds__(kJeffF32Waves * 64, 1) void jeff_attention_f32_kern
 // p != 0 in key order (lib.rs:716-754), then the gate. Kept out of line so
 // that its registers never weigh on the walk. ws: the wave's LDS rows.
 template <int HDP, bool VEC, int TAG>
-__device__ __noinline__ void jeff_redo_wave(const JeffArgs a, const float *__restrict__ kp, int row,
-                                            int head, int q0, int kt_begin, int kt_end, int start,
-                                            float *ws) {
+__device__ __noinline__ void jeff_redo_wave(const JeffArgs *ap, const float *__restrict__ kp,
+                                            int row, int head, int q0, int kt_begin, int kt_end,
+                                            int start, float *ws) {
+  const JeffArgs &a = *ap;
   constexpr int KT = kJeffKeyTile, QS = HDP / 4, NB = HDP / 16, PS = KT + 1;
   const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
   const int L = a.L, hd = a.hd;
@@ -1379,7 +1387,7 @@ __global__ __launch_bounds__(256, 3) void jeff_split_f32_kernel(const JeffArgs a
   if (__ballot(q_live && bad) != 0 && lane == 0) s_bad = 1;
   __syncthreads();
   if (tainted || s_bad != 0) {
-    if (wave == 0) jeff_redo_wave<HDP, true, 1>(a, kp, row, head, q0, kt_begin, kt_end, start, smem);
+    if (wave == 0) jeff_redo_wave<HDP, true, 1>(kernel_jeff_args(), kp, row, head, q0, kt_begin, kt_end, start, smem);
     return;
   }
 

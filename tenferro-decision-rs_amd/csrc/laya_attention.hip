@@ -225,8 +225,9 @@ struct LayaStage {
 // probabilities (lib.rs:1143-1151). Kept out of line so that its registers
 // never weigh on the walk. Pw: 32 x 17 floats of LDS owned by the wave.
 template <int HDP, int MODE, bool ROPE>
-__device__ __noinline__ void laya_redo_wave(const LayaArgs a, int b, int head, int q0,
+__device__ __noinline__ void laya_redo_wave(const LayaArgs *ap, int b, int head, int q0,
                                             int kt_begin, int kt_end, float *Pw) {
+  const LayaArgs &a = *ap;
   constexpr int QS = HDP / 4, NB = HDP / 16, PS = 17;
   const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
   const int L = a.L, hd = a.hd, hh = a.half, nkt = a.nkt;
@@ -354,9 +355,34 @@ __global__ __launch_bounds__(256, laya_groups_per_cu<HDP>()) void laya_attention
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform, in a scalar register
   const int col = lane & 15, grp = lane >> 4;
-  const int head = blockIdx.y, b = blockIdx.z;
   const int L = a.L, hd = a.hd, hh = a.half, nkt = a.nkt;
-  const int qg0 = blockIdx.x * GQ;
+  // Work item (batch row b, head, 64-query block qb). The dispatcher hands
+  // workgroup p to XCD p % 8 (each XCD has its own L2) and, while all fit,
+  // to CU slot p % (CUs): when the counts allow it, each XCD gets an equal
+  // share of every batch row (consecutive (head, block) items, so a head's
+  // keys and values are read by at most two XCDs) and the three workgroups
+  // of a CU come from three different rows (r, r + 3, r + 6).
+  int b = blockIdx.z, head = blockIdx.y, qb = blockIdx.x;
+  {
+    const int nqb = gridDim.x, H = gridDim.y, B = gridDim.z;
+    const int per_row = H * nqb;      // items of one batch row
+    const int M = per_row / 8;        // of them per XCD
+    // (One dispatch round only: beyond it, workgroups start where others
+    // end and the grid order is the better schedule.)
+    const bool one_round = a.cus > 0 && nqb * H * B <= laya_groups_per_cu<HDP>() * a.cus;
+    if (one_round && per_row % 8 == 0 && 32 % B == 0 && M % (32 / B) == 0) {
+      const int p = blockIdx.x + nqb * (blockIdx.y + H * blockIdx.z);
+      const int x = p % 8, j = p / 8;
+      const int t = j / 32, c = j % 32;            // round, CU of the XCD
+      const int row = (c + 3 * t) % B;
+      const int k = t * (32 / B) + c / B;          // item of that row on this XCD
+      const int r = x * M + k;
+      b = row;
+      head = r / nqb;
+      qb = r % nqb;
+    }
+  }
+  const int qg0 = qb * GQ;
   const int q0w = qg0 + wave * kLayaWaveQueries;
   const int q = q0w + col;
   const bool qin = q < L;
@@ -652,7 +678,11 @@ __global__ __launch_bounds__(256, laya_groups_per_cu<HDP>()) void laya_attention
 #pragma unroll
     for (int r = 0; r < 4; ++r) bad |= !__builtin_isfinite(O[j][r]);
   if (tainted || __ballot(qin && bad) != 0) {
-    laya_redo_wave<HDP, MODE, ROPE>(a, b, head, q0w, kt_begin, kt_end,
+    // The kernel's LayaArgs (its first parameter, at offset 0 of the kernel
+    // argument segment): passing the struct by value would copy it to
+    // scratch.
+    laya_redo_wave<HDP, MODE, ROPE>((const LayaArgs *)__builtin_amdgcn_kernarg_segment_ptr(), b,
+                                    head, q0w, kt_begin, kt_end,
                                     smem + wave * kKeyTile * 17);
     return;
   }

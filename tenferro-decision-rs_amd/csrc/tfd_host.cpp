@@ -303,6 +303,7 @@ int laya_run(tfd_ctx *c, const char *op, const float *qkv, const uint8_t *keep,
     if ((rc = operand(c, flags, 2, valid, valid_len, &mask_d))) return rc;
   }
   tfd::LayaArgs a{};
+  a.cus = c->cus;
   a.qkv = static_cast<const float *>(qkv_d);
   a.out = static_cast<float *>(out_d);
   a.d = (int)hidden;

@@ -36,6 +36,7 @@ struct LayaArgs {
   const float *sin_t;
   float *out;            // (d, L, B)
   int d, hd, half, L, nkt, window;
+  int cus;               // compute units of the device (grid shapes)
   float c1;              // (1/sqrt(hd)) * log2(e)
 };
 
