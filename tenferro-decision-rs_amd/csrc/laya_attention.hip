@@ -579,6 +579,11 @@ __global__ __launch_bounds__(256, laya_groups_per_cu<HDP>()) void laya_attention
     w = keep_word(kt_begin, m0);
   }
   __syncthreads();
+  // Nothing may still be in flight when the walk starts: otherwise the
+  // compiler can carry a prologue load's register into the loop's wait
+  // bookkeeping and make every tile's first product wait for the prefetch of
+  // the next tile (costs nothing here: the first tile's commit has waited).
+  __builtin_amdgcn_s_waitcnt(0);
   bool tainted = false;  // wave-uniform
   int cur = 0;
   for (int kt = kt_begin; kt < kt_end; ++kt) {
