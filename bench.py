@@ -35,7 +35,12 @@ def log(*a):
 
 
 def time_gpu(fn, steps, warmup, ctx):
-    """(ms per step by torch events on the shared stream, avg attention-kernel ms)."""
+    """(ms per step by torch events on the shared stream, avg attention-kernel ms).
+
+    Two passes of `steps` steps: the whole-op time without the library's
+    per-kernel events (they sit between the op's kernels and add a few
+    microseconds per step), then the attention kernel's own duration with
+    them."""
     import torch
     import tenferro_ext as te
 
@@ -43,14 +48,16 @@ def time_gpu(fn, steps, warmup, ctx):
         for _ in range(warmup):
             fn()
         torch.cuda.synchronize()
-        ctx.take_kernel_time()
-        ctx.set_timing(True)
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
         start.record()
         for _ in range(steps):
             fn()
         end.record()
+        torch.cuda.synchronize()
+        ctx.take_kernel_time()
+        ctx.set_timing(True)
+        for _ in range(steps):
+            fn()
         torch.cuda.synchronize()
         ctx.set_timing(False)
     total, launches = ctx.take_kernel_time()

@@ -30,6 +30,80 @@ namespace tfd {
 // writes the tile map: byte (b*ng + g)*laya_map_row(nkt) + kt is 1 when any
 // of queries 64g..64g+63 keeps a key of tile kt (ng = ceil(L/64)); the
 // attention workgroups read their group's row with scalar loads.
+// Placement plan of a one-round attention grid (laya_xcd_layout, kMaskBits):
+// the item and key span of workgroup p, computed from the whole tile map by
+// one wave (every workgroup derives the same plan). Workgroup p runs on XCD
+// x = p % 8, CU c = (p / 8) % 32 of it, round t = p / 256 (S = grid / 256
+// rounds). As in the fixed layout, XCD x runs the items r in [x*M, x*M + M)
+// of every batch row (M = heads*nqb / 8; a head's keys are read by at most
+// two XCDs). Which CU runs which of them follows the row's cost, the widest
+// key span over its 64-query groups: the XCD's items sorted by cost, longest
+// first, are dealt out in snake order for rounds 0 .. S-2, and the last round
+// gives the largest remaining items to the least loaded CUs. Every XCD holds
+// the same multiset of row costs, so one CU order serves all eight. Only the
+// work of a CU changes, never a result. `scratch` holds B*ng + 96 ints of
+// LDS. Returns {row, item head*nqb + qb, kt_begin, kt_end}, uniform.
+__device__ int4 laya_plan_item(const uint8_t *__restrict__ any, int L, int nkt, int B, int H,
+                               int p, int *scratch) {
+  const int lane = threadIdx.x & 63;
+  const int ng = (L + 63) / 64, G = B * ng;
+  const int M = H * ng / 8, S = B * M / 32;
+  int *s_span = scratch, *s_cost = scratch + G, *s_rows = s_cost + 32, *s_load = s_rows + 32;
+  auto wave_sync = [] {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+  if (lane < 32) s_cost[lane] = 0;
+  wave_sync();
+  for (int g = lane; g < G; g += 64) {  // the span of every (row, 64-query group)
+    const uint4 *row = reinterpret_cast<const uint4 *>(any + (size_t)g * laya_map_row(nkt));
+    int lo = -1, hi = -1;
+    for (int t0 = 0; t0 < nkt; t0 += 16) {
+      const uint4 v = row[t0 / 16];  // 16 flags; rows are padded to 64 bytes
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = t0 + 4 * i;
+        uint32_t x = w[i];
+        if (t + 4 > nkt) x = t >= nkt ? 0u : x & ((1u << (8 * (nkt - t))) - 1u);
+        if (x != 0u) {
+          if (lo < 0) lo = t + (int)__builtin_ctz(x) / 8;
+          hi = t + (31 - (int)__builtin_clz(x)) / 8;
+        }
+      }
+    }
+    s_span[g] = lo < 0 ? 0 : lo | ((hi + 1) << 16);
+    if (lo >= 0) atomicMax(&s_cost[g / ng], hi + 1 - lo);
+  }
+  wave_sync();
+  if (lane < B) {  // rows by cost, longest first (ties: lower row first)
+    const int cb = s_cost[lane];
+    int rank = 0;
+    for (int o = 0; o < B; ++o) rank += s_cost[o] > cb || (s_cost[o] == cb && o < lane);
+    s_rows[rank] = lane;
+  }
+  wave_sync();
+  auto snake = [](int t, int c) { return 32 * t + ((t & 1) ? 31 - c : c); };
+  if (lane < 32) {  // CU `lane`'s load after the snake rounds
+    int load = 0;
+    for (int t = 0; t < S - 1; ++t) load += s_cost[s_rows[snake(t, lane) / M]];
+    s_load[lane] = load;
+  }
+  wave_sync();
+  const int x = p % 8, c = (p / 8) % 32, t = p / 256;
+  int pos = snake(t, c);
+  if (t == S - 1) {  // last round: this CU's place by load, least loaded first
+    const int lc = s_load[c];
+    const bool before = lane < 32 && (s_load[lane] < lc || (s_load[lane] == lc && lane < c));
+    pos = 32 * t + __builtin_popcountll(__ballot(before));
+  }
+  const int b = s_rows[pos / M];
+  const int r = x * M + pos % M;
+  const int sp = s_span[b * ng + r % ng];
+  return make_int4(b, r, sp & 0xffff, sp >> 16);
+}
+
 __global__ __launch_bounds__(256) void laya_keep_bits_kernel(const uint8_t *__restrict__ keep,
                                                              uint32_t *__restrict__ bits,
                                                              uint8_t *__restrict__ any, int L,
@@ -330,18 +404,13 @@ __device__ __noinline__ void laya_redo_wave(const LayaArgs *ap, int b, int head,
   }
 }
 
-// Occupancy target: four workgroups (16 waves) per CU where LDS and
-// registers allow it. On gfx950 the f32 MFMAs and the vector ALU share the
-// SIMD (they never run at the same time), so the walk keeps its vector work
-// per tile small and relies on other waves to cover memory and barrier
-// waits.
-template <int HDP>
-constexpr int laya_groups_per_cu() {
-  return HDP <= 64 ? 4 : 2;
-}
-
+// Occupancy target (laya_groups_per_cu): four workgroups (16 waves) per CU
+// where LDS and registers allow it. On gfx950 the f32 MFMAs and the vector
+// ALU share the SIMD (they never run at the same time), so the walk keeps its
+// vector work per tile small and relies on other waves to cover memory and
+// barrier waits.
 template <int HDP, int MODE, bool VEC, bool ROPE>
-__global__ __launch_bounds__(256, laya_groups_per_cu<HDP>()) void laya_attention_kernel(
+__global__ __launch_bounds__(256, laya_groups_per_cu(HDP)) void laya_attention_kernel(
     const LayaArgs a) {
   using Stage = LayaStage<HDP, VEC, ROPE>;
   constexpr int KS = Stage::KS, VS = Stage::VS;
@@ -358,24 +427,40 @@ __global__ __launch_bounds__(256, laya_groups_per_cu<HDP>()) void laya_attention
   const int L = a.L, hd = a.hd, hh = a.half, nkt = a.nkt;
   // Work item (batch row b, head, 64-query block qb). The dispatcher hands
   // workgroup p to XCD p % 8 (each XCD has its own L2) and, while all fit,
-  // to CU slot p % (CUs): when the counts allow it, each XCD gets an equal
-  // share of every batch row (consecutive (head, block) items, so a head's
-  // keys and values are read by at most two XCDs) and the three workgroups
-  // of a CU come from three different rows (r, r + 3, r + 6).
+  // to CU slot p % (CUs): when the counts allow it (laya_xcd_layout), each
+  // XCD gets an equal share of every batch row (consecutive (head, block)
+  // items, so a head's keys and values are read by at most two XCDs). The
+  // keep-bits kernel's plan, when given, also balances the key tiles per CU
+  // and carries the item's key span; otherwise the workgroups of a CU come
+  // from different rows (r, r + 3, r + 6). Beyond one dispatch round,
+  // workgroups start where others end and the grid order is the better
+  // schedule.
   int b = blockIdx.z, head = blockIdx.y, qb = blockIdx.x;
+  int kt_begin = 0, kt_end = 0;
+  const int nqb = gridDim.x, H = gridDim.y, B = gridDim.z;
+  const bool xcd = laya_xcd_layout(nqb, H, B, laya_groups_per_cu(HDP), a.cus);
+  const bool planned = MODE == kMaskBits && xcd && nqb * B <= kLayaPlanMax;
   {
-    const int nqb = gridDim.x, H = gridDim.y, B = gridDim.z;
-    const int per_row = H * nqb;      // items of one batch row
-    const int M = per_row / 8;        // of them per XCD
-    // (One dispatch round only: beyond it, workgroups start where others
-    // end and the grid order is the better schedule.)
-    const bool one_round = a.cus > 0 && nqb * H * B <= laya_groups_per_cu<HDP>() * a.cus;
-    if (one_round && per_row % 8 == 0 && 32 % B == 0 && M % (32 / B) == 0) {
-      const int p = blockIdx.x + nqb * (blockIdx.y + H * blockIdx.z);
+    const int p = blockIdx.x + nqb * (blockIdx.y + H * blockIdx.z);
+    if (planned) {
+      __shared__ int4 s_item;
+      if (wave == 0) {
+        const int4 e = laya_plan_item(a.any, L, nkt, B, H, p, reinterpret_cast<int *>(smem));
+        if (lane == 0) s_item = e;
+      }
+      __syncthreads();
+      const int4 e = s_item;
+      b = __builtin_amdgcn_readfirstlane(e.x);
+      head = __builtin_amdgcn_readfirstlane(e.y) / nqb;
+      qb = __builtin_amdgcn_readfirstlane(e.y) % nqb;
+      kt_begin = e.z;
+      kt_end = e.w;
+    } else if (xcd) {
+      const int M = H * nqb / 8;  // items of a batch row per XCD
       const int x = p % 8, j = p / 8;
-      const int t = j / 32, c = j % 32;            // round, CU of the XCD
+      const int t = j / 32, c = j % 32;  // round, CU of the XCD
       const int row = (c + 3 * t) % B;
-      const int k = t * (32 / B) + c / B;          // item of that row on this XCD
+      const int k = t * (32 / B) + c / B;  // item of that row on this XCD
       const int r = x * M + k;
       b = row;
       head = r / nqb;
@@ -395,7 +480,6 @@ __global__ __launch_bounds__(256, laya_groups_per_cu<HDP>()) void laya_attention
   // wave computes it on its own from ballots (identical scalar results, no
   // barrier). Its bytes are read before anything else, so that waiting for
   // them never waits for the Q rows issued after them.
-  int kt_begin = 0, kt_end = 0;
   const int ng = (L + 63) / 64;
   // kMaskBits: the workgroup's 64 queries are exactly tile-map group qg0 / 64.
   const uint8_t *anyb = a.any + ((size_t)b * ng + qg0 / 64) * laya_map_row(nkt);
@@ -439,7 +523,9 @@ __global__ __launch_bounds__(256, laya_groups_per_cu<HDP>()) void laya_attention
       hi = max(hi, k0 + 63 - (int)__builtin_clzll(mk));
     }
   };
-  if (MODE == kMaskBits) {
+  if (planned) {
+    // the span came with the plan entry
+  } else if (MODE == kMaskBits) {
     // The group's row of the tile map, 64 flags (16 words) per scalar load.
     const uint32_t *anyw = reinterpret_cast<const uint32_t *>(anyb);
     for (int t0 = 0; t0 < nkt; t0 += 64) {

@@ -21,6 +21,24 @@ constexpr int kJeffKeyTile = 16;      // keys per Jeff f32 tile
 // whole 64-byte scalar loads.
 __host__ __device__ constexpr int laya_map_row(int nkt) { return (nkt + 63) & ~63; }
 
+// Laya workgroups per CU (launch bounds): four at padded head dims up to 64,
+// two at 128.
+__host__ __device__ constexpr int laya_groups_per_cu(int hd_pad) { return hd_pad <= 64 ? 4 : 2; }
+
+// Whether a Laya grid of nqb x H x B workgroups gets the XCD-aware layout:
+// the whole grid fits in one dispatch round (workgroup p then runs on XCD
+// p % 8 and CU slot p % cus) and each of the 8 XCDs can take an equal share
+// of every batch row, three (or S) workgroups per CU from different rows.
+__host__ __device__ constexpr bool laya_xcd_layout(int nqb, int H, int B, int groups_per_cu,
+                                                    int cus) {
+  return cus > 0 && nqb * H * B <= groups_per_cu * cus && (H * nqb) % 8 == 0 && 32 % B == 0 &&
+         ((H * nqb) / 8) % (32 / B) == 0;
+}
+
+// Most (batch row, 64-query group) spans a Laya placement plan tabulates in
+// LDS.
+constexpr int kLayaPlanMax = 1024;
+
 enum LayaMaskMode : int {
   kMaskBits = 0,    // general (L, L, B) keep tensor, pre-packed into 32-key words
   kMaskStruct = 1,  // valid (L, B) + window (build_mask semantics)

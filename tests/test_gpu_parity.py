@@ -223,6 +223,53 @@ def test_laya_full_config_device_pointers(gpu_ctx, cfg):
     assert torch.equal(got, st)
 
 
+# (batch, heads, hd, window): grids of 256 (one round per CU slot), 512 and
+# 1024 workgroups at hd 64, 512 at hd 128, 1024 at hd 32, and a sliding
+# window (per-group spans differ from the row's).
+PLANNED_GRIDS = [(8, 4, 64, -1), (4, 16, 64, -1), (8, 16, 64, 64), (8, 8, 128, -1), (2, 64, 32, -1)]
+
+
+@pytest.mark.parametrize("batch,heads,hd,window", PLANNED_GRIDS)
+def test_laya_planned_grids(gpu_ctx, batch, heads, hd, window):
+    """Grids that fit one dispatch round follow a placement plan that each
+    workgroup derives from the tile map (rows longest first over the CUs of
+    each XCD). Ragged rows with an empty row and an interior hole; each shape
+    runs twice, after another planned shape. The drop-in (planned) must equal
+    the structured entry (never planned) bitwise, and the oracle within
+    tolerance on the first shape."""
+    import torch
+
+    L = 512
+    d = heads * hd
+    rng = Lcg(900 + batch * heads + hd)
+    valid = np.zeros(L * batch, np.uint8)
+    for b in range(batch):
+        n = 0 if b == 1 else int(rng.uniform(1)[0] * (L - 64)) + 64
+        valid[b * L:b * L + n] = 1
+    valid[L // 3] = 0  # a hole in row 0
+    qkv = (rng.uniform(3 * d * L * batch) * 2.0 - 1.0).astype(np.float32)
+    keep = oracle.laya_build_mask(valid, L, batch, window)
+    base = 160000.0 if window < 0 else 10000.0
+    dev = torch.device("cuda:0")
+    tq = torch.from_numpy(qkv).to(dev)
+    tk = torch.from_numpy(keep).to(dev)
+    tv = torch.from_numpy(valid).to(dev)
+    # another planned shape first (the tile map workspace is reused)
+    ob, oh, ohd, ow = PLANNED_GRIDS[(PLANNED_GRIDS.index((batch, heads, hd, window)) + 1) % len(PLANNED_GRIDS)]
+    od = oh * ohd
+    oqkv = torch.zeros(3 * od * L * ob, dtype=torch.float32, device=dev)
+    okeep = torch.ones(L * L * ob, dtype=torch.uint8, device=dev)
+    te.laya_attention_block(oqkv, okeep, od, oh, 160000.0, qkv_shape=(3 * od, L, ob), ctx=gpu_ctx)
+    st = te.laya_attention_structured(tq, tv, d, heads, L, batch, window, base, ctx=gpu_ctx)
+    for _ in range(2):
+        got = te.laya_attention_block(tq, tk, d, heads, base, qkv_shape=(3 * d, L, batch), ctx=gpu_ctx)
+        assert torch.equal(torch.isnan(got), torch.isnan(st))
+        assert torch.equal(got.view(torch.int32), st.view(torch.int32))
+    if (batch, heads, hd, window) == PLANNED_GRIDS[0]:
+        want = oracle.laya_attention_block(qkv, keep, d, heads, L, batch, base)
+        assert_close(got.cpu().numpy(), want, F32_TOL)
+
+
 # ------------------------------------------------------------------ Jeff
 
 def jeff_case(seed, length, heads, hd, kv_heads, holes):
