@@ -22,33 +22,11 @@
 // Each wavefront owns 16 queries and walks 32-key tiles on the 16x16x4 f32
 // MFMA: S^T = K Q^T as two 16-key blocks, then O^T += V^T P^T. At hd = 256
 // this keeps Q (hd/4 registers) and O^T (hd/4) within one wave's registers.
+#include "jeff_common.hpp"
 #include "tfd_device.hpp"
 #include "tfd_internal.hpp"
 
 namespace tfd {
-
-// x * (scale * (1 + w)) with the reference's rounding (no contraction).
-__device__ __forceinline__ float rms_apply(float x, float scale, float w) {
-#pragma clang fp contract(off)
-  return x * (scale * (1.0f + w));
-}
-
-__device__ __forceinline__ float rope_lo(float a, float b, float c, float s) {
-#pragma clang fp contract(off)
-  return a * c - b * s;
-}
-
-__device__ __forceinline__ float rope_hi(float a, float b, float c, float s) {
-#pragma clang fp contract(off)
-  return a * s + b * c;
-}
-
-// 1 / sqrt(mean + eps) with mean = sumsq / hd, in the reference's order.
-__device__ __forceinline__ float rms_scale(float sumsq, int hd, float eps) {
-#pragma clang fp contract(off)
-  const float mean = sumsq / (float)hd;
-  return 1.0f / sqrtf(mean + eps);
-}
 
 // Scans one row's key mask: first and last active key (mask != 0).
 __device__ __forceinline__ void scan_active(const float *maskr, int L, int tid, int lane,
@@ -1494,7 +1472,9 @@ struct JeffStageBf16 {
 // P.V MFMA per 16-row block of O^T.
 template <int HDP, bool VEC>
 __global__ __launch_bounds__(256, 2) void jeff_attention_bf16_kernel(const JeffArgs a,
-                                                                     const uint16_t *__restrict__ kp) {
+                                                                     const uint16_t *__restrict__ kp,
+                                                                     const int *__restrict__ redo,
+                                                                     int redo_qt) {
   constexpr int KT = 32;
   constexpr int QS8 = HDP / 32;  // bf16x8 B operands of Q per lane
   constexpr int NB = HDP / 16;   // 16-row blocks of O^T
@@ -1520,6 +1500,16 @@ __global__ __launch_bounds__(256, 2) void jeff_attention_bf16_kernel(const JeffA
   const int QT = kJeffWaveQueries * qsubs;
   const int qa = blockIdx.x * QT;
   const int q = qa + (wave / hg) * kJeffWaveQueries + col;
+  if (redo != nullptr) {
+    // Exact pass after jeff_bf16_wide_kernel: only the (head, query tile of
+    // redo_qt) units it flagged, for every query of this workgroup.
+    const int nqt = (L + redo_qt - 1) / redo_qt;
+    const int t_lo = qa / redo_qt, t_hi = (min(qa + QT, L) - 1) / redo_qt;
+    int any = 0;
+    for (int h = blockIdx.y * hg; h < blockIdx.y * hg + hg; ++h)
+      for (int t = t_lo; t <= t_hi; ++t) any |= redo[((size_t)row * a.heads + h) * nqt + t];
+    if (any == 0) return;  // uniform over the workgroup
+  }
   const bool qin = q < L;
   const float *maskr = a.mask + (size_t)row * L;
   const uint16_t *Q = static_cast<const uint16_t *>(a.q) + row * a.q_row + (size_t)head * hd * L;
@@ -1821,7 +1811,16 @@ hipError_t launch_jeff_attention_f32(const JeffArgs &a, int rows, int hd_pad, vo
   }
 }
 
+// bf16 at head dim 256: the flags of jeff_bf16_wide_kernel follow.
+size_t jeff_bf16_flags_offset(const JeffArgs &a, int rows) {
+  const size_t b = jeff_kp_main_bytes(a, rows, 256, true) + (size_t)rows * 2 * sizeof(int) +
+                   (size_t)rows * ((a.L + 31) / 32) * sizeof(uint32_t);
+  return (b + 255) & ~(size_t)255;
+}
+
 size_t jeff_kp_bytes(const JeffArgs &a, int rows, int hd_pad, bool bf16) {
+  if (bf16 && hd_pad == 256 && jeff_bf16_wide_fits(a))
+    return jeff_bf16_flags_offset(a, rows) + jeff_bf16_wide_flag_count(a, rows) * sizeof(int);
   return jeff_kp_main_bytes(a, rows, hd_pad, bf16) + (size_t)rows * 2 * sizeof(int) +
          (size_t)rows * ((a.L + 31) / 32) * sizeof(uint32_t);
 }
@@ -1833,15 +1832,28 @@ static hipError_t launch_jeff_bf16_hd(const JeffArgs &a, int rows, uint16_t *kp,
   hipLaunchKernelGGL((jeff_k_prep_kernel<HDP, uint16_t>), pgrid, dim3(256), 0, stream, a, kp);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  // Head dim 256: the 32x32x16 kernel, then this one as the exact pass over
+  // the query tiles it flagged (non-finite values).
+  const int *redo = nullptr;
+  int redo_qt = 0;
+  if (HDP == 256 && jeff_bf16_wide_fits(a)) {
+    int *flags = reinterpret_cast<int *>(reinterpret_cast<char *>(kp) + jeff_bf16_flags_offset(a, rows));
+    e = launch_jeff_bf16_wide(a, rows, kp, flags, stream);
+    if (e != hipSuccess) return e;
+    redo = flags;
+    redo_qt = jeff_bf16_wide_query_tile(a);
+  }
   const int qsubs = kWavesPerGroup / a.heads_per_group;
   const int qt = kJeffWaveQueries * qsubs;
   dim3 grid((a.L + qt - 1) / qt, a.heads / a.heads_per_group, rows);
   // 16-byte V loads along tokens need L % 8 == 0 and an aligned base.
   const bool vec = a.L % 8 == 0 && (reinterpret_cast<uintptr_t>(a.v) & 15) == 0;
   if (vec)
-    hipLaunchKernelGGL((jeff_attention_bf16_kernel<HDP, true>), grid, dim3(256), 0, stream, a, kp);
+    hipLaunchKernelGGL((jeff_attention_bf16_kernel<HDP, true>), grid, dim3(256), 0, stream, a, kp,
+                       redo, redo_qt);
   else
-    hipLaunchKernelGGL((jeff_attention_bf16_kernel<HDP, false>), grid, dim3(256), 0, stream, a, kp);
+    hipLaunchKernelGGL((jeff_attention_bf16_kernel<HDP, false>), grid, dim3(256), 0, stream, a, kp,
+                       redo, redo_qt);
   return hipGetLastError();
 }
 

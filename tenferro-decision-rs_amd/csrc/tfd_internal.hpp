@@ -87,5 +87,14 @@ hipError_t launch_jeff_attention_f32(const JeffArgs &a, int rows, int hd_pad, vo
                                      hipStream_t stream);
 hipError_t launch_jeff_attention_bf16(const JeffArgs &a, int rows, int hd_pad, void *kp,
                                       hipStream_t stream);
+// The bf16 kernel at head dim 256 on the 32x32x16 matrix cores (used by
+// launch_jeff_attention_bf16 when it fits): one flag per (row, head, query
+// tile of jeff_bf16_wide_query_tile) marks tiles left to the exact pass.
+bool jeff_bf16_wide_fits(const JeffArgs &a);
+int jeff_bf16_wide_query_tile(const JeffArgs &a);
+size_t jeff_bf16_wide_flag_count(const JeffArgs &a, int rows);
+size_t jeff_bf16_flags_offset(const JeffArgs &a, int rows);
+hipError_t launch_jeff_bf16_wide(const JeffArgs &a, int rows, const uint16_t *kp, int *flags,
+                                 hipStream_t stream);
 
 }  // namespace tfd

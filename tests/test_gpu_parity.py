@@ -484,6 +484,50 @@ def test_jeff_bf16_kept_nonfinite_values_propagate(gpu_ctx):
     assert np.abs(got[fin] - want[fin]).max() <= BF16_TOL
 
 
+# Head dim 256 with L % 8 == 0 runs the 32x32x16 kernel (4 wavefronts: hw
+# heads of a GQA group x 4/hw blocks of 32 queries); other RoPE widths fall
+# back to the 16x16x32 kernel.
+@pytest.mark.parametrize("length", [8, 40, 96, 264])
+@pytest.mark.parametrize("heads,kv,rot", [(8, 2, 64), (4, 2, 32), (2, 2, 0), (6, 2, 64),
+                                          (8, 1, 64), (4, 2, 48)])
+def test_jeff_bf16_hd256_rows_match_oracle(gpu_ctx, length, heads, kv, rot):
+    rows, hd = 2, 256
+    for trim in (False, True):
+        bits, vals, qn, kn, mask = bf16_case(7 * length + heads + rot, rows, length, heads, kv, hd,
+                                             True)
+        want = oracle.jeff_rows(*vals, qn, kn, mask, rows, length, heads, kv, hd, rot, 1e7, 1e-6,
+                                trim_leading=trim)
+        got = te.jeff_full_attention_rows(*bits, qn, kn, mask, rows, length, heads, kv, hd, rot,
+                                          1e7, 1e-6, trim_leading=trim, bf16=True, ctx=gpu_ctx)
+        assert_close(got, want, BF16_TOL)
+
+
+def test_jeff_bf16_hd256_nonfinite_takes_exact_pass(gpu_ctx):
+    """Head dim 256: tiles with non-finite values are left to the exact
+    kernel (flags); a clean call on the same context right after must not see
+    stale flags."""
+    rows, length, heads, kv, hd, rot = 2, 200, 8, 2, 256, 64
+    bits, vals, qn, kn, mask = bf16_case(11, rows, length, heads, kv, hd, False)
+    clean = [b.copy() for b in bits]
+    Vb = bits[2].reshape(rows, kv * hd, length)
+    Vb[0, 7, 12] = 0x7F80        # +inf value, kept from query 12 on
+    Vb[1, hd + 2, 150] = 0x7FC0  # NaN value in kv head 1 of row 1
+    mask[5] = 0.0
+    Vb[0, 9, 5] = 0x7FC0         # masked NaN: must not leak
+    Kb = bits[1].reshape(rows, kv * hd, length)
+    Kb[1, 3, 90] = 0x7FC0        # NaN key: NaN scores for kv head 0 of row 1
+    vals = [te.bf16_bits_to_f32(b) for b in bits]
+    want = oracle.jeff_rows(*vals, qn, kn, mask, rows, length, heads, kv, hd, rot, 1e7, 1e-6)
+    got = np.asarray(te.jeff_full_attention_rows(*bits, qn, kn, mask, rows, length, heads, kv, hd,
+                                                 rot, 1e7, 1e-6, bf16=True, ctx=gpu_ctx))
+    assert_same_nonfinite(got, want, BF16_TOL)
+    cvals = [te.bf16_bits_to_f32(b) for b in clean]
+    want = oracle.jeff_rows(*cvals, qn, kn, mask, rows, length, heads, kv, hd, rot, 1e7, 1e-6)
+    got = te.jeff_full_attention_rows(*clean, qn, kn, mask, rows, length, heads, kv, hd, rot, 1e7,
+                                      1e-6, bf16=True, ctx=gpu_ctx)
+    assert_close(got, want, BF16_TOL)
+
+
 def test_jeff_c5_reduced_matches_oracle(gpu_ctx):
     """C5 shape (GQA 8/2 x 256, causal, all active) at L 1024 against the oracle."""
     w = jeff_config(5, rows=2, length=1024)
