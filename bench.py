@@ -37,10 +37,10 @@ def log(*a):
 def time_gpu(fn, steps, warmup, ctx):
     """(ms per step by torch events on the shared stream, avg attention-kernel ms).
 
-    Two passes of `steps` steps: the whole-op time without the library's
-    per-kernel events (they sit between the op's kernels and add a few
-    microseconds per step), then the attention kernel's own duration with
-    them."""
+    Two passes of `steps` steps: the whole-op time, then the attention
+    kernel's own mean duration from the library's HIP event pairs, which the
+    kernel dispatches themselves record on the op's stream (start of the
+    first attention kernel, end of the last; hipExtLaunchKernel)."""
     import torch
     import tenferro_ext as te
 

@@ -83,8 +83,10 @@ size_t tfd_ctx_retained_bytes(const tfd_ctx *ctx);
 
 /* Kernel timing, a profiling aid with no counterpart in the reference (its
  * closest is raw_exec::take_drain_stats, crates/tenferro-ext/src/raw_exec.rs:781).
- * While enabled, the context records a HIP event pair on its stream around
- * every attention-kernel launch (not around uploads or the keep packing).
+ * While enabled, every call's attention kernel(s) carry a HIP event pair that
+ * their own dispatches record (hipExtLaunchKernel): the start when the first
+ * of them begins executing, the stop when the last one ends (Jeff: K prep
+ * and attention; never uploads or the keep packing).
  * take() synchronizes the stream and returns, then resets, the summed
  * duration in milliseconds and the number of timed launches. */
 int tfd_ctx_set_timing(tfd_ctx *ctx, int enabled);

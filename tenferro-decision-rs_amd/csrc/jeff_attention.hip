@@ -1756,7 +1756,8 @@ static size_t jeff_kp_main_bytes(const JeffArgs &a, int rows, int hd_pad, bool b
 }
 
 template <int HDP>
-static hipError_t launch_jeff_f32_hd(const JeffArgs &a, int rows, float *kp, hipStream_t stream) {
+static hipError_t launch_jeff_f32_hd(const JeffArgs &a, int rows, float *kp, hipStream_t stream,
+                                     const KernelEvents &ev) {
   dim3 pgrid((a.L + kKeyTile - 1) / kKeyTile, a.kv_heads, rows);
   // Query tiles of 16 in causal pairs, kJeffF32Waves / heads_per_group tiles
   // (half as many pairs) per workgroup.
@@ -1779,34 +1780,38 @@ static hipError_t launch_jeff_f32_hd(const JeffArgs &a, int rows, float *kp, hip
                                            jeff_kp_main_bytes(a, rows, HDP, false));
       uint32_t *kbits = reinterpret_cast<uint32_t *>(spans + 2 * rows);
       const dim3 sp((a.L + 15) / 16, a.kv_heads, rows);
-      hipLaunchKernelGGL(jeff_k_prep_split_kernel, sp, dim3(256), 0, stream, a, kp, spans, kbits);
+      hipExtLaunchKernelGGL(jeff_k_prep_split_kernel, sp, dim3(256), 0, stream, ev.start, nullptr,
+                            0, a, kp, spans, kbits);
       hipError_t e = hipGetLastError();
       if (e != hipSuccess) return e;
       const dim3 sgrid(nq * rows * a.heads);
-      hipLaunchKernelGGL((jeff_split_f32_kernel<HDP>), sgrid, dim3(256), 0, stream, a, kp, spans,
-                         kbits, rows);
+      hipExtLaunchKernelGGL((jeff_split_f32_kernel<HDP>), sgrid, dim3(256), 0, stream, nullptr,
+                            ev.stop, 0, a, kp, spans, kbits, rows);
       return hipGetLastError();
     }
   }
-  hipLaunchKernelGGL((jeff_k_prep_kernel<HDP, float>), pgrid, dim3(256), 0, stream, a, kp);
+  hipExtLaunchKernelGGL((jeff_k_prep_kernel<HDP, float>), pgrid, dim3(256), 0, stream, ev.start,
+                        nullptr, 0, a, kp);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const dim3 block(kJeffF32Waves * 64);
   if (vec)
-    hipLaunchKernelGGL((jeff_attention_f32_kernel<HDP, true>), grid, block, 0, stream, a, kp);
+    hipExtLaunchKernelGGL((jeff_attention_f32_kernel<HDP, true>), grid, block, 0, stream, nullptr,
+                          ev.stop, 0, a, kp);
   else
-    hipLaunchKernelGGL((jeff_attention_f32_kernel<HDP, false>), grid, block, 0, stream, a, kp);
+    hipExtLaunchKernelGGL((jeff_attention_f32_kernel<HDP, false>), grid, block, 0, stream, nullptr,
+                          ev.stop, 0, a, kp);
   return hipGetLastError();
 }
 
 hipError_t launch_jeff_attention_f32(const JeffArgs &a, int rows, int hd_pad, void *kp,
-                                     hipStream_t stream) {
+                                     hipStream_t stream, const KernelEvents &ev) {
   float *k = static_cast<float *>(kp);
   switch (hd_pad) {
-    case 32: return launch_jeff_f32_hd<32>(a, rows, k, stream);
-    case 64: return launch_jeff_f32_hd<64>(a, rows, k, stream);
-    case 128: return launch_jeff_f32_hd<128>(a, rows, k, stream);
-    case 256: return launch_jeff_f32_hd<256>(a, rows, k, stream);
+    case 32: return launch_jeff_f32_hd<32>(a, rows, k, stream, ev);
+    case 64: return launch_jeff_f32_hd<64>(a, rows, k, stream, ev);
+    case 128: return launch_jeff_f32_hd<128>(a, rows, k, stream, ev);
+    case 256: return launch_jeff_f32_hd<256>(a, rows, k, stream, ev);
     default: return hipErrorInvalidValue;
   }
 }
@@ -1827,9 +1832,10 @@ size_t jeff_kp_bytes(const JeffArgs &a, int rows, int hd_pad, bool bf16) {
 
 template <int HDP>
 static hipError_t launch_jeff_bf16_hd(const JeffArgs &a, int rows, uint16_t *kp,
-                                      hipStream_t stream) {
+                                      hipStream_t stream, const KernelEvents &ev) {
   dim3 pgrid((a.L + kKeyTile - 1) / kKeyTile, a.kv_heads, rows);
-  hipLaunchKernelGGL((jeff_k_prep_kernel<HDP, uint16_t>), pgrid, dim3(256), 0, stream, a, kp);
+  hipExtLaunchKernelGGL((jeff_k_prep_kernel<HDP, uint16_t>), pgrid, dim3(256), 0, stream, ev.start,
+                        nullptr, 0, a, kp);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   // Head dim 256: the 32x32x16 kernel, then this one as the exact pass over
@@ -1849,22 +1855,22 @@ static hipError_t launch_jeff_bf16_hd(const JeffArgs &a, int rows, uint16_t *kp,
   // 16-byte V loads along tokens need L % 8 == 0 and an aligned base.
   const bool vec = a.L % 8 == 0 && (reinterpret_cast<uintptr_t>(a.v) & 15) == 0;
   if (vec)
-    hipLaunchKernelGGL((jeff_attention_bf16_kernel<HDP, true>), grid, dim3(256), 0, stream, a, kp,
-                       redo, redo_qt);
+    hipExtLaunchKernelGGL((jeff_attention_bf16_kernel<HDP, true>), grid, dim3(256), 0, stream,
+                          nullptr, ev.stop, 0, a, kp, redo, redo_qt);
   else
-    hipLaunchKernelGGL((jeff_attention_bf16_kernel<HDP, false>), grid, dim3(256), 0, stream, a, kp,
-                       redo, redo_qt);
+    hipExtLaunchKernelGGL((jeff_attention_bf16_kernel<HDP, false>), grid, dim3(256), 0, stream,
+                          nullptr, ev.stop, 0, a, kp, redo, redo_qt);
   return hipGetLastError();
 }
 
 hipError_t launch_jeff_attention_bf16(const JeffArgs &a, int rows, int hd_pad, void *kp,
-                                      hipStream_t stream) {
+                                      hipStream_t stream, const KernelEvents &ev) {
   uint16_t *k = static_cast<uint16_t *>(kp);
   switch (hd_pad) {
-    case 32: return launch_jeff_bf16_hd<32>(a, rows, k, stream);
-    case 64: return launch_jeff_bf16_hd<64>(a, rows, k, stream);
-    case 128: return launch_jeff_bf16_hd<128>(a, rows, k, stream);
-    case 256: return launch_jeff_bf16_hd<256>(a, rows, k, stream);
+    case 32: return launch_jeff_bf16_hd<32>(a, rows, k, stream, ev);
+    case 64: return launch_jeff_bf16_hd<64>(a, rows, k, stream, ev);
+    case 128: return launch_jeff_bf16_hd<128>(a, rows, k, stream, ev);
+    case 256: return launch_jeff_bf16_hd<256>(a, rows, k, stream, ev);
     default: return hipErrorInvalidValue;
   }
 }

@@ -494,23 +494,33 @@ __global__ __launch_bounds__(256, laya_groups_per_cu(HDP)) void laya_attention_k
   // -------- Q: rotated, in registers. Lane (col, grp) holds
   // Q[q][grp*QS + x] for x < QS, the B operand of step x.
   float qreg[QS];
-  f32x4 qown[VEC ? QS / 4 : 1], qpar[VEC && ROPE ? QS / 4 : 1], qcs[VEC && ROPE ? QS / 4 : 1],
-      qsn[VEC && ROPE ? QS / 4 : 1];
   const int qq = qin ? q : 0;
   const int d0 = grp * QS;
-  const bool qlo = d0 < hh;  // VEC: lane groups 0, 1 hold the low half of the row
+  // VEC (hd == HDP): the wave's 16 Q rows are loaded along the rows, so that
+  // every load instruction reads whole cache lines once: task (t, p) is
+  // token q0w + t with its chunk pair (p, p + hd/8), the two 16-byte pieces
+  // that RoPE rotates together, plus table chunk p of that token. The
+  // rotated rows go to the wave's staging rows in LDS (the second K/V
+  // buffer, unused until the walk's first barrier has passed) and come back
+  // in the MFMA layout after the loads.
+  constexpr int QT = 16 * HDP / 8 / 64;  // tasks per lane
+  constexpr int QSR = HDP + 4;           // staging row stride: conflict-free 16-byte accesses
+  f32x4 qlo4[VEC ? QT : 1], qhi4[VEC ? QT : 1], qc4[VEC && ROPE ? QT : 1], qs4[VEC && ROPE ? QT : 1];
+  float *qst = nullptr;
   if constexpr (VEC) {
-    // hd == HDP: this lane's quarter of the row and (with RoPE) its partner
-    // quarter half a row away; 16-byte loads, all in flight together.
-    const float *row = xb + (size_t)qq * tok;
-    const int dp = qlo ? d0 + hh : d0 - hh, ci = qlo ? d0 : dp;
+    static_assert(2 * 16 * QSR <= Stage::KBUF && 2 * 16 * QSR <= Stage::VBUF,
+                  "Q staging: two waves per second K or V buffer");
+    qst = (wave < 2 ? Ks(1) : Vs(1)) + (wave & 1) * 16 * QSR;
 #pragma unroll
-    for (int c = 0; c < QS / 4; ++c) {
-      qown[c] = reinterpret_cast<const f32x4 *>(row + d0)[c];
+    for (int i = 0; i < QT; ++i) {
+      const int task = lane + 64 * i, pp = task % (HDP / 8), t = task / (HDP / 8);
+      const int tq = min(q0w + t, L - 1);
+      const float *row = xb + (size_t)tq * tok + 4 * pp;
+      qlo4[i] = *reinterpret_cast<const f32x4 *>(row);
+      qhi4[i] = *reinterpret_cast<const f32x4 *>(row + hh);
       if constexpr (ROPE) {
-        qpar[c] = reinterpret_cast<const f32x4 *>(row + dp)[c];
-        qcs[c] = reinterpret_cast<const f32x4 *>(a.cos_t + (size_t)qq * hh + ci)[c];
-        qsn[c] = reinterpret_cast<const f32x4 *>(a.sin_t + (size_t)qq * hh + ci)[c];
+        qc4[i] = *reinterpret_cast<const f32x4 *>(a.cos_t + (size_t)tq * hh + 4 * pp);
+        qs4[i] = *reinterpret_cast<const f32x4 *>(a.sin_t + (size_t)tq * hh + 4 * pp);
       }
     }
   }
@@ -599,10 +609,22 @@ __global__ __launch_bounds__(256, laya_groups_per_cu(HDP)) void laya_attention_k
 
   if constexpr (VEC) {
 #pragma unroll
+    for (int i = 0; i < QT; ++i) {
+      const int task = lane + 64 * i, pp = task % (HDP / 8), t = task / (HDP / 8);
+      f32x4 lo = qlo4[i], hi = qhi4[i];
+      if constexpr (ROPE) {
+        lo = rot_lo(qlo4[i], qhi4[i], qc4[i], qs4[i]);
+        hi = rot_hi(qlo4[i], qhi4[i], qc4[i], qs4[i]);
+      }
+      *reinterpret_cast<f32x4 *>(qst + t * QSR + 4 * pp) = lo;
+      *reinterpret_cast<f32x4 *>(qst + t * QSR + hh + 4 * pp) = hi;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
     for (int c = 0; c < QS / 4; ++c) {
-      f32x4 v = qown[c];
-      if constexpr (ROPE)
-        v = qlo ? rot_lo(qown[c], qpar[c], qcs[c], qsn[c]) : rot_hi(qpar[c], qown[c], qcs[c], qsn[c]);
+      const f32x4 v = *reinterpret_cast<const f32x4 *>(qst + col * QSR + d0 + 4 * c);
 #pragma unroll
       for (int e = 0; e < 4; ++e) qreg[4 * c + e] = qin ? v[e] : 0.0f;
     }
@@ -828,20 +850,20 @@ hipError_t launch_laya_keep_bits(const uint8_t *keep, uint32_t *bits, uint8_t *a
 
 template <int HDP, bool VEC, bool ROPE>
 static hipError_t launch_laya_hd(const LayaArgs &a, int heads, int batch, int mode,
-                                 hipStream_t stream) {
+                                 hipStream_t stream, const KernelEvents &ev) {
   dim3 grid((a.L + kLayaGroupQueries - 1) / kLayaGroupQueries, heads, batch);
   if (mode == kMaskBits)
-    hipLaunchKernelGGL((laya_attention_kernel<HDP, kMaskBits, VEC, ROPE>), grid, dim3(256), 0,
-                       stream, a);
+    hipExtLaunchKernelGGL((laya_attention_kernel<HDP, kMaskBits, VEC, ROPE>), grid, dim3(256), 0,
+                          stream, ev.start, ev.stop, 0, a);
   else
-    hipLaunchKernelGGL((laya_attention_kernel<HDP, kMaskStruct, VEC, ROPE>), grid, dim3(256), 0,
-                       stream, a);
+    hipExtLaunchKernelGGL((laya_attention_kernel<HDP, kMaskStruct, VEC, ROPE>), grid, dim3(256),
+                          0, stream, ev.start, ev.stop, 0, a);
   return hipGetLastError();
 }
 
 template <int HDP>
 static hipError_t launch_laya_pick(const LayaArgs &a, int heads, int batch, int mode,
-                                   hipStream_t stream) {
+                                   hipStream_t stream, const KernelEvents &ev) {
   // 16-byte row loads need hd == HDP, hd % 8 == 0 (RoPE halves in whole
   // chunks), a row stride of whole chunks and aligned bases.
   // Buffer loads also need one batch row of qkv within 2 GiB.
@@ -851,18 +873,18 @@ static hipError_t launch_laya_pick(const LayaArgs &a, int heads, int batch, int 
                    (size_t)a.L * 3 * (size_t)a.d * 4 < ((size_t)1 << 31);
   const bool rope = a.cos_t != nullptr;
   if (vec)
-    return rope ? launch_laya_hd<HDP, true, true>(a, heads, batch, mode, stream)
-                : launch_laya_hd<HDP, true, false>(a, heads, batch, mode, stream);
-  return rope ? launch_laya_hd<HDP, false, true>(a, heads, batch, mode, stream)
-              : launch_laya_hd<HDP, false, false>(a, heads, batch, mode, stream);
+    return rope ? launch_laya_hd<HDP, true, true>(a, heads, batch, mode, stream, ev)
+                : launch_laya_hd<HDP, true, false>(a, heads, batch, mode, stream, ev);
+  return rope ? launch_laya_hd<HDP, false, true>(a, heads, batch, mode, stream, ev)
+              : launch_laya_hd<HDP, false, false>(a, heads, batch, mode, stream, ev);
 }
 
 hipError_t launch_laya_attention(const LayaArgs &a, int heads, int batch, int hd_pad, int mode,
-                                 hipStream_t stream) {
+                                 hipStream_t stream, const KernelEvents &ev) {
   switch (hd_pad) {
-    case 32: return launch_laya_pick<32>(a, heads, batch, mode, stream);
-    case 64: return launch_laya_pick<64>(a, heads, batch, mode, stream);
-    case 128: return launch_laya_pick<128>(a, heads, batch, mode, stream);
+    case 32: return launch_laya_pick<32>(a, heads, batch, mode, stream, ev);
+    case 64: return launch_laya_pick<64>(a, heads, batch, mode, stream, ev);
+    case 128: return launch_laya_pick<128>(a, heads, batch, mode, stream, ev);
     default: return hipErrorInvalidValue;
   }
 }

@@ -224,23 +224,19 @@ int rope_table(tfd_ctx *c, int kind, size_t length, size_t dim, float base, uint
   return TFD_OK;
 }
 
-// Event pair around the next attention-kernel launch (timing enabled only).
-int timing_begin(tfd_ctx *c, hipEvent_t *after) {
-  *after = nullptr;
+// Event pair for the next op's attention kernel(s), recorded by their
+// dispatches (timing enabled only; both null otherwise).
+int timing_events(tfd_ctx *c, tfd::KernelEvents *ev) {
+  *ev = tfd::KernelEvents{};
   if (!c->timing) return TFD_OK;
   while (c->events.size() < 2 * (c->events_used + 1)) {
     hipEvent_t e;
     TFD_HIP(c, hipEventCreate(&e), "hipEventCreate");
     c->events.push_back(e);
   }
-  TFD_HIP(c, hipEventRecord(c->events[2 * c->events_used], c->stream), "hipEventRecord");
-  *after = c->events[2 * c->events_used + 1];
+  ev->start = c->events[2 * c->events_used];
+  ev->stop = c->events[2 * c->events_used + 1];
   c->events_used++;
-  return TFD_OK;
-}
-
-int timing_end(tfd_ctx *c, hipEvent_t after) {
-  if (after) TFD_HIP(c, hipEventRecord(after, c->stream), "hipEventRecord");
   return TFD_OK;
 }
 
@@ -340,11 +336,10 @@ int laya_run(tfd_ctx *c, const char *op, const float *qkv, const uint8_t *keep,
   } else {
     a.valid = static_cast<const uint8_t *>(mask_d);
   }
-  hipEvent_t after;
-  if ((rc = timing_begin(c, &after))) return rc;
-  TFD_HIP(c, tfd::launch_laya_attention(a, (int)heads, (int)batch, hd_pad, mode, c->stream),
+  tfd::KernelEvents ev;
+  if ((rc = timing_events(c, &ev))) return rc;
+  TFD_HIP(c, tfd::launch_laya_attention(a, (int)heads, (int)batch, hd_pad, mode, c->stream, ev),
           "laya_attention launch");
-  if ((rc = timing_end(c, after))) return rc;
   return finish(c, flags, out, out_d, sizeof(float) * n);
 }
 
@@ -411,11 +406,11 @@ int jeff_run(tfd_ctx *c, const char *op, bool bf16, size_t rows, size_t length, 
       return rc;
   }
   if ((rc = reserve(c, c->kp, tfd::jeff_kp_bytes(a, (int)rows, hd_pad, bf16)))) return rc;
-  hipEvent_t after;
-  if ((rc = timing_begin(c, &after))) return rc;
-  hipError_t e = bf16 ? tfd::launch_jeff_attention_bf16(a, (int)rows, hd_pad, c->kp.ptr, c->stream)
-                      : tfd::launch_jeff_attention_f32(a, (int)rows, hd_pad, c->kp.ptr, c->stream);
-  if ((rc = timing_end(c, after))) return rc;
+  tfd::KernelEvents ev;
+  if ((rc = timing_events(c, &ev))) return rc;
+  hipError_t e =
+      bf16 ? tfd::launch_jeff_attention_bf16(a, (int)rows, hd_pad, c->kp.ptr, c->stream, ev)
+           : tfd::launch_jeff_attention_f32(a, (int)rows, hd_pad, c->kp.ptr, c->stream, ev);
   if (e == hipErrorNotSupported)
     return fail(c, TFD_EUNSUPPORTED, "%s: this variant is not available", op);
   if (e != hipSuccess) return hip_fail(c, e, "jeff_attention launch");

@@ -2,6 +2,7 @@
 // kernels (laya_attention.hip, jeff_attention.hip). Not part of the C ABI.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -73,20 +74,28 @@ struct JeffArgs {
   size_t q_row, kv_row;          // elements per row: L*heads*hd and L*kv_heads*hd
 };
 
+// Timing of an op's attention kernel(s): `start` is recorded when the first
+// of them begins executing and `stop` when the last one ends (the dispatch
+// packets' own timestamps, hipExtLaunchKernel), so the pair measures the
+// kernels and not the queue around them. Both null: untimed.
+struct KernelEvents {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+
 // Kernel launchers (return the launch status). hd_pad selects the
 // compile-time padded head dim (32, 64, 128 or 256).
 hipError_t launch_fill_zero(float *out, size_t n, hipStream_t stream);
 hipError_t launch_laya_keep_bits(const uint8_t *keep, uint32_t *bits, uint8_t *any, int L, int B,
                                  int nkt, hipStream_t stream);
 hipError_t launch_laya_attention(const LayaArgs &a, int heads, int batch, int hd_pad, int mode,
-                                 hipStream_t stream);
+                                 hipStream_t stream, const KernelEvents &ev);
 // Jeff launchers run a K prep kernel into `kp` (workspace of
 // jeff_kp_bytes()) and then the attention kernel.
 size_t jeff_kp_bytes(const JeffArgs &a, int rows, int hd_pad, bool bf16);
 hipError_t launch_jeff_attention_f32(const JeffArgs &a, int rows, int hd_pad, void *kp,
-                                     hipStream_t stream);
+                                     hipStream_t stream, const KernelEvents &ev);
 hipError_t launch_jeff_attention_bf16(const JeffArgs &a, int rows, int hd_pad, void *kp,
-                                      hipStream_t stream);
+                                      hipStream_t stream, const KernelEvents &ev);
 // The bf16 kernel at head dim 256 on the 32x32x16 matrix cores (used by
 // launch_jeff_attention_bf16 when it fits): one flag per (row, head, query
 // tile of jeff_bf16_wide_query_tile) marks tiles left to the exact pass.

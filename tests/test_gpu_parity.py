@@ -70,6 +70,28 @@ def test_laya_c1_matches_oracle(gpu_ctx):
     assert_close(got, want, F32_TOL)
 
 
+def test_kernel_timing_events(gpu_ctx):
+    """Timed calls give the same outputs and one positive duration per call."""
+    w = laya_config(1)
+    j = jeff_config(4, rows=2, length=64)
+    gpu_ctx.take_kernel_time()
+    gpu_ctx.set_timing(True)
+    try:
+        got = laya_gpu(gpu_ctx, w.qkv, w.keep, w.hidden, w.heads, w.length, w.batch, w.rope_base)
+        gj = te.jeff_full_attention_rows(j.q, j.k, j.v, j.gate, j.q_norm, j.k_norm, j.mask, j.rows,
+                                         j.length, j.heads, j.kv_heads, j.head_dim, j.rotary_dim,
+                                         j.theta, j.eps, ctx=gpu_ctx)
+        ms, launches = gpu_ctx.take_kernel_time()
+    finally:
+        gpu_ctx.set_timing(False)
+    assert launches == 2 and 0.0 < ms < 1000.0
+    want = oracle.laya_attention_block(w.qkv, w.keep, w.hidden, w.heads, w.length, w.batch, w.rope_base)
+    assert_close(got, want, F32_TOL)
+    wj = oracle.jeff_rows(j.q, j.k, j.v, j.gate, j.q_norm, j.k_norm, j.mask, j.rows, j.length,
+                          j.heads, j.kv_heads, j.head_dim, j.rotary_dim, j.theta, j.eps)
+    assert_close(gj, wj, F32_TOL)
+
+
 @pytest.mark.parametrize("length", [1, 2, 31, 32, 33, 63, 64, 65, 127, 129, 200])
 @pytest.mark.parametrize("hd", [4, 16, 64, 128])
 def test_laya_sweep_keep_and_structured(gpu_ctx, length, hd):
