@@ -550,6 +550,31 @@ def test_jeff_bf16_hd256_nonfinite_takes_exact_pass(gpu_ctx):
     assert_close(got, want, BF16_TOL)
 
 
+@pytest.mark.parametrize("align", [0.4, 1.0])
+def test_jeff_bf16_hd256_score_growth(gpu_ctx, align):
+    """Head dim 256, no RoPE: key 200 points (fraction `align`) where query 230
+    of head 0 does, so that query's score there towers over every earlier
+    one (normalized rows: about 16 * align against ~N(0, 1)). At align 1 the
+    walk's reference would have to move by more than its slack under
+    accumulated output and the tile takes the exact pass; at 0.4 it stays in
+    the walk."""
+    rows, length, heads, kv, hd, rot = 1, 256, 4, 1, 256, 0
+    bits, vals, qn, kn, mask = bf16_case(13, rows, length, heads, kv, hd, False)
+    q, k, v, g = vals
+    Q = q.reshape(heads * hd, length)
+    K = k.reshape(kv * hd, length)
+    u = Q[:hd, 230] / np.linalg.norm(Q[:hd, 230])
+    r = K[:, 17] - np.dot(K[:, 17], u) * u
+    r /= np.linalg.norm(r)
+    K[:, 200] = (align * u + np.sqrt(1.0 - align * align) * r) * 16.0
+    bits = [te.to_bf16_bits(x) for x in (q, k, v, g)]
+    vals = [te.bf16_bits_to_f32(b) for b in bits]
+    want = oracle.jeff_rows(*vals, qn, kn, mask, rows, length, heads, kv, hd, rot, 1e7, 1e-6)
+    got = te.jeff_full_attention_rows(*bits, qn, kn, mask, rows, length, heads, kv, hd, rot, 1e7,
+                                      1e-6, bf16=True, ctx=gpu_ctx)
+    assert_close(got, want, BF16_TOL)
+
+
 def test_jeff_c5_reduced_matches_oracle(gpu_ctx):
     """C5 shape (GQA 8/2 x 256, causal, all active) at L 1024 against the oracle."""
     w = jeff_config(5, rows=2, length=1024)
