@@ -237,6 +237,7 @@ def run(args):
                     float((wj.mask[: 2 * wj.length] != 0).sum()) / t, 1)
                 also["C4"]["cpu_port_sample"] = f"2 of 16 rows, median of 3, {cores} threads"
             del tq, tk, tv, tg, tqn, tkn, tm, oj
+        also.update(layer_lines(args, ctx, dev))
     result["also"] = also
 
     # ------------------------------------------------------------ CPU baseline
@@ -257,6 +258,60 @@ def run(args):
         result["gpu_over_cpu"] = round(value / (flops / t_all / 1e12), 1)
     ctx.close()
     return result
+
+
+def _layer_steps(ctx, dev):
+    """Step functions of the two layer entries at the C2 and C4 shapes:
+    (name, step, attention flops, projection flops, valid tokens)."""
+    import numpy as np
+    import torch
+
+    import tenferro_ext as te
+    from tenferro_ext.workloads import jeff_layer_config, laya_layer_config
+
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    lw = laya_layer_config(2)
+    la = [t(a) for a in (lw.x, lw.keep, lw.w_in, lw.w_out)]
+    lo = torch.empty(lw.hidden * lw.length * lw.batch, dtype=torch.float32, device=dev)
+    lf = 4 * (lw.hidden // lw.heads) * int(lw.keep.astype(np.int64).sum()) * lw.heads
+
+    def laya_step():
+        te.laya_attention_layer(la[0], la[1], la[2], None, la[3], None, lw.hidden, lw.heads,
+                                lw.length, lw.batch, lw.rope_base, ctx=ctx, out=lo)
+
+    jw = jeff_layer_config(4)
+    ja = [t(getattr(jw, n)) for n in ("x", "w_q", "w_gate", "w_k", "w_v", "w_o", "q_norm",
+                                      "k_norm", "mask")]
+    jo = torch.empty(jw.rows * jw.length * jw.hidden, dtype=torch.float32, device=dev)
+    m = jw.mask.reshape(jw.rows, jw.length) != 0
+    # pairs counted as the C4 line counts them: each position t with the
+    # active keys at or before it
+    jf = 4 * jw.head_dim * int(np.cumsum(m, axis=1).sum()) * jw.heads
+
+    def jeff_step():
+        te.jeff_full_attention_layer_rows(*ja, jw.rows, jw.length, jw.hidden, jw.heads,
+                                          jw.kv_heads, jw.head_dim, jw.rotary_dim, jw.theta,
+                                          jw.eps, ctx=ctx, out=jo)
+
+    return [("C2_layer", laya_step, lf, lw.gemm_flops(), lw.valid.astype(np.int64).sum()),
+            ("C4_layer", jeff_step, jf, jw.gemm_flops(), int(m.sum()))]
+
+
+def layer_lines(args, ctx, dev):
+    """Whole attention layers (projections by rocBLAS sgemm + the fused op):
+    step time, the attention kernels' share, and the layer's f32 TFLOP/s."""
+    out = {}
+    for name, step, att_flops, gemm_flops, tokens in _layer_steps(ctx, dev):
+        log(f"[bench] {name}")
+        ms, kern = time_gpu(step, args.steps, args.warmup, ctx)
+        total = att_flops + gemm_flops
+        out[name] = {"ms_per_step": round(ms, 5), "attention_kernel_ms": round(kern, 5),
+                     "tflops": round(total / (ms * 1e-3) / 1e12, 3),
+                     "pct_of_f32_mfma_peak": round(100.0 * total / (ms * 1e-3) / 1e12
+                                                   / F32_MFMA_PEAK, 2),
+                     "tokens_per_s": round(float(tokens) / (ms * 1e-3), 1),
+                     "projection_flops": gemm_flops, "attention_flops": att_flops}
+    return out
 
 
 def run_only(args):
@@ -281,6 +336,13 @@ def run_only(args):
         torch.cuda.synchronize()
         return {"only": "copy", "bytes_read_per_copy": 4 * n, "bytes_written_per_copy": 4 * n}
     ctx = te.Context(0, stream=stream.cuda_stream)
+    if args.only.endswith("l"):
+        name, fn, att, gemm, _ = [s for s in _layer_steps(ctx, dev)
+                                  if s[0] == f"C{args.only[1]}_layer"][0]
+        ms, kern = time_gpu(fn, args.steps, args.warmup, ctx)
+        ctx.close()
+        return {"only": name, "ms_per_step": round(ms, 5), "attention_kernel_ms": round(kern, 5),
+                "tflops": round((att + gemm) / (ms * 1e-3) / 1e12, 3)}
     cfg = int(args.only[1])
     if cfg in (2, 3):
         w = laya_config(cfg)
@@ -337,7 +399,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="only the C2 headline")
-    ap.add_argument("--only", choices=["c2", "c3", "c4", "c5", "copy"], default=None,
+    ap.add_argument("--only", choices=["c2", "c3", "c4", "c5", "c2l", "c4l", "copy"], default=None,
                     help="profiling aid: run one configuration's op (steps + warmup calls), "
                          "print its timing line and skip everything else")
     args = ap.parse_args()

@@ -172,6 +172,52 @@ int tfd_jeff_full_attention_rows_bf16(tfd_ctx *ctx, size_t rows, size_t length, 
                                       uint32_t theta_bits, uint32_t eps_bits, float *out,
                                       unsigned flags);
 
+/*
+ * A whole Laya attention layer on the GPU: in_proj, the fused split + RoPE +
+ * attention op and out_proj, as attention_block_tenferro runs them on the
+ * f32 CPU path (laya-infer model.rs:1304-1347, linears by
+ * linear_feature_first, model.rs:1179-1216):
+ *   qkv      = W_in^T x (+ b_in)            (3*hidden, L, B)
+ *   attended = laya_attention_block(qkv, keep, hidden, heads, rope_base)
+ *   out      = W_out^T attended (+ b_out)   (hidden, L, B)
+ *   x, out: (hidden, L, B) feature-first, element f + hidden*(l + L*b).
+ *   w_in:   (hidden, 3*hidden) column-major, element i + hidden*o; b_in (3*hidden) or NULL.
+ *   w_out:  (hidden, hidden) column-major; b_out (hidden) or NULL.
+ *   keep:   (L, L, B) bytes as for tfd_laya_attention_block_f32.
+ * The linears run as f32 GEMMs (rocBLAS) on the context's stream; the
+ * intermediates live in the context's workspace.
+ */
+int tfd_laya_attention_layer_f32(tfd_ctx *ctx, const float *x, size_t hidden, size_t heads,
+                                 size_t length, size_t batch, const uint8_t *keep,
+                                 const float *w_in, const float *b_in, const float *w_out,
+                                 const float *b_out, uint32_t rope_base_bits, float *out,
+                                 unsigned flags);
+
+/*
+ * A whole Jeff full-attention layer over `rows` rows: the q, gate, k and v
+ * projections, the fused attention op (with native GQA) and o_proj, as
+ * full_attention_tenferro runs them on the f32 CPU path (jeff-infer
+ * model.rs:686-780, linears y = x W by linear_tenferro, model.rs:289-317):
+ *   q = x W_q, gate = x W_gate    (L, heads*head_dim)
+ *   k = x W_k, v = x W_v          (L, kv_heads*head_dim)
+ *   merged = the tfd_jeff_full_attention_rows_f32 op on them
+ *   out = merged W_o              (L, hidden)
+ *   x, out:       rows x (L, hidden), token-contiguous (t + L*i), row r at r*L*hidden.
+ *   w_q, w_gate:  (hidden, heads*head_dim) column-major, element i + hidden*o.
+ *   w_k, w_v:     (hidden, kv_heads*head_dim) column-major.
+ *   w_o:          (heads*head_dim, hidden) column-major.
+ *   q_norm, k_norm (head_dim), mask rows x (L): as for the rows op.
+ * The linears run as f32 GEMMs (rocBLAS) on the context's stream.
+ */
+int tfd_jeff_full_attention_layer_rows_f32(tfd_ctx *ctx, size_t rows, size_t length,
+                                           size_t hidden, size_t heads, size_t kv_heads,
+                                           size_t head_dim, size_t rotary_dim, const float *x,
+                                           const float *w_q, const float *w_gate,
+                                           const float *w_k, const float *w_v, const float *w_o,
+                                           const float *q_norm, const float *k_norm,
+                                           const float *mask, uint32_t theta_bits,
+                                           uint32_t eps_bits, float *out, unsigned flags);
+
 #ifdef __cplusplus
 }
 #endif

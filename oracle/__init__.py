@@ -161,3 +161,60 @@ def jeff_rows(q, k, v, gate, q_norm, k_norm, mask, rows, length, heads, kv_heads
         full[:, start:] = o.reshape(W, n)
         out[r * length * W:(r + 1) * length * W] = full.reshape(-1)
     return out
+
+
+# ------------------------------------------------------------------ layers
+#
+# The layer entries' linears restated as float32 GEMMs (numpy, i.e. a library
+# sgemm with f32 accumulation, like the reference's matrixmultiply / portable
+# gemm on the CPU path); the attention op between them is the C restatement.
+
+
+def _cols(flat, rows_of_matrix):
+    """A column-major (m, n) buffer as an (m, n) numpy view."""
+    return np.asarray(flat, np.float32).reshape(-1, rows_of_matrix).T
+
+
+def laya_attention_layer(x, keep, w_in, b_in, w_out, b_out, hidden, heads, length, batch,
+                         rope_base):
+    """attention_block_tenferro (laya-infer model.rs:1304-1347), f32 CPU path:
+    qkv = W_in^T x (+ b_in) by linear_feature_first (model.rs:1179-1216), the
+    Laya op, out = W_out^T attended (+ b_out). Flat (hidden, L, B) in and out."""
+    d, n = hidden, length * batch
+    X = _cols(x, d)                                  # (d, N)
+    qkv = _cols(w_in, d).T @ X                       # (3d, N)
+    if b_in is not None:
+        qkv = qkv + np.asarray(b_in, np.float32)[:, None]
+    att = laya_attention_block(np.ascontiguousarray(qkv.T).reshape(-1), keep, d, heads, length,
+                               batch, rope_base)
+    y = _cols(w_out, d).T @ _cols(att, d)            # (d, N)
+    if b_out is not None:
+        y = y + np.asarray(b_out, np.float32)[:, None]
+    return np.ascontiguousarray(y.T, np.float32).reshape(-1)
+
+
+def jeff_layer_rows(x, w_q, w_gate, w_k, w_v, w_o, q_norm, k_norm, mask, rows, length, hidden,
+                    heads, kv_heads, head_dim, rotary_dim, theta, eps, *, trim_leading=False):
+    """full_attention_tenferro (jeff-infer model.rs:686-780), f32 CPU path,
+    row by row: y = x W by linear_tenferro (model.rs:289-317) for q, gate, k
+    and v, the Jeff op (GQA), out = merged W_o. Flat rows x (L, hidden)."""
+    W, KW = heads * head_dim, kv_heads * head_dim
+    x = np.asarray(x, np.float32)
+    Wq, Wg = _cols(w_q, hidden), _cols(w_gate, hidden)
+    Wk, Wv, Wo = _cols(w_k, hidden), _cols(w_v, hidden), _cols(w_o, W)
+    flat = lambda m: np.ascontiguousarray(m.T, np.float32).reshape(-1)
+    q, g, k, v = [], [], [], []
+    for r in range(rows):
+        Xr = _cols(x[r * length * hidden:(r + 1) * length * hidden], length)  # (L, hidden)
+        q.append(flat(Xr @ Wq))
+        g.append(flat(Xr @ Wg))
+        k.append(flat(Xr @ Wk))
+        v.append(flat(Xr @ Wv))
+    merged = jeff_rows(np.concatenate(q), np.concatenate(k), np.concatenate(v), np.concatenate(g),
+                       q_norm, k_norm, mask, rows, length, heads, kv_heads, head_dim, rotary_dim,
+                       theta, eps, trim_leading=trim_leading)
+    out = []
+    for r in range(rows):
+        Mr = _cols(merged[r * length * W:(r + 1) * length * W], length)       # (L, W)
+        out.append(flat(Mr @ Wo))
+    return np.concatenate(out)

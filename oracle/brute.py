@@ -96,3 +96,33 @@ def jeff_full_attention_host(q, k, v, gate, q_norm, k_norm, mask, length, heads,
         o[empty] = 0.0 if zero_empty else np.nan
         out[f] = (o / (1.0 + np.exp(-gh))).T
     return out.reshape(-1)
+
+
+def laya_attention_layer_host(x, keep, w_in, b_in, w_out, b_out, hidden, heads, length, batch,
+                              rope_base):
+    """The Laya layer (laya-infer model.rs:1304-1347) in float64: linears as
+    float64 matrix products around laya_attention_host."""
+    d = hidden
+    X = np.asarray(x, np.float64).reshape(-1, d).T
+    qkv = np.asarray(w_in, np.float64).reshape(-1, d) @ X
+    if b_in is not None:
+        qkv = qkv + np.asarray(b_in, np.float64)[:, None]
+    att = laya_attention_host(qkv.T.reshape(-1), keep, d, heads, length, batch, rope_base)
+    y = np.asarray(w_out, np.float64).reshape(-1, d) @ att.reshape(-1, d).T
+    if b_out is not None:
+        y = y + np.asarray(b_out, np.float64)[:, None]
+    return y.T.reshape(-1)
+
+
+def jeff_layer_host(x, w_q, w_gate, w_k_expanded, w_v_expanded, w_o, q_norm, k_norm, mask,
+                    length, hidden, heads, head_dim, rotary_dim, theta, eps):
+    """One row of the Jeff layer (jeff-infer model.rs:686-780) in float64,
+    with K/V projections already expanded to every query head."""
+    W = heads * head_dim
+    X = np.asarray(x, np.float64).reshape(hidden, length).T                  # (L, hidden)
+    proj = lambda w: (X @ np.asarray(w, np.float64).reshape(-1, hidden).T).T.reshape(-1)
+    merged = jeff_full_attention_host(proj(w_q), proj(w_k_expanded), proj(w_v_expanded),
+                                      proj(w_gate), q_norm, k_norm, mask, length, heads,
+                                      head_dim, rotary_dim, theta, eps)
+    M = merged.reshape(W, length).T                                            # (L, W)
+    return (M @ np.asarray(w_o, np.float64).reshape(hidden, W).T).T.reshape(-1)

@@ -831,6 +831,14 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(float *__restrict__ out,
     out[i] = 0.0f;
 }
 
+__global__ __launch_bounds__(256) void add_row_bias_kernel(float *__restrict__ c,
+                                                           const float *__restrict__ b, int m,
+                                                           size_t total) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (size_t)gridDim.x * blockDim.x)
+    c[i] += b[i % (size_t)m];
+}
+
 // ----------------------------------------------------------------- launchers
 
 hipError_t launch_fill_zero(float *out, size_t n, hipStream_t stream) {
@@ -838,6 +846,16 @@ hipError_t launch_fill_zero(float *out, size_t n, hipStream_t stream) {
   size_t blocks = (n + 255) / 256;
   if (blocks > 4096) blocks = 4096;
   hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, out, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_add_row_bias(float *c, const float *b, int m, size_t n, hipStream_t stream) {
+  const size_t total = (size_t)m * n;
+  if (total == 0) return hipSuccess;
+  size_t blocks = (total + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(add_row_bias_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, c, b, m,
+                     total);
   return hipGetLastError();
 }
 

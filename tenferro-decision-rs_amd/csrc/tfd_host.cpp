@@ -9,6 +9,7 @@
 #include "tfd_attention.h"
 
 #include <hip/hip_runtime.h>
+#include <rocblas/rocblas.h>
 
 #include <cmath>
 #include <cstdarg>
@@ -52,9 +53,11 @@ struct tfd_ctx {
   bool ready = false;
   int cus = 0;  // compute units of the device (launch shape heuristics)
   std::string err;
-  DevBuf staging[8];  // uploads of host-pointer operands
+  DevBuf staging[12];  // uploads of host-pointer operands
   DevBuf bits;        // Laya packed keep words
   DevBuf kp;          // Jeff normalized + rotated keys
+  DevBuf layer;       // intermediates of the layer entries (projections, attention output)
+  rocblas_handle blas = nullptr;  // the layer entries' GEMMs, on `stream`
   std::vector<RopeEntry> rope;
   uint64_t clock = 0;
   bool timing = false;
@@ -438,6 +441,159 @@ int jeff_rows_common(tfd_ctx *c, bool bf16, size_t rows, size_t length, size_t h
                   q_norm, k_norm, mask, theta_bits, eps_bits, out, flags);
 }
 
+// ------------------------------------------------------------------ layers
+
+int blas_fail(tfd_ctx *c, rocblas_status st, const char *what) {
+  return fail(c, TFD_EHIP, "%s: rocBLAS status %d (%s)", what, (int)st,
+              rocblas_status_to_string(st));
+}
+
+int blas_ready(tfd_ctx *c) {
+  if (!c->blas) {
+    const rocblas_status st = rocblas_create_handle(&c->blas);
+    if (st != rocblas_status_success) {
+      c->blas = nullptr;
+      return blas_fail(c, st, "rocblas_create_handle");
+    }
+  }
+  const rocblas_status st = rocblas_set_stream(c->blas, c->stream);
+  if (st != rocblas_status_success) return blas_fail(c, st, "rocblas_set_stream");
+  return TFD_OK;
+}
+
+// C_b = op(A_b) op(B_b) for b < batch, column-major f32 (strides in
+// elements, 0 repeats an operand), on the context's stream.
+int gemm(tfd_ctx *c, bool ta, bool tb, size_t m, size_t n, size_t k, const float *A, size_t lda,
+         size_t sa, const float *B, size_t ldb, size_t sb, float *C, size_t ldc, size_t sc,
+         size_t batch) {
+  if (m > INT32_MAX || n > INT32_MAX || k > INT32_MAX || lda > INT32_MAX || ldb > INT32_MAX ||
+      ldc > INT32_MAX || batch > INT32_MAX)
+    return fail(c, TFD_EUNSUPPORTED, "linear: dimensions exceed the GEMM interface");
+  const float one = 1.0f, zero = 0.0f;
+  const rocblas_status st = rocblas_sgemm_strided_batched(
+      c->blas, ta ? rocblas_operation_transpose : rocblas_operation_none,
+      tb ? rocblas_operation_transpose : rocblas_operation_none, (rocblas_int)m, (rocblas_int)n,
+      (rocblas_int)k, &one, A, (rocblas_int)lda, (rocblas_stride)sa, B, (rocblas_int)ldb,
+      (rocblas_stride)sb, &zero, C, (rocblas_int)ldc, (rocblas_stride)sc, (rocblas_int)batch);
+  if (st != rocblas_status_success) return blas_fail(c, st, "rocblas_sgemm_strided_batched");
+  return TFD_OK;
+}
+
+// attention_block_tenferro (laya-infer model.rs:1304-1347) on the f32 path.
+int laya_layer(tfd_ctx *c, const float *x, size_t hidden, size_t heads, size_t length,
+               size_t batch, const uint8_t *keep, const float *w_in, const float *b_in,
+               const float *w_out, const float *b_out, uint32_t rope_bits, float *out,
+               unsigned flags) {
+  const char *op = "tfd_laya_attention_layer_f32";
+  size_t n = 0, tokens = 0, keep_len = 0, wi = 0, wo = 0;
+  if (!mul_ok(length, batch, &tokens) || !mul_ok(hidden, tokens, &n) ||
+      !mul_ok(length, length, &keep_len) || !mul_ok(keep_len, batch, &keep_len) ||
+      !mul_ok(hidden, hidden, &wo) || !mul_ok(wo, 3, &wi) || n > SIZE_MAX / 16)
+    return invalid(c, op, "shape", "attention dimensions overflow");
+  if (n == 0) return TFD_OK;
+  if (!x || !keep || !w_in || !w_out || !out) return invalid(c, op, "inputs", "null buffer");
+  int rc = ensure_ready(c);
+  if (rc) return rc;
+  if ((rc = blas_ready(c))) return rc;
+  const void *x_d = nullptr, *k_d = nullptr, *wi_d = nullptr, *wo_d = nullptr, *bi_d = nullptr,
+             *bo_d = nullptr;
+  void *out_d = nullptr;
+  if ((rc = operand(c, flags, 1, x, sizeof(float) * n, &x_d))) return rc;
+  if ((rc = operand(c, flags, 2, keep, keep_len, &k_d))) return rc;
+  if ((rc = operand(c, flags, 3, w_in, sizeof(float) * wi, &wi_d))) return rc;
+  if ((rc = operand(c, flags, 4, w_out, sizeof(float) * wo, &wo_d))) return rc;
+  if (b_in && (rc = operand(c, flags, 5, b_in, sizeof(float) * 3 * hidden, &bi_d))) return rc;
+  if (b_out && (rc = operand(c, flags, 6, b_out, sizeof(float) * hidden, &bo_d))) return rc;
+  if ((rc = output(c, flags, 0, out, sizeof(float) * n, &out_d))) return rc;
+  // Workspace: qkv (3d, L, B), then the attention output (d, L, B).
+  if ((rc = reserve(c, c->layer, sizeof(float) * 4 * n))) return rc;
+  float *qkv = static_cast<float *>(c->layer.ptr), *att = qkv + 3 * n;
+  // qkv = W_in^T x (+ b_in): linear_feature_first (model.rs:1179-1216).
+  if ((rc = gemm(c, true, false, 3 * hidden, tokens, hidden, static_cast<const float *>(wi_d),
+                 hidden, 0, static_cast<const float *>(x_d), hidden, 0, qkv, 3 * hidden, 0, 1)))
+    return rc;
+  if (bi_d)
+    TFD_HIP(c, tfd::launch_add_row_bias(qkv, static_cast<const float *>(bi_d), (int)(3 * hidden),
+                                        tokens, c->stream),
+            "bias launch");
+  if ((rc = laya_run(c, op, qkv, static_cast<const uint8_t *>(k_d), nullptr, -1, hidden, heads,
+                     length, batch, rope_bits, att, TFD_DEVICE_PTRS | TFD_ASYNC)))
+    return rc;
+  if ((rc = gemm(c, true, false, hidden, tokens, hidden, static_cast<const float *>(wo_d), hidden,
+                 0, att, hidden, 0, static_cast<float *>(out_d), hidden, 0, 1)))
+    return rc;
+  if (bo_d)
+    TFD_HIP(c, tfd::launch_add_row_bias(static_cast<float *>(out_d),
+                                        static_cast<const float *>(bo_d), (int)hidden, tokens,
+                                        c->stream),
+            "bias launch");
+  return finish(c, flags, out, out_d, sizeof(float) * n);
+}
+
+// full_attention_tenferro (jeff-infer model.rs:686-780) on the f32 path,
+// over rows.
+int jeff_layer(tfd_ctx *c, size_t rows, size_t length, size_t hidden, size_t heads,
+               size_t kv_heads, size_t head_dim, size_t rotary_dim, const float *x,
+               const float *w_q, const float *w_gate, const float *w_k, const float *w_v,
+               const float *w_o, const float *q_norm, const float *k_norm, const float *mask,
+               uint32_t theta_bits, uint32_t eps_bits, float *out, unsigned flags) {
+  const char *op = "tfd_jeff_full_attention_layer_rows_f32";
+  if (kv_heads == 0 || heads % kv_heads != 0)
+    return invalid(c, op, "kv_heads", "heads must be a multiple of kv_heads");
+  if (rotary_dim > head_dim)
+    return invalid(c, op, "rotary_dim", "rotary_dim must not exceed head_dim");
+  size_t W = 0, KW = 0, xn = 0, qn = 0, kvn = 0, mn = 0, wq = 0, wk = 0;
+  if (!mul_ok(heads, head_dim, &W) || !mul_ok(kv_heads, head_dim, &KW) ||
+      !mul_ok(length, hidden, &xn) || !mul_ok(xn, rows, &xn) || !mul_ok(length, W, &qn) ||
+      !mul_ok(qn, rows, &qn) || !mul_ok(length, KW, &kvn) || !mul_ok(kvn, rows, &kvn) ||
+      !mul_ok(rows, length, &mn) || !mul_ok(hidden, W, &wq) || !mul_ok(hidden, KW, &wk) ||
+      qn > SIZE_MAX / 32)
+    return invalid(c, op, "shape", "attention dimensions overflow");
+  if (xn == 0) return TFD_OK;
+  if (!x || !w_q || !w_gate || !w_k || !w_v || !w_o || !q_norm || !k_norm || !mask || !out)
+    return invalid(c, op, "inputs", "null buffer");
+  int rc = ensure_ready(c);
+  if (rc) return rc;
+  if ((rc = blas_ready(c))) return rc;
+  const void *x_d = nullptr, *wq_d = nullptr, *wg_d = nullptr, *wk_d = nullptr, *wv_d = nullptr,
+             *wo_d = nullptr, *qn_d = nullptr, *kn_d = nullptr, *m_d = nullptr;
+  void *out_d = nullptr;
+  if ((rc = operand(c, flags, 1, x, sizeof(float) * xn, &x_d))) return rc;
+  if ((rc = operand(c, flags, 2, w_q, sizeof(float) * wq, &wq_d))) return rc;
+  if ((rc = operand(c, flags, 3, w_gate, sizeof(float) * wq, &wg_d))) return rc;
+  if ((rc = operand(c, flags, 4, w_k, sizeof(float) * wk, &wk_d))) return rc;
+  if ((rc = operand(c, flags, 5, w_v, sizeof(float) * wk, &wv_d))) return rc;
+  if ((rc = operand(c, flags, 6, w_o, sizeof(float) * wq, &wo_d))) return rc;
+  if ((rc = operand(c, flags, 7, q_norm, sizeof(float) * head_dim, &qn_d))) return rc;
+  if ((rc = operand(c, flags, 8, k_norm, sizeof(float) * head_dim, &kn_d))) return rc;
+  if ((rc = operand(c, flags, 9, mask, sizeof(float) * mn, &m_d))) return rc;
+  if ((rc = output(c, flags, 0, out, sizeof(float) * xn, &out_d))) return rc;
+  // Workspace: q, gate, merged (rows x (L, W)), then k, v (rows x (L, KW)).
+  if ((rc = reserve(c, c->layer, sizeof(float) * (3 * qn + 2 * kvn)))) return rc;
+  float *q = static_cast<float *>(c->layer.ptr), *g = q + qn, *merged = g + qn, *k = merged + qn,
+        *v = k + kvn;
+  const float *xf = static_cast<const float *>(x_d);
+  // y_r = x_r W for every row r, (L, hidden) x (hidden, out): linear_tenferro
+  // (model.rs:289-317).
+  auto proj = [&](const void *w, size_t out_dim, float *y) {
+    return gemm(c, false, false, length, out_dim, hidden, xf, length, length * hidden,
+                static_cast<const float *>(w), hidden, 0, y, length, length * out_dim, rows);
+  };
+  if ((rc = proj(wq_d, W, q)) || (rc = proj(wg_d, W, g)) || (rc = proj(wk_d, KW, k)) ||
+      (rc = proj(wv_d, KW, v)))
+    return rc;
+  if ((rc = jeff_run(c, op, false, rows, length, heads, kv_heads, head_dim, rotary_dim, q, k, v, g,
+                     static_cast<const float *>(qn_d), static_cast<const float *>(kn_d),
+                     static_cast<const float *>(m_d), theta_bits, eps_bits, merged,
+                     (flags & TFD_TRIM_LEADING) | TFD_DEVICE_PTRS | TFD_ASYNC)))
+    return rc;
+  if ((rc = gemm(c, false, false, length, hidden, W, merged, length, length * W,
+                 static_cast<const float *>(wo_d), W, 0, static_cast<float *>(out_d), length,
+                 length * hidden, rows)))
+    return rc;
+  return finish(c, flags, out, out_d, sizeof(float) * xn);
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------- C ABI
@@ -474,6 +630,8 @@ void tfd_ctx_destroy(tfd_ctx *c) {
       if (b.ptr) (void)hipFree(b.ptr);
     if (c->bits.ptr) (void)hipFree(c->bits.ptr);
     if (c->kp.ptr) (void)hipFree(c->kp.ptr);
+    if (c->layer.ptr) (void)hipFree(c->layer.ptr);
+    if (c->blas) (void)rocblas_destroy_handle(c->blas);
     for (auto &e : c->rope) {
       (void)hipFree(e.cos_d);
       (void)hipFree(e.sin_d);
@@ -502,7 +660,7 @@ void *tfd_ctx_stream(tfd_ctx *c) {
 
 size_t tfd_ctx_retained_bytes(const tfd_ctx *c) {
   if (!c) return 0;
-  size_t total = sizeof(tfd_ctx) + c->bits.cap + c->kp.cap;
+  size_t total = sizeof(tfd_ctx) + c->bits.cap + c->kp.cap + c->layer.cap;
   for (const auto &b : c->staging) total += b.cap;
   for (const auto &e : c->rope) total += e.bytes;
   return total;
@@ -631,6 +789,36 @@ int tfd_jeff_full_attention_rows_bf16(tfd_ctx *c, size_t rows, size_t length, si
                                       unsigned flags) {
   return jeff_rows_common(c, true, rows, length, heads, kv_heads, head_dim, rotary_dim, q, k, v,
                           gate, q_norm, k_norm, mask, theta_bits, eps_bits, out, flags);
+}
+
+int tfd_laya_attention_layer_f32(tfd_ctx *c, const float *x, size_t hidden, size_t heads,
+                                 size_t length, size_t batch, const uint8_t *keep,
+                                 const float *w_in, const float *b_in, const float *w_out,
+                                 const float *b_out, uint32_t rope_base_bits, float *out,
+                                 unsigned flags) {
+  if (!c) return TFD_EINVAL;
+  c->err.clear();
+  int rc = check_flags(c, "tfd_laya_attention_layer_f32", flags, TFD_DEVICE_PTRS | TFD_ASYNC);
+  if (rc) return rc;
+  return laya_layer(c, x, hidden, heads, length, batch, keep, w_in, b_in, w_out, b_out,
+                    rope_base_bits, out, flags);
+}
+
+int tfd_jeff_full_attention_layer_rows_f32(tfd_ctx *c, size_t rows, size_t length,
+                                           size_t hidden, size_t heads, size_t kv_heads,
+                                           size_t head_dim, size_t rotary_dim, const float *x,
+                                           const float *w_q, const float *w_gate,
+                                           const float *w_k, const float *w_v, const float *w_o,
+                                           const float *q_norm, const float *k_norm,
+                                           const float *mask, uint32_t theta_bits,
+                                           uint32_t eps_bits, float *out, unsigned flags) {
+  if (!c) return TFD_EINVAL;
+  c->err.clear();
+  int rc = check_flags(c, "tfd_jeff_full_attention_layer_rows_f32", flags,
+                       TFD_DEVICE_PTRS | TFD_ASYNC | TFD_TRIM_LEADING);
+  if (rc) return rc;
+  return jeff_layer(c, rows, length, hidden, heads, kv_heads, head_dim, rotary_dim, x, w_q,
+                    w_gate, w_k, w_v, w_o, q_norm, k_norm, mask, theta_bits, eps_bits, out, flags);
 }
 
 }  // extern "C"

@@ -85,6 +85,9 @@ struct KernelEvents {
 // Kernel launchers (return the launch status). hd_pad selects the
 // compile-time padded head dim (32, 64, 128 or 256).
 hipError_t launch_fill_zero(float *out, size_t n, hipStream_t stream);
+// c[o + m*j] += b[o] for o < m, j < n: a column-major (m, n) matrix plus a
+// per-row bias (the linears of the layer entries).
+hipError_t launch_add_row_bias(float *c, const float *b, int m, size_t n, hipStream_t stream);
 hipError_t launch_laya_keep_bits(const uint8_t *keep, uint32_t *bits, uint8_t *any, int L, int B,
                                  int nkt, hipStream_t stream);
 hipError_t launch_laya_attention(const LayaArgs &a, int heads, int batch, int hd_pad, int mode,

@@ -64,6 +64,8 @@ EXPORTED_SYMBOLS = (
     "tfd_jeff_full_attention_f32",
     "tfd_jeff_full_attention_rows_f32",
     "tfd_jeff_full_attention_rows_bf16",
+    "tfd_laya_attention_layer_f32",
+    "tfd_jeff_full_attention_layer_rows_f32",
 )
 
 
@@ -138,6 +140,9 @@ def load_library(path: Optional[str] = None) -> ctypes.CDLL:
             I, [P, S, S, S, S, S, S, P, P, P, P, P, P, P, U32, U32, P, F]),
         "tfd_jeff_full_attention_rows_bf16": (
             I, [P, S, S, S, S, S, S, P, P, P, P, P, P, P, U32, U32, P, F]),
+        "tfd_laya_attention_layer_f32": (I, [P, P, S, S, S, S, P, P, P, P, P, U32, P, F]),
+        "tfd_jeff_full_attention_layer_rows_f32": (
+            I, [P, S, S, S, S, S, S, S, P, P, P, P, P, P, P, P, P, U32, U32, P, F]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -489,3 +494,50 @@ def to_bf16_bits(x: np.ndarray) -> np.ndarray:
 
 def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
     return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+# ------------------------------------------------------------------ layers
+
+def laya_attention_layer(x, keep, w_in, b_in, w_out, b_out, hidden: int, heads: int,
+                         length: int, batch: int, rope_base: float, *,
+                         ctx: Optional[Context] = None, out=None):
+    """A Laya attention layer (laya-infer model.rs:1304-1347, f32 path):
+    qkv = W_in^T x (+ b_in), the fused attention op, out = W_out^T attended
+    (+ b_out). x and out are (hidden, L, B) flat, W_in (hidden, 3*hidden) and
+    W_out (hidden, hidden) column-major; biases may be None."""
+    ctx = ctx or default_context()
+    ax, ak = _Arg(x, np.float32, "x"), _Arg(keep, np.uint8, "keep")
+    awi, awo = _Arg(w_in, np.float32, "w_in"), _Arg(w_out, np.float32, "w_out")
+    abi, abo = _Arg(b_in, np.float32, "b_in"), _Arg(b_out, np.float32, "b_out")
+    flags = _flags([ax, ak, awi, awo, abi, abo])
+    if out is None:
+        out = _new_out(ax, hidden * length * batch)
+    a_out = _Arg(out, np.float32, "out")
+    ctx.check(ctx._lib.tfd_laya_attention_layer_f32(
+        ctx.handle, ax.ptr, hidden, heads, length, batch, ak.ptr, awi.ptr, abi.ptr, awo.ptr,
+        abo.ptr, f32_bits(rope_base), a_out.ptr, flags))
+    return a_out.obj
+
+
+def jeff_full_attention_layer_rows(x, w_q, w_gate, w_k, w_v, w_o, q_norm, k_norm, mask,
+                                   rows: int, length: int, hidden: int, heads: int,
+                                   kv_heads: int, head_dim: int, rotary_dim: int, theta: float,
+                                   eps: float, *, trim_leading: bool = False,
+                                   ctx: Optional[Context] = None, out=None):
+    """A Jeff full-attention layer over rows (jeff-infer model.rs:686-780, f32
+    path): q/gate/k/v = x W, the fused rows op with native GQA, out = merged
+    W_o. x and out are rows x (L, hidden) flat; weights (in, out) column-major."""
+    ctx = ctx or default_context()
+    args = [_Arg(a, np.float32, nm) for a, nm in
+            ((x, "x"), (w_q, "w_q"), (w_gate, "w_gate"), (w_k, "w_k"), (w_v, "w_v"),
+             (w_o, "w_o"), (q_norm, "q_norm"), (k_norm, "k_norm"), (mask, "mask"))]
+    flags = _flags(args)
+    if trim_leading:
+        flags |= TFD_TRIM_LEADING
+    if out is None:
+        out = _new_out(args[0], rows * length * hidden)
+    a_out = _Arg(out, np.float32, "out")
+    ctx.check(ctx._lib.tfd_jeff_full_attention_layer_rows_f32(
+        ctx.handle, rows, length, hidden, heads, kv_heads, head_dim, rotary_dim,
+        *[a.ptr for a in args], f32_bits(theta), f32_bits(eps), a_out.ptr, flags))
+    return a_out.obj

@@ -226,3 +226,88 @@ def jeff_config(cfg: int, *, rows: Optional[int] = None, length: Optional[int] =
         q, gate, k, v = (bf16_bits_to_f32(to_bf16_bits(x)) for x in (q, gate, k, v))
     return JeffWorkload(f"C{cfg}", R, L, H, KV, hd, rot, theta, eps, q, k, v, gate, q_norm,
                         k_norm, mask, bf16)
+
+
+# ------------------------------------------------------------------ layers
+#
+# Whole-layer inputs for the layer entries: unit activations x and
+# N(0, 0.02^2) projection weights (the reading under which configs[1] and
+# configs[3] give the projections' scale used above), seeded 100 + cfg.
+
+
+@dataclass
+class LayaLayerWorkload:
+    name: str
+    hidden: int
+    heads: int
+    length: int
+    batch: int
+    rope_base: float
+    x: np.ndarray       # flat (d, L, B)
+    w_in: np.ndarray    # flat (d, 3d) column-major
+    w_out: np.ndarray   # flat (d, d) column-major
+    b_in: Optional[np.ndarray]
+    b_out: Optional[np.ndarray]
+    valid: np.ndarray
+    window: int
+    keep: np.ndarray
+
+    def gemm_flops(self) -> int:
+        n = self.length * self.batch
+        return 2 * n * self.hidden * (3 * self.hidden) + 2 * n * self.hidden * self.hidden
+
+
+def laya_layer_config(cfg: int, *, bias: bool = False) -> LayaLayerWorkload:
+    """C1 or C2 shape (valid lengths as laya_config) with x and weights."""
+    base = laya_config(cfg)
+    d, L, B = base.hidden, base.length, base.batch
+    rng = Lcg(100 + cfg)
+    x = rng.normal(d * L * B).astype(np.float32)
+    w_in = (rng.normal(d * 3 * d) * 0.02).astype(np.float32)
+    w_out = (rng.normal(d * d) * 0.02).astype(np.float32)
+    b_in = (rng.normal(3 * d) * 0.02).astype(np.float32) if bias else None
+    b_out = (rng.normal(d) * 0.02).astype(np.float32) if bias else None
+    return LayaLayerWorkload(f"C{cfg}-layer", d, base.heads, L, B, base.rope_base, x, w_in, w_out,
+                             b_in, b_out, base.valid, base.window, base.keep)
+
+
+@dataclass
+class JeffLayerWorkload:
+    name: str
+    rows: int
+    length: int
+    hidden: int
+    heads: int
+    kv_heads: int
+    head_dim: int
+    rotary_dim: int
+    theta: float
+    eps: float
+    x: np.ndarray       # flat rows x (L, hidden)
+    w_q: np.ndarray     # (hidden, W) column-major
+    w_gate: np.ndarray
+    w_k: np.ndarray     # (hidden, KW)
+    w_v: np.ndarray
+    w_o: np.ndarray     # (W, hidden)
+    q_norm: np.ndarray
+    k_norm: np.ndarray
+    mask: np.ndarray
+
+    def gemm_flops(self) -> int:
+        W, KW = self.heads * self.head_dim, self.kv_heads * self.head_dim
+        t = self.rows * self.length
+        return 2 * t * self.hidden * (2 * W + 2 * KW) + 2 * t * W * self.hidden
+
+
+def jeff_layer_config(cfg: int = 4, *, rows: Optional[int] = None,
+                      length: Optional[int] = None, hidden: int = 1024) -> JeffLayerWorkload:
+    """C4 shape (mask as jeff_config) with x and weights."""
+    base = jeff_config(cfg, rows=rows, length=length)
+    R, L, H, KV, hd = base.rows, base.length, base.heads, base.kv_heads, base.head_dim
+    W, KW = H * hd, KV * hd
+    rng = Lcg(100 + cfg)
+    x = rng.normal(R * L * hidden).astype(np.float32)
+    w = lambda n: (rng.normal(n) * 0.02).astype(np.float32)
+    return JeffLayerWorkload(f"C{cfg}-layer", R, L, hidden, H, KV, hd, base.rotary_dim, base.theta,
+                             base.eps, x, w(hidden * W), w(hidden * W), w(hidden * KW),
+                             w(hidden * KW), w(W * hidden), base.q_norm, base.k_norm, base.mask)
