@@ -238,6 +238,7 @@ def run(args):
                 also["C4"]["cpu_port_sample"] = f"2 of 16 rows, median of 3, {cores} threads"
             del tq, tk, tv, tg, tqn, tkn, tm, oj
         also.update(layer_lines(args, ctx, dev))
+        also["laya_model_forward"] = model_line(args, ctx, dev)
     result["also"] = also
 
     # ------------------------------------------------------------ CPU baseline
@@ -314,6 +315,61 @@ def layer_lines(args, ctx, dev):
     return out
 
 
+def _model_step(ctx, dev):
+    """The Laya decision-model forward at ModernBERT-base shape (22 layers,
+    d 768, 12 heads, intermediate 1152, local_attention 128, vocab 50368,
+    one head layer) on a C2-shaped batch (L 512, B 8, right padding with
+    valid lengths U{64..512}, 8 marker slots): (step, flops, valid tokens)."""
+    import numpy as np
+
+    from tenferro_ext.laya_model import LayaModel
+    from tenferro_ext.workloads import laya_config, laya_model_batch, laya_model_checkpoint
+
+    d, inter, layers, L, B, K = 768, 1152, 22, 512, 8, 8
+    ckpt = laya_model_checkpoint(vocab=50368, hidden=d, intermediate=inter, layers=layers,
+                                 heads=12, local_attention=128, seed=2, fast=True)
+    ids, _mask, pos, mm, qtype = laya_model_batch(L, B, K, 50368, min_len=64)
+    valid = laya_config(2, with_keep=False).valid.astype(bool)  # C2's row lengths
+    pos = np.minimum(pos, 63)                                   # markers inside every row
+    model = LayaModel(ckpt, ctx=ctx)
+    T = L * B
+    proj = 2 * T * (d * 3 * d + d * d + d * 2 * inter + inter * d) * layers
+    head = 2 * T * (d * 3 * d + d * d + 2 * d * 4 * d)
+    pairs_global = int(sum(L * int(valid[b * L:(b + 1) * L].sum()) for b in range(B)))
+    att = 0
+    for kind in ckpt.encoder.layer_types:
+        if kind == "full_attention":
+            att += 4 * d * pairs_global
+        else:
+            w = laya_config(2, with_keep=False)
+            w.window = 64
+            att += 4 * d * w.kept_pairs()
+    att += 4 * d * pairs_global  # the head layer
+    import torch
+
+    dl = torch.empty(K * B, dtype=torch.float32, device=dev)
+    da = torch.empty(ckpt.agent.action_count() * B, dtype=torch.float32, device=dev)
+
+    def step():
+        model.forward(ids, valid, pos, mm, qtype, logits=dl, action=da)
+
+    return step, proj + head + att, int(valid.sum()), layers + 1
+
+
+def model_line(args, ctx, dev):
+    """Whole Laya forward: ms, tokens/s, f32 TFLOP/s (projections + attention
+    algorithmic flops) and the attention kernels' share of the step."""
+    step, flops, tokens, att_launches = _model_step(ctx, dev)
+    log("[bench] Laya model forward")
+    steps = max(3, args.steps // 5)
+    ms, kern = time_gpu(step, steps, max(1, args.warmup // 5), ctx)
+    return {"ms_per_step": round(ms, 4), "tokens_per_s": round(tokens / (ms * 1e-3), 1),
+            "tflops": round(flops / (ms * 1e-3) / 1e12, 3),
+            "attention_ms_per_step": round(kern * att_launches, 4), "steps": steps,
+            "workload": "ModernBERT-base shape (22 layers) + decision head, L 512, B 8, "
+                        "synthetic weights"}
+
+
 def run_only(args):
     """One configuration's op alone (for rocprofv3 runs of a single kernel)."""
     import numpy as np
@@ -336,6 +392,10 @@ def run_only(args):
         torch.cuda.synchronize()
         return {"only": "copy", "bytes_read_per_copy": 4 * n, "bytes_written_per_copy": 4 * n}
     ctx = te.Context(0, stream=stream.cuda_stream)
+    if args.only == "model":
+        res = model_line(args, ctx, dev)
+        ctx.close()
+        return {"only": "model", **res}
     if args.only.endswith("l"):
         name, fn, att, gemm, _ = [s for s in _layer_steps(ctx, dev)
                                   if s[0] == f"C{args.only[1]}_layer"][0]
@@ -399,7 +459,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="only the C2 headline")
-    ap.add_argument("--only", choices=["c2", "c3", "c4", "c5", "c2l", "c4l", "copy"], default=None,
+    ap.add_argument("--only", choices=["c2", "c3", "c4", "c5", "c2l", "c4l", "model", "copy"], default=None,
                     help="profiling aid: run one configuration's op (steps + warmup calls), "
                          "print its timing line and skip everything else")
     args = ap.parse_args()

@@ -1,0 +1,179 @@
+// Elementwise and per-column kernels of the Laya decision-model forward
+// (laya-infer model.rs:387-458, 635-645, 773-837, 867-977) around the fused
+// attention op and the rocBLAS projections. Activations are feature-first
+// column-major (d, columns): one column = one token (or marker) and its d
+// contiguous features, so a wavefront owns a column and its loads coalesce.
+// These kernels move a few bytes per flop and are bound by HBM / launch
+// latency; none of them is on the attention hot path.
+#include <math.h>
+
+#include "tfd_device.hpp"
+#include "tfd_internal.hpp"
+
+namespace tfd {
+namespace {
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// x * (1 + erf(x / sqrt 2)) / 2 (model.rs:312-314) with the device library's
+// erff (correctly rounded to within 2 ulp).
+__device__ __forceinline__ float gelu_erf(float x) {
+  return x * (1.0f + erff(x / 1.41421356237309515f)) / 2.0f;
+}
+
+__device__ __forceinline__ float activate(float x, int act) {
+  if (act == kActRelu) return fmaxf(x, 0.0f);
+  if (act == kActGelu) return gelu_erf(x);
+  return x;
+}
+
+// One wavefront per output column c: source column map ? map[c] : c of x
+// (leading dimension ldx), LayerNorm over its d features (layer_norm_host,
+// model.rs:387-422: mean, then the mean of squared deviations, then
+// (x - mean) * (1 / sqrt(var + eps)) * w (+ b)), then plus column
+// add_col[c / per] of `add` when given (the type embedding, model.rs:916-931).
+__global__ __launch_bounds__(256) void norm_columns_kernel(NormArgs a) {
+  const int lane = threadIdx.x & 63;
+  const long c = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (c >= a.cols) return;
+  const long src = a.map ? (long)a.map[c] : c;
+  const float *x = a.x + src * (long)a.ldx;
+  const int d = a.d;
+  float s = 0.0f;
+  for (int i = lane; i < d; i += 64) s += x[i];
+  const float mean = wave_sum(s) / (float)d;
+  float v = 0.0f;
+  for (int i = lane; i < d; i += 64) {
+    const float t = x[i] - mean;
+    v += t * t;
+  }
+  const float var = wave_sum(v) / (float)d;
+  const float inv = 1.0f / sqrtf(var + a.eps);
+  float *y = a.y + c * (long)d;
+  const float *t = a.add ? a.add + (long)a.add_col[c / a.per] * d : nullptr;
+  for (int i = lane; i < d; i += 64) {
+    float value = (x[i] - mean) * inv;
+    value = value * a.w[i];
+    if (a.b) value = value + a.b[i];
+    if (t) value = value + t[i];
+    y[i] = value;
+  }
+}
+
+// y[o + m*j] = act(y[o + m*j] + b[o]) (b may be null).
+__global__ __launch_bounds__(256) void bias_act_kernel(float *__restrict__ y,
+                                                       const float *__restrict__ b, int m,
+                                                       size_t total, int act) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (size_t)gridDim.x * blockDim.x) {
+    float v = y[i];
+    if (b) v = v + b[i % (size_t)m];
+    y[i] = activate(v, act);
+  }
+}
+
+// gelu_gate_host (model.rs:635-645): g[i + I*c] = gelu(u[i + 2I*c]) *
+// u[I + i + 2I*c], each u plus its bias when the projection has one.
+__global__ __launch_bounds__(256) void geglu_kernel(const float *__restrict__ u,
+                                                    const float *__restrict__ b, int inter,
+                                                    size_t cols, float *__restrict__ g) {
+  const size_t total = (size_t)inter * cols;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const size_t c = i / inter, f = i - c * inter;
+    float x = u[2 * inter * c + f], y = u[2 * inter * c + inter + f];
+    if (b) {
+      x = x + b[f];
+      y = y + b[inter + f];
+    }
+    g[i] = gelu_erf(x) * y;
+  }
+}
+
+// pool_host (model.rs:773-837) for batch column blockIdx.x, in the
+// reference's sequential order on one lane (K is a handful of markers), and
+// the pooled action-head input [h[:, 0, b]; top1; top1 - top2; entropy;
+// used / 255] (model.rs:944-952).
+__global__ __launch_bounds__(64) void pool_kernel(PoolArgs a) {
+  const int b = blockIdx.x;
+  const int K = a.k;
+  const float *raw = a.raw + (size_t)b * K;
+  const uint8_t *mm = a.marker_mask + (size_t)b * K;
+  float *lo = a.logits + (size_t)b * K;
+  float *pooled = a.pooled + (size_t)b * (a.d + 4);
+  const float *h0 = a.h + (size_t)b * a.L * a.d;
+  for (int i = threadIdx.x; i < a.d; i += 64) pooled[i] = h0[i];
+  if (threadIdx.x != 0) return;
+  float mx = -INFINITY;
+  int count = 0;
+  for (int j = 0; j < K; ++j) {
+    const float v = mm[j] ? raw[j] : -1.0e4f;
+    lo[j] = v;
+    mx = fmaxf(mx, v);
+    count += mm[j] ? 1 : 0;
+  }
+  float sum = 0.0f;
+  for (int j = 0; j < K; ++j) sum += expf(lo[j] - mx);
+  float top1 = -INFINITY, top2 = -INFINITY, ent = 0.0f;
+  for (int j = 0; j < K; ++j) {
+    const float p = expf(lo[j] - mx) / sum;
+    if (p > top1) {
+      top2 = top1;
+      top1 = p;
+    } else if (p > top2) {
+      top2 = p;
+    }
+    ent -= p * logf(fmaxf(p, 1.0e-9f));
+  }
+  const float used = (float)(count > 2 ? count : 2);
+  ent /= logf(used);
+  pooled[a.d] = top1;
+  pooled[a.d + 1] = top1 - top2;
+  pooled[a.d + 2] = ent;
+  pooled[a.d + 3] = used / 255.0f;
+}
+
+unsigned grid_for(size_t total) {
+  size_t blocks = (total + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  return (unsigned)(blocks ? blocks : 1);
+}
+
+}  // namespace
+
+hipError_t launch_norm_columns(const NormArgs &a, hipStream_t stream) {
+  if (a.cols <= 0) return hipSuccess;
+  hipLaunchKernelGGL(norm_columns_kernel, dim3((unsigned)((a.cols + 3) / 4)), dim3(256), 0, stream,
+                     a);
+  return hipGetLastError();
+}
+
+hipError_t launch_bias_act(float *y, const float *b, int m, size_t n, int act,
+                           hipStream_t stream) {
+  const size_t total = (size_t)m * n;
+  if (total == 0) return hipSuccess;
+  hipLaunchKernelGGL(bias_act_kernel, dim3(grid_for(total)), dim3(256), 0, stream, y, b, m, total,
+                     act);
+  return hipGetLastError();
+}
+
+hipError_t launch_geglu(const float *u, const float *b, int inter, size_t cols, float *g,
+                        hipStream_t stream) {
+  const size_t total = (size_t)inter * cols;
+  if (total == 0) return hipSuccess;
+  hipLaunchKernelGGL(geglu_kernel, dim3(grid_for(total)), dim3(256), 0, stream, u, b, inter, cols,
+                     g);
+  return hipGetLastError();
+}
+
+hipError_t launch_pool(const PoolArgs &a, int batch, hipStream_t stream) {
+  if (batch <= 0) return hipSuccess;
+  hipLaunchKernelGGL(pool_kernel, dim3((unsigned)batch), dim3(64), 0, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace tfd

@@ -7,10 +7,12 @@
 // kernels on the context's stream. No CPU fallback exists: every failure to
 // reach the GPU is reported as TFD_EHIP.
 #include "tfd_attention.h"
+#include "tfd_laya_model.h"
 
 #include <hip/hip_runtime.h>
 #include <rocblas/rocblas.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -57,6 +59,9 @@ struct tfd_ctx {
   DevBuf bits;        // Laya packed keep words
   DevBuf kp;          // Jeff normalized + rotated keys
   DevBuf layer;       // intermediates of the layer entries (projections, attention output)
+  DevBuf model;       // activations and token inputs of the model forward
+  std::vector<uint8_t> model_host;  // packed token inputs of the last model forward
+  bool model_inflight = false;      // an asynchronous forward may still read model_host
   rocblas_handle blas = nullptr;  // the layer entries' GEMMs, on `stream`
   std::vector<RopeEntry> rope;
   uint64_t clock = 0;
@@ -465,17 +470,50 @@ int blas_ready(tfd_ctx *c) {
 // elements, 0 repeats an operand), on the context's stream.
 int gemm(tfd_ctx *c, bool ta, bool tb, size_t m, size_t n, size_t k, const float *A, size_t lda,
          size_t sa, const float *B, size_t ldb, size_t sb, float *C, size_t ldc, size_t sc,
-         size_t batch) {
+         size_t batch, float beta = 0.0f) {
   if (m > INT32_MAX || n > INT32_MAX || k > INT32_MAX || lda > INT32_MAX || ldb > INT32_MAX ||
       ldc > INT32_MAX || batch > INT32_MAX)
     return fail(c, TFD_EUNSUPPORTED, "linear: dimensions exceed the GEMM interface");
-  const float one = 1.0f, zero = 0.0f;
+  const float one = 1.0f;
   const rocblas_status st = rocblas_sgemm_strided_batched(
       c->blas, ta ? rocblas_operation_transpose : rocblas_operation_none,
       tb ? rocblas_operation_transpose : rocblas_operation_none, (rocblas_int)m, (rocblas_int)n,
       (rocblas_int)k, &one, A, (rocblas_int)lda, (rocblas_stride)sa, B, (rocblas_int)ldb,
-      (rocblas_stride)sb, &zero, C, (rocblas_int)ldc, (rocblas_stride)sc, (rocblas_int)batch);
+      (rocblas_stride)sb, &beta, C, (rocblas_int)ldc, (rocblas_stride)sc, (rocblas_int)batch);
   if (st != rocblas_status_success) return blas_fail(c, st, "rocblas_sgemm_strided_batched");
+  return TFD_OK;
+}
+
+// attention_block_tenferro (laya-infer model.rs:1304-1347) on device
+// pointers: qkv = W_in^T x (+ b_in), the fused op under a keep tensor or a
+// structured (valid, window) mask, out = W_out^T attended (+ b_out); with
+// `accumulate` the projection adds into out (a residual stream). Uses the
+// context's layer workspace.
+int laya_layer_dev(tfd_ctx *c, const char *op, const float *x, size_t hidden, size_t heads,
+                   size_t length, size_t batch, const uint8_t *keep, const uint8_t *valid,
+                   int64_t window, const float *w_in, const float *b_in, const float *w_out,
+                   const float *b_out, uint32_t rope_bits, float *out, bool accumulate) {
+  const size_t tokens = length * batch, n = hidden * tokens;
+  int rc = 0;
+  // Workspace: qkv (3d, L, B), then the attention output (d, L, B).
+  if ((rc = reserve(c, c->layer, sizeof(float) * 4 * n))) return rc;
+  float *qkv = static_cast<float *>(c->layer.ptr), *att = qkv + 3 * n;
+  // qkv = W_in^T x (+ b_in): linear_feature_first (model.rs:1179-1216).
+  if ((rc = gemm(c, true, false, 3 * hidden, tokens, hidden, w_in, hidden, 0, x, hidden, 0, qkv,
+                 3 * hidden, 0, 1)))
+    return rc;
+  if (b_in)
+    TFD_HIP(c, tfd::launch_add_row_bias(qkv, b_in, (int)(3 * hidden), tokens, c->stream),
+            "bias launch");
+  if ((rc = laya_run(c, op, qkv, keep, valid, window, hidden, heads, length, batch, rope_bits, att,
+                     TFD_DEVICE_PTRS | TFD_ASYNC)))
+    return rc;
+  if ((rc = gemm(c, true, false, hidden, tokens, hidden, w_out, hidden, 0, att, hidden, 0, out,
+                 hidden, 0, 1, accumulate ? 1.0f : 0.0f)))
+    return rc;
+  if (b_out)
+    TFD_HIP(c, tfd::launch_add_row_bias(out, b_out, (int)hidden, tokens, c->stream),
+            "bias launch");
   return TFD_OK;
 }
 
@@ -505,28 +543,12 @@ int laya_layer(tfd_ctx *c, const float *x, size_t hidden, size_t heads, size_t l
   if (b_in && (rc = operand(c, flags, 5, b_in, sizeof(float) * 3 * hidden, &bi_d))) return rc;
   if (b_out && (rc = operand(c, flags, 6, b_out, sizeof(float) * hidden, &bo_d))) return rc;
   if ((rc = output(c, flags, 0, out, sizeof(float) * n, &out_d))) return rc;
-  // Workspace: qkv (3d, L, B), then the attention output (d, L, B).
-  if ((rc = reserve(c, c->layer, sizeof(float) * 4 * n))) return rc;
-  float *qkv = static_cast<float *>(c->layer.ptr), *att = qkv + 3 * n;
-  // qkv = W_in^T x (+ b_in): linear_feature_first (model.rs:1179-1216).
-  if ((rc = gemm(c, true, false, 3 * hidden, tokens, hidden, static_cast<const float *>(wi_d),
-                 hidden, 0, static_cast<const float *>(x_d), hidden, 0, qkv, 3 * hidden, 0, 1)))
+  if ((rc = laya_layer_dev(c, op, static_cast<const float *>(x_d), hidden, heads, length, batch,
+                           static_cast<const uint8_t *>(k_d), nullptr, -1,
+                           static_cast<const float *>(wi_d), static_cast<const float *>(bi_d),
+                           static_cast<const float *>(wo_d), static_cast<const float *>(bo_d),
+                           rope_bits, static_cast<float *>(out_d), false)))
     return rc;
-  if (bi_d)
-    TFD_HIP(c, tfd::launch_add_row_bias(qkv, static_cast<const float *>(bi_d), (int)(3 * hidden),
-                                        tokens, c->stream),
-            "bias launch");
-  if ((rc = laya_run(c, op, qkv, static_cast<const uint8_t *>(k_d), nullptr, -1, hidden, heads,
-                     length, batch, rope_bits, att, TFD_DEVICE_PTRS | TFD_ASYNC)))
-    return rc;
-  if ((rc = gemm(c, true, false, hidden, tokens, hidden, static_cast<const float *>(wo_d), hidden,
-                 0, att, hidden, 0, static_cast<float *>(out_d), hidden, 0, 1)))
-    return rc;
-  if (bo_d)
-    TFD_HIP(c, tfd::launch_add_row_bias(static_cast<float *>(out_d),
-                                        static_cast<const float *>(bo_d), (int)hidden, tokens,
-                                        c->stream),
-            "bias launch");
   return finish(c, flags, out, out_d, sizeof(float) * n);
 }
 
@@ -594,6 +616,259 @@ int jeff_layer(tfd_ctx *c, size_t rows, size_t length, size_t hidden, size_t hea
   return finish(c, flags, out, out_d, sizeof(float) * xn);
 }
 
+// ------------------------------------------------------------ model forward
+
+// LayerNorm columns (see tfd::NormArgs) on the context's stream.
+int norm_cols(tfd_ctx *c, const float *x, const int *map, long cols, size_t d, const float *w,
+              const float *b, float eps, float *y, const float *add = nullptr,
+              const int *add_col = nullptr, size_t per = 1) {
+  tfd::NormArgs a{};
+  a.x = x;
+  a.map = map;
+  a.w = w;
+  a.b = b;
+  a.add = add;
+  a.add_col = add_col;
+  a.y = y;
+  a.cols = cols;
+  a.ldx = (int)d;
+  a.d = (int)d;
+  a.per = (int)per;
+  a.eps = eps;
+  TFD_HIP(c, tfd::launch_norm_columns(a, c->stream), "norm launch");
+  return TFD_OK;
+}
+
+// y (out, cols) = W^T x for a column-major (in, out) weight, then + bias and
+// the activation (linear_host, model.rs:424-457, with the elementwise maps
+// the forward applies to its result). `accumulate`: y += W^T x instead.
+int linear_cols(tfd_ctx *c, const float *w, const float *b, size_t in, size_t out,
+                const float *x, size_t cols, float *y, int act, bool accumulate = false) {
+  int rc = gemm(c, true, false, out, cols, in, w, in, 0, x, in, 0, y, out, 0, 1,
+                accumulate ? 1.0f : 0.0f);
+  if (rc) return rc;
+  if (b || act != tfd::kActNone)
+    TFD_HIP(c, tfd::launch_bias_act(y, b, (int)out, cols, act, c->stream), "bias launch");
+  return TFD_OK;
+}
+
+int missing(tfd_ctx *c, const char *op, const std::string &field) {
+  return invalid(c, op, field.c_str(), "missing weights");
+}
+
+// LayaWeights::validate (model.rs:187-295) on the shapes the struct carries;
+// the element counts are fixed by those shapes.
+int validate_model(tfd_ctx *c, const char *op, const tfd_laya_model *m) {
+  const size_t d = m->hidden;
+  if (d == 0) return invalid(c, op, "encoder.hidden_size", "must be positive");
+  if (!m->tok_embeddings || m->vocab == 0)
+    return invalid(c, op, "laya.tok_embeddings", "shape must be (hidden, vocab)");
+  if (!m->embed_norm_w) return missing(c, op, "laya.embed_norm");
+  if (!m->final_norm_w) return missing(c, op, "laya.final_norm");
+  if (m->n_layers && !m->layers) return missing(c, op, "laya.layers");
+  for (size_t i = 0; i < m->n_layers; ++i) {
+    const tfd_laya_encoder_layer &l = m->layers[i];
+    const std::string f = "laya.layers[" + std::to_string(i) + "]";
+    if (m->heads == 0 || d % m->heads != 0)
+      return invalid(c, op, (f + ".num_heads").c_str(), "must divide hidden_size");
+    if ((d / m->heads) % 2 != 0)
+      return invalid(c, op, (f + ".num_heads").c_str(),
+                     "the attention head dimension must be even for RoPE");
+    if (!l.wqkv) return missing(c, op, f + ".wqkv");
+    if (!l.wo) return missing(c, op, f + ".wo");
+    if (!l.mlp_norm_w) return missing(c, op, f + ".mlp_norm");
+    if (!l.wi) return missing(c, op, f + ".wi");
+    if (!l.wo_mlp) return missing(c, op, f + ".wo_mlp");
+    const float base = bits_to_f32(l.rope_base_bits);
+    if (!(std::isfinite(base) && base > 0.0f))
+      return invalid(c, op, (f + ".rope_base").c_str(), "must be a positive finite number");
+  }
+  if (m->n_layers && m->intermediate == 0) return missing(c, op, "laya.layers[0].wi");
+  if (!m->type_emb) return invalid(c, op, "laya.type_emb", "shape must be (hidden, 3)");
+  if (!m->scorer_norm_w) return missing(c, op, "laya.scorer_norm");
+  if (!m->scorer1_w) return missing(c, op, "laya.scorer1");
+  if (!m->scorer2_w) return missing(c, op, "laya.scorer2");
+  if (m->n_head_layers && !m->head) return missing(c, op, "laya.head");
+  for (size_t i = 0; i < m->n_head_layers; ++i) {
+    const tfd_laya_head_layer &h = m->head[i];
+    const std::string f = "laya.head[" + std::to_string(i) + "]";
+    if (h.heads == 0 || d % h.heads != 0)
+      return invalid(c, op, (f + ".num_heads").c_str(), "must divide hidden_size");
+    if (!h.norm1_w) return missing(c, op, f + ".norm1");
+    if (!h.in_proj_w) return missing(c, op, f + ".in_proj");
+    if (!h.out_proj_w) return missing(c, op, f + ".out_proj");
+    if (!h.norm2_w) return missing(c, op, f + ".norm2");
+    if (!h.linear1_w || h.ff == 0)
+      return invalid(c, op, (f + ".linear1").c_str(), "shape must be (hidden, ff)");
+    if (!h.linear2_w) return missing(c, op, f + ".linear2");
+  }
+  if (!m->act1_w || m->action_hidden == 0) return missing(c, op, "laya.act1");
+  if (!m->act2_w || m->actions == 0) return missing(c, op, "laya.act2");
+  return TFD_OK;
+}
+
+// forward_reference (laya-infer model.rs:867-977): encoder (646-713), typed
+// head (916-935), head layers (715-747), marker scorer (937-941), pooling
+// (773-837) and the action head (943-966), all on the context's stream.
+int laya_forward(tfd_ctx *c, const tfd_laya_model *m, const int64_t *ids, const uint8_t *mask,
+                 size_t L, size_t B, const int64_t *marker_pos, const uint8_t *marker_mask,
+                 size_t K, const int64_t *qtype, float *logits, float *action, unsigned flags) {
+  const char *op = "tfd_laya_forward_f32";
+  if (!m) return invalid(c, op, "model", "null model");
+  // The reference's checks, in its order (model.rs:877-911, 661-669, 920-927).
+  if (B == 0) return invalid(c, op, "laya.qtype", "the batch must be non-empty");
+  if (L == 0) return invalid(c, op, "laya.ids", "ids must be a non-empty (L, B) batch");
+  if (!ids || !mask || !qtype || (K && (!marker_pos || !marker_mask)) || !logits || !action)
+    return invalid(c, op, "inputs", "null buffer");
+  int rc = validate_model(c, op, m);
+  if (rc) return rc;
+  if (K < 2) return invalid(c, op, "laya.marker_pos", "at least two marker slots are required");
+  const size_t d = m->hidden, I = m->intermediate, AH = m->action_hidden, A = m->actions;
+  size_t T = 0, KB = 0, xs = 0;
+  if (!mul_ok(L, B, &T) || !mul_ok(K, B, &KB) || !mul_ok(d, T, &xs) || T > (size_t)INT32_MAX ||
+      KB > (size_t)INT32_MAX || d > (size_t)INT32_MAX / 4 || xs > SIZE_MAX / 64)
+    return invalid(c, op, "shape", "dimensions overflow");
+  for (size_t t = 0; t < T; ++t)
+    if (ids[t] < 0 || (uint64_t)ids[t] >= m->vocab)
+      return invalid(c, op, "laya.ids", "token id is outside the vocabulary");
+  for (size_t b = 0; b < B; ++b)
+    if (qtype[b] < 0 || qtype[b] > 2)
+      return invalid(c, op, "laya.qtype", "qtype must be 0 (choice), 1 (score) or 2 (noul)");
+  // gather_markers_host reads token max(pos, 0) of its own row.
+  for (size_t j = 0; j < KB; ++j)
+    if (marker_pos[j] >= (int64_t)L)
+      return invalid(c, op, "laya.marker_pos", "marker position outside the sequence");
+  size_t ff_max = 0;
+  for (size_t i = 0; i < m->n_head_layers; ++i) ff_max = std::max(ff_max, m->head[i].ff);
+  const size_t wide = std::max(2 * I, ff_max);
+  if (wide > SIZE_MAX / 64 / (T ? T : 1)) return invalid(c, op, "shape", "dimensions overflow");
+  const float eps = bits_to_f32(m->eps_bits);
+  if ((rc = ensure_ready(c))) return rc;
+  if ((rc = blas_ready(c))) return rc;
+
+  // Host token inputs, packed: ids (T i32), marker columns (KB i32), qtype
+  // (B i32), valid (T u8), marker mask (KB u8).
+  if (c->model_inflight) {
+    TFD_HIP(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    c->model_inflight = false;
+  }
+  auto up = [](size_t bytes) { return (bytes + 255) & ~(size_t)255; };
+  const size_t o_cols = up(4 * T), o_qt = o_cols + up(4 * KB), o_valid = o_qt + up(4 * B),
+               o_mm = o_valid + up(T), host_bytes = o_mm + up(KB);
+  c->model_host.assign(host_bytes, 0);
+  uint8_t *hb = c->model_host.data();
+  int32_t *h_ids = reinterpret_cast<int32_t *>(hb), *h_cols = reinterpret_cast<int32_t *>(hb + o_cols),
+          *h_qt = reinterpret_cast<int32_t *>(hb + o_qt);
+  for (size_t t = 0; t < T; ++t) {
+    h_ids[t] = (int32_t)ids[t];
+    hb[o_valid + t] = mask[t] ? 1 : 0;
+  }
+  for (size_t j = 0; j < KB; ++j) {
+    const int64_t pos = marker_pos[j] < 0 ? 0 : marker_pos[j];
+    h_cols[j] = (int32_t)(pos + (int64_t)L * (int64_t)(j / K));
+    hb[o_mm + j] = marker_mask[j] ? 1 : 0;
+  }
+  for (size_t b = 0; b < B; ++b) h_qt[b] = (int32_t)qtype[b];
+
+  // Device workspace: the packed inputs, then float activations.
+  const size_t nf = 2 * xs + wide * T + I * T + 2 * d * KB + KB + (d + 4) * B + AH * B + A * B +
+                    KB + 64;
+  if ((rc = reserve(c, c->model, host_bytes + sizeof(float) * nf + 1024))) return rc;
+  uint8_t *db = static_cast<uint8_t *>(c->model.ptr);
+  TFD_HIP(c, hipMemcpyAsync(db, hb, host_bytes, hipMemcpyHostToDevice, c->stream),
+          "hipMemcpyAsync");
+  const int *d_ids = reinterpret_cast<const int *>(db);
+  const int *d_cols = reinterpret_cast<const int *>(db + o_cols);
+  const int *d_qt = reinterpret_cast<const int *>(db + o_qt);
+  const uint8_t *d_valid = db + o_valid, *d_mm = db + o_mm;
+  float *fp = reinterpret_cast<float *>(db + up(host_bytes));
+  auto take = [&](size_t n) {
+    float *p = fp;
+    fp += (n + 63) & ~(size_t)63;
+    return p;
+  };
+  float *x = take(xs), *a = take(xs), *u = take(wide * T), *g = take(I * T), *s0 = take(d * KB),
+        *s1 = take(d * KB), *raw = take(KB), *pooled = take((d + 4) * B), *a1 = take(AH * B);
+  const bool dev_out = (flags & TFD_DEVICE_PTRS) != 0;
+  float *act_d = dev_out ? action : take(A * B), *log_d = dev_out ? logits : take(KB);
+
+  // Encoder: x = LN(tok_embeddings[:, ids]) (model.rs:671-686).
+  if ((rc = norm_cols(c, m->tok_embeddings, d_ids, (long)T, d, m->embed_norm_w, m->embed_norm_b,
+                      eps, x)))
+    return rc;
+  for (size_t i = 0; i < m->n_layers; ++i) {
+    const tfd_laya_encoder_layer &l = m->layers[i];
+    const float *ain = x;
+    if (l.attn_norm_w) {
+      if ((rc = norm_cols(c, x, nullptr, (long)T, d, l.attn_norm_w, l.attn_norm_b, eps, a)))
+        return rc;
+      ain = a;
+    }
+    // z = x + attention_block(attn_input) (model.rs:693-704)
+    if ((rc = laya_layer_dev(c, op, ain, d, m->heads, L, B, nullptr, d_valid,
+                             l.sliding ? (int64_t)m->window : -1, l.wqkv, l.bqkv, l.wo, l.bo,
+                             l.rope_base_bits, x, true)))
+      return rc;
+    // z += Wo_mlp^T geglu(Wi^T LN(z)) (model.rs:706-710)
+    if ((rc = norm_cols(c, x, nullptr, (long)T, d, l.mlp_norm_w, l.mlp_norm_b, eps, a))) return rc;
+    if ((rc = gemm(c, true, false, 2 * I, T, d, l.wi, d, 0, a, d, 0, u, 2 * I, 0, 1))) return rc;
+    TFD_HIP(c, tfd::launch_geglu(u, l.bi, (int)I, T, g, c->stream), "geglu launch");
+    if ((rc = linear_cols(c, l.wo_mlp, l.bo_mlp, I, d, g, T, x, tfd::kActNone, true))) return rc;
+  }
+  // h = final_norm(x) + type_emb[:, qtype[b]] (model.rs:706-712, 916-931)
+  float *h = a, *n = x;
+  if ((rc = norm_cols(c, x, nullptr, (long)T, d, m->final_norm_w, m->final_norm_b, eps, h,
+                      m->type_emb, d_qt, L)))
+    return rc;
+  // Head layers, full attention without RoPE (model.rs:715-747, 932-935).
+  for (size_t i = 0; i < m->n_head_layers; ++i) {
+    const tfd_laya_head_layer &hl = m->head[i];
+    if ((rc = norm_cols(c, h, nullptr, (long)T, d, hl.norm1_w, hl.norm1_b, eps, n))) return rc;
+    if ((rc = laya_layer_dev(c, op, n, d, hl.heads, L, B, nullptr, d_valid, -1, hl.in_proj_w,
+                             hl.in_proj_b, hl.out_proj_w, hl.out_proj_b, 0u, h, true)))
+      return rc;
+    if ((rc = norm_cols(c, h, nullptr, (long)T, d, hl.norm2_w, hl.norm2_b, eps, n))) return rc;
+    if ((rc = linear_cols(c, hl.linear1_w, hl.linear1_b, d, hl.ff, n, T, u, tfd::kActRelu)))
+      return rc;
+    if ((rc = linear_cols(c, hl.linear2_w, hl.linear2_b, hl.ff, d, u, T, h, tfd::kActNone, true)))
+      return rc;
+  }
+  // Marker scorer: LN of the gathered columns, linear + GELU, linear to one
+  // logit per marker (model.rs:937-941).
+  if ((rc = norm_cols(c, h, d_cols, (long)KB, d, m->scorer_norm_w, m->scorer_norm_b, eps, s0)))
+    return rc;
+  if ((rc = linear_cols(c, m->scorer1_w, m->scorer1_b, d, d, s0, KB, s1, tfd::kActGelu))) return rc;
+  if ((rc = linear_cols(c, m->scorer2_w, m->scorer2_b, d, 1, s1, KB, raw, tfd::kActNone))) return rc;
+  tfd::PoolArgs pa{};
+  pa.raw = raw;
+  pa.marker_mask = d_mm;
+  pa.h = h;
+  pa.logits = log_d;
+  pa.pooled = pooled;
+  pa.k = (int)K;
+  pa.d = (int)d;
+  pa.L = (int)L;
+  TFD_HIP(c, tfd::launch_pool(pa, (int)B, c->stream), "pool launch");
+  // Action head (model.rs:954-966).
+  if ((rc = linear_cols(c, m->act1_w, m->act1_b, d + 4, AH, pooled, B, a1, tfd::kActGelu)))
+    return rc;
+  if ((rc = linear_cols(c, m->act2_w, m->act2_b, AH, A, a1, B, act_d, tfd::kActNone))) return rc;
+  if (dev_out) {
+    if (flags & TFD_ASYNC) {
+      c->model_inflight = true;
+      return TFD_OK;
+    }
+    TFD_HIP(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return TFD_OK;
+  }
+  TFD_HIP(c, hipMemcpyAsync(logits, log_d, sizeof(float) * KB, hipMemcpyDeviceToHost, c->stream),
+          "hipMemcpyAsync");
+  TFD_HIP(c, hipMemcpyAsync(action, act_d, sizeof(float) * A * B, hipMemcpyDeviceToHost, c->stream),
+          "hipMemcpyAsync");
+  TFD_HIP(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  return TFD_OK;
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------- C ABI
@@ -631,6 +906,7 @@ void tfd_ctx_destroy(tfd_ctx *c) {
     if (c->bits.ptr) (void)hipFree(c->bits.ptr);
     if (c->kp.ptr) (void)hipFree(c->kp.ptr);
     if (c->layer.ptr) (void)hipFree(c->layer.ptr);
+    if (c->model.ptr) (void)hipFree(c->model.ptr);
     if (c->blas) (void)rocblas_destroy_handle(c->blas);
     for (auto &e : c->rope) {
       (void)hipFree(e.cos_d);
@@ -660,7 +936,8 @@ void *tfd_ctx_stream(tfd_ctx *c) {
 
 size_t tfd_ctx_retained_bytes(const tfd_ctx *c) {
   if (!c) return 0;
-  size_t total = sizeof(tfd_ctx) + c->bits.cap + c->kp.cap + c->layer.cap;
+  size_t total = sizeof(tfd_ctx) + c->bits.cap + c->kp.cap + c->layer.cap + c->model.cap +
+                 c->model_host.capacity();
   for (const auto &b : c->staging) total += b.cap;
   for (const auto &e : c->rope) total += e.bytes;
   return total;
@@ -819,6 +1096,18 @@ int tfd_jeff_full_attention_layer_rows_f32(tfd_ctx *c, size_t rows, size_t lengt
   if (rc) return rc;
   return jeff_layer(c, rows, length, hidden, heads, kv_heads, head_dim, rotary_dim, x, w_q,
                     w_gate, w_k, w_v, w_o, q_norm, k_norm, mask, theta_bits, eps_bits, out, flags);
+}
+
+int tfd_laya_forward_f32(tfd_ctx *c, const tfd_laya_model *model, const int64_t *ids,
+                         const uint8_t *mask, size_t length, size_t batch,
+                         const int64_t *marker_pos, const uint8_t *marker_mask, size_t k_count,
+                         const int64_t *qtype, float *logits, float *action, unsigned flags) {
+  if (!c) return TFD_EINVAL;
+  c->err.clear();
+  int rc = check_flags(c, "tfd_laya_forward_f32", flags, TFD_DEVICE_PTRS | TFD_ASYNC);
+  if (rc) return rc;
+  return laya_forward(c, model, ids, mask, length, batch, marker_pos, marker_mask, k_count, qtype,
+                      logits, action, flags);
 }
 
 }  // extern "C"

@@ -109,4 +109,42 @@ size_t jeff_bf16_flags_offset(const JeffArgs &a, int rows);
 hipError_t launch_jeff_bf16_wide(const JeffArgs &a, int rows, const uint16_t *kp, int *flags,
                                  hipStream_t stream);
 
+// ------------------------------------------------ Laya decision-model forward
+
+enum Activation : int { kActNone = 0, kActRelu = 1, kActGelu = 2 };
+
+// LayerNorm of `cols` feature columns (d features each): output column c
+// reads column map ? map[c] : c of x (column stride ldx); y is (d, cols).
+// add/add_col/per: optional y[:, c] += add[:, add_col[c / per]].
+struct NormArgs {
+  const float *x;
+  const int *map;
+  const float *w, *b;
+  const float *add;
+  const int *add_col;
+  float *y;
+  long cols;
+  int ldx, d, per;
+  float eps;
+};
+
+// Marker pooling: raw (K, B) logits, marker_mask (K, B) bytes, h (d, L, B)
+// head output; writes the masked logits (K, B) and pooled (d + 4, B).
+struct PoolArgs {
+  const float *raw;
+  const uint8_t *marker_mask;
+  const float *h;
+  float *logits, *pooled;
+  int k, d, L;
+};
+
+hipError_t launch_norm_columns(const NormArgs &a, hipStream_t stream);
+// y[o + m*j] = act(y[o + m*j] + b[o]) for o < m, j < n (b may be null).
+hipError_t launch_bias_act(float *y, const float *b, int m, size_t n, int act,
+                           hipStream_t stream);
+// g (I, cols) = gelu(u[:I] + b[:I]) * (u[I:] + b[I:]) per column of u (2I, cols).
+hipError_t launch_geglu(const float *u, const float *b, int inter, size_t cols, float *g,
+                        hipStream_t stream);
+hipError_t launch_pool(const PoolArgs &a, int batch, hipStream_t stream);
+
 }  // namespace tfd

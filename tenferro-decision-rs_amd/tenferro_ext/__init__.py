@@ -66,6 +66,7 @@ EXPORTED_SYMBOLS = (
     "tfd_jeff_full_attention_rows_bf16",
     "tfd_laya_attention_layer_f32",
     "tfd_jeff_full_attention_layer_rows_f32",
+    "tfd_laya_forward_f32",
 )
 
 
@@ -143,6 +144,7 @@ def load_library(path: Optional[str] = None) -> ctypes.CDLL:
         "tfd_laya_attention_layer_f32": (I, [P, P, S, S, S, S, P, P, P, P, P, U32, P, F]),
         "tfd_jeff_full_attention_layer_rows_f32": (
             I, [P, S, S, S, S, S, S, S, P, P, P, P, P, P, P, P, P, U32, U32, P, F]),
+        "tfd_laya_forward_f32": (I, [P, P, P, P, S, S, P, P, S, P, P, P, F]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)

@@ -311,3 +311,89 @@ def jeff_layer_config(cfg: int = 4, *, rows: Optional[int] = None,
     return JeffLayerWorkload(f"C{cfg}-layer", R, L, hidden, H, KV, hd, base.rotary_dim, base.theta,
                              base.eps, x, w(hidden * W), w(hidden * W), w(hidden * KW),
                              w(hidden * KW), w(W * hidden), base.q_norm, base.k_norm, base.mask)
+
+
+# ------------------------------------------------------------------ decision model
+#
+# Synthetic Laya decision models for the forward entry: the checkpoint
+# layout of a given shape with seeded random weights (linears N(0, 1/in),
+# norm scales 1 + N(0, 0.1^2), biases N(0, 0.1^2)), so that every component
+# of the forward moves its outputs.
+
+
+def laya_model_checkpoint(*, vocab=263, hidden=32, intermediate=48, layers=2, heads=2,
+                          local_attention=16, head_layers=1, actions=2, seed=7, max_len=None,
+                          fast=False):
+    """A LayaCheckpoint with random weights (see above) and the given shape.
+    fast: numpy's PCG64 normals instead of the LCG (model-size checkpoints)."""
+    from .laya_model import ACTION_HIDDEN, AgentConfig, EncoderConfig, LayaCheckpoint
+
+    enc = EncoderConfig.from_json({
+        "vocab_size": vocab, "hidden_size": hidden, "intermediate_size": intermediate,
+        "num_hidden_layers": layers, "num_attention_heads": heads,
+        "local_attention": local_attention,
+        "max_position_embeddings": max(8192, (max_len or 0) + 1)})
+    agent = AgentConfig(head_layers=head_layers, max_len=max_len or 512,
+                        head_max_len=min(192, (max_len or 512) - 1),
+                        action_names=[f"a{i}" for i in range(actions - 1)])
+    rng = Lcg(seed)
+    if fast:
+        gen = np.random.default_rng(seed)
+
+        class _Fast:
+            @staticmethod
+            def normal(n):
+                return gen.standard_normal(n, dtype=np.float32)
+        rng = _Fast()
+    d, inter = hidden, intermediate
+    lin = lambda n_in, n_out: (rng.normal(n_in * n_out) / np.sqrt(n_in)).astype(np.float32)
+    scale = lambda n: (1.0 + 0.1 * rng.normal(n)).astype(np.float32)
+    bias = lambda n: (0.1 * rng.normal(n)).astype(np.float32)
+    w = {"tok_embeddings": rng.normal(vocab * d).astype(np.float32),
+         "embed_norm.w": scale(d), "embed_norm.b": None}
+    for i in range(layers):
+        p = f"layers.{i}."
+        w[p + "attn_norm.w"] = scale(d) if i else None
+        w[p + "attn_norm.b"] = None
+        w[p + "wqkv.w"], w[p + "wqkv.b"] = lin(d, 3 * d), None
+        w[p + "wo.w"], w[p + "wo.b"] = lin(d, d), None
+        w[p + "mlp_norm.w"], w[p + "mlp_norm.b"] = scale(d), None
+        w[p + "wi.w"], w[p + "wi.b"] = lin(d, 2 * inter), None
+        w[p + "wo_mlp.w"], w[p + "wo_mlp.b"] = lin(inter, d), None
+    w["final_norm.w"], w["final_norm.b"] = scale(d), None
+    for i in range(head_layers):
+        p = f"head.{i}."
+        for part, n_in, n_out in (("in_proj", d, 3 * d), ("out_proj", d, d),
+                                  ("linear1", d, 4 * d), ("linear2", 4 * d, d)):
+            w[p + part + ".w"], w[p + part + ".b"] = lin(n_in, n_out), bias(n_out)
+        for part in ("norm1", "norm2"):
+            w[p + part + ".w"], w[p + part + ".b"] = scale(d), bias(d)
+    w["type_emb"] = rng.normal(3 * d).astype(np.float32)
+    w["scorer_norm.w"], w["scorer_norm.b"] = scale(d), bias(d)
+    w["scorer1.w"], w["scorer1.b"] = lin(d, d), bias(d)
+    w["scorer2.w"], w["scorer2.b"] = lin(d, 1), bias(1)
+    w["act1.w"], w["act1.b"] = lin(d + 4, ACTION_HIDDEN), bias(ACTION_HIDDEN)
+    w["act2.w"], w["act2.b"] = lin(ACTION_HIDDEN, actions), bias(actions)
+    return LayaCheckpoint(enc, agent, w, max(1, hidden // 64))
+
+
+def laya_model_batch(L, B, K, vocab, *, seed=11, min_len=None):
+    """Prompts for the forward: right-padded rows of random valid lengths in
+    [min_len, L], ids in [0, vocab), K marker slots at distinct valid
+    positions (the last slot masked in every other row), qtype cycling 0..2.
+    Returns flat column-major (ids, mask, marker_pos, marker_mask, qtype)."""
+    rng = Lcg(seed)
+    lo = min_len if min_len is not None else max(K + 1, L // 2)
+    lens = (lo + (rng.uniform(B) * (L - lo + 1)).astype(np.int64)).clip(lo, L)
+    ids = (rng.uniform(L * B) * vocab).astype(np.int64).clip(0, vocab - 1)
+    mask = np.zeros(L * B, bool)
+    pos = np.zeros(K * B, np.int64)
+    mm = np.ones(K * B, bool)
+    for b in range(B):
+        mask[b * L:b * L + lens[b]] = True
+        step = max(1, (int(lens[b]) - 1) // K)
+        pos[b * K:(b + 1) * K] = 1 + step * np.arange(K)
+        if b % 2:
+            mm[b * K + K - 1] = False
+    qtype = np.arange(B, dtype=np.int64) % 3
+    return ids, mask, pos, mm, qtype

@@ -12,7 +12,7 @@ import pytest
 import tenferro_ext as te
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "tfd_attention.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("tfd_attention.h", "tfd_laya_model.h")]
 
 
 @pytest.fixture(scope="module")
@@ -28,8 +28,13 @@ def ctx():
 
 
 def header_symbols():
-    text = open(HEADER).read()
+    text = "".join(open(h).read() for h in HEADERS)
     return sorted(set(re.findall(r"\b(tfd_\w+)\s*\(", text)))
+
+
+def test_every_header_is_checked():
+    on_disk = sorted(f for f in os.listdir(os.path.join(ROOT, "include")) if f.endswith(".h"))
+    assert on_disk == sorted(os.path.basename(h) for h in HEADERS)
 
 
 def test_library_exports_every_declared_symbol(lib):
