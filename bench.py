@@ -34,9 +34,32 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+SETTLE_S = 0.08
+_settled = {"steps": 0}
+
+
+def settle(fn, seconds=SETTLE_S):
+    """Untimed steps until the GPU has run `fn` back to back for `seconds` of
+    wall time. Its clocks ramp up over the first ~30 ms of continuous work
+    (kernel times fall 8-10% and then stay flat), so the timed steps measure
+    the steady state. The count is reported as "settle_steps"."""
+    import torch
+
+    t0 = time.perf_counter()
+    n = 0
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(20):
+            fn()
+        torch.cuda.synchronize()
+        n += 20
+    _settled["steps"] += n
+
+
 def time_gpu(fn, steps, warmup, ctx):
     """(ms per step by torch events on the shared stream, avg attention-kernel ms).
 
+    Before the `warmup` steps, settle() runs untimed steps until the clocks
+    are steady.
     Two passes of `steps` steps: the whole-op time, then the attention
     kernel's own mean duration from the library's HIP event pairs, which the
     kernel dispatches themselves record on the op's stream (start of the
@@ -45,6 +68,7 @@ def time_gpu(fn, steps, warmup, ctx):
     import tenferro_ext as te
 
     with te.asynchronous():
+        settle(fn)
         for _ in range(warmup):
             fn()
         torch.cuda.synchronize()
@@ -131,6 +155,7 @@ def run(args):
 
     log(f"[bench] C2 drop-in: {args.warmup} warmup + {args.steps} timed steps")
     ms, kern_ms = time_gpu(step, args.steps, args.warmup, ctx)
+    settle_steps = _settled["steps"]
     value = flops / (ms * 1e-3) / 1e12
     achieved = flops / (kern_ms * 1e-3) / 1e12
     tokens = w.valid_tokens()
@@ -141,6 +166,8 @@ def run(args):
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle": {"seconds": SETTLE_S, "untimed_steps": settle_steps,
+                   "note": "untimed steps before the warmup until the clocks are steady"},
         "ms_per_step": round(ms, 5),
         "higher_is_better": True,
         "scaling": "weak",

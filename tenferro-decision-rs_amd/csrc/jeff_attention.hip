@@ -1006,8 +1006,11 @@ __device__ __noinline__ void jeff_redo_wave(const JeffArgs *ap, const float *__r
 // flow is workgroup-uniform.
 //
 // Memory: K comes from the prep workspace in the split layout (each wave's
-// run of a tile is one contiguous 1 KB read), V columns straight from V, one
-// tile ahead, into registers. Q, the gate and the output move along tokens
+// run of a tile is one contiguous 1 KB read), V columns straight from V,
+// into registers at the top of each tile's step: without a second tile of
+// registers the kernel fits 128 VGPRs, and the four workgroups per CU that
+// this allows hide the load latency better than a one-tile prefetch at three
+// (5% on C4). Q, the gate and the output move along tokens
 // 16 bytes at a time and are transposed in the wave's own LDS rows, so a
 // wave issues four vector memory instructions per tensor. The row's key span
 // and active-key bits come from the prep (scalar loads).
@@ -1017,7 +1020,7 @@ __device__ __noinline__ void jeff_redo_wave(const JeffArgs *ap, const float *__r
 // (row, kv head) share an id residue mod 8 (one XCD, one L2) when the counts
 // allow it.
 template <int HDP>
-__global__ __launch_bounds__(256, 3) void jeff_split_f32_kernel(const JeffArgs a,
+__global__ __launch_bounds__(256, 4) void jeff_split_f32_kernel(const JeffArgs a,
                                                                 const float *__restrict__ kp,
                                                                 const int *__restrict__ spans,
                                                                 const uint32_t *__restrict__ kbits,
@@ -1085,7 +1088,7 @@ __global__ __launch_bounds__(256, 3) void jeff_split_f32_kernel(const JeffArgs a
   const __amdgpu_buffer_rsrc_t rv = buffer_rsrc(V, (uint32_t)((size_t)hd * L * 4));
   const int okk = wave * 4096 + lane * 16;
   const int ovv = ((wave * DS + col) * L + 4 * grp) * 4;
-  f32x4 kc[QS / 4], vc[NB], kn[QS / 4], vn[NB];
+  f32x4 kc[QS / 4], vc[NB];
   auto fetch = [&](int k0, f32x4 (&kr)[QS / 4], f32x4 (&vr)[NB]) {
     k0 = __builtin_amdgcn_readfirstlane(k0);  // uniform: scalar offsets, no waterfall
 #pragma unroll
@@ -1273,9 +1276,9 @@ __global__ __launch_bounds__(256, 3) void jeff_split_f32_kernel(const JeffArgs a
   for (int kt = kt_hi; kt >= kt_begin; --kt) {
     const bool more = kt > kt_begin;
     uint32_t bnext = 0u;
+    if (kt != kt_hi) fetch(kt * KT, kc, vc);
     if (more) {
       bnext = bits_of(kt - 1);
-      fetch((kt - 1) * KT, kn, vn);
     } else {
       load_gate();
     }
@@ -1346,13 +1349,7 @@ __global__ __launch_bounds__(256, 3) void jeff_split_f32_kernel(const JeffArgs a
           for (int j = 0; j < NB; ++j) O[j] = mfma_16x16x4(vc[j][r], ex[r], O[j]);
       }
     }
-    if (more) {
-#pragma unroll
-      for (int c = 0; c < QS / 4; ++c) kc[c] = kn[c];
-#pragma unroll
-      for (int j = 0; j < NB; ++j) vc[j] = vn[j];
-      w = keep_word(kt - 1, bnext);
-    }
+    if (more) w = keep_word(kt - 1, bnext);
   }
 
   // -------- careful redo (rare): the scores (shared) or this wave's O went
