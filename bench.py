@@ -220,6 +220,8 @@ def run(args):
                                                                   w3.batch, w3.window, w3.rope_base,
                                                                   ctx=ctx, out=o3),
                              args.steps, args.warmup, ctx)
+        if not args.no_cpu:
+            t3 = cpu_laya(w3, min(16, os.cpu_count() or 1), reps=3, warmup=1)
         also["C3"] = {"ms_per_step": round(ms3, 5), "kernel_ms": round(k3ms, 5),
                       "tflops": round(f3 / (ms3 * 1e-3) / 1e12, 3),
                       "kernel_tflops": round(f3 / (k3ms * 1e-3) / 1e12, 3),
@@ -227,6 +229,10 @@ def run(args):
                       "structured_kernel_tflops": round(f3 / (k3s * 1e-3) / 1e12, 3),
                       "tokens_per_s": round(w3.valid_tokens() / (ms3 * 1e-3), 1),
                       "algorithmic_flops": f3}
+        if not args.no_cpu:
+            also["C3"]["cpu_port_tflops"] = round(f3 / t3 / 1e12, 5)
+            also["C3"]["cpu_port_sample"] = (f"full C3 workload, median of 3 after 1, "
+                                             f"{min(16, os.cpu_count() or 1)} threads, {t3 * 1e3:.1f} ms")
         del q3, k3, v3, o3
 
         for cfg in (4, 5):
@@ -263,6 +269,14 @@ def run(args):
                 also["C4"]["cpu_port_tokens_per_s"] = round(
                     float((wj.mask[: 2 * wj.length] != 0).sum()) / t, 1)
                 also["C4"]["cpu_port_sample"] = f"2 of 16 rows, median of 3, {cores} threads"
+            if cfg == 5 and not args.no_cpu:
+                cores = min(16, os.cpu_count() or 1)
+                ws = jeff_config(5, rows=1, length=2048)
+                t = cpu_jeff_rows(ws, 1, cores, reps=1)
+                fs = 4 * ws.head_dim * ws.kept_pairs() * ws.heads
+                also["C5"]["cpu_port_tflops"] = round(fs / t / 1e12, 5)
+                also["C5"]["cpu_port_sample"] = (f"1 row x L 2048 of the C5 generator (f32 path), "
+                                                 f"{cores} threads, {t:.2f} s")
             del tq, tk, tv, tg, tqn, tkn, tm, oj
         also.update(layer_lines(args, ctx, dev))
         also["laya_model_forward"] = model_line(args, ctx, dev)
@@ -321,15 +335,29 @@ def _layer_steps(ctx, dev):
                                           jw.kv_heads, jw.head_dim, jw.rotary_dim, jw.theta,
                                           jw.eps, ctx=ctx, out=jo)
 
-    return [("C2_layer", laya_step, lf, lw.gemm_flops(), lw.valid.astype(np.int64).sum()),
-            ("C4_layer", jeff_step, jf, jw.gemm_flops(), int(m.sum()))]
+    def laya_cpu():
+        import oracle
+
+        oracle.laya_attention_layer(lw.x, lw.keep, lw.w_in, None, lw.w_out, None, lw.hidden,
+                                    lw.heads, lw.length, lw.batch, lw.rope_base)
+
+    def jeff_cpu():
+        import oracle
+
+        oracle.jeff_layer_rows(jw.x, jw.w_q, jw.w_gate, jw.w_k, jw.w_v, jw.w_o, jw.q_norm,
+                               jw.k_norm, jw.mask, jw.rows, jw.length, jw.hidden, jw.heads,
+                               jw.kv_heads, jw.head_dim, jw.rotary_dim, jw.theta, jw.eps)
+
+    return [("C2_layer", laya_step, lf, lw.gemm_flops(), lw.valid.astype(np.int64).sum(),
+             laya_cpu),
+            ("C4_layer", jeff_step, jf, jw.gemm_flops(), int(m.sum()), jeff_cpu)]
 
 
 def layer_lines(args, ctx, dev):
     """Whole attention layers (projections by rocBLAS sgemm + the fused op):
     step time, the attention kernels' share, and the layer's f32 TFLOP/s."""
     out = {}
-    for name, step, att_flops, gemm_flops, tokens in _layer_steps(ctx, dev):
+    for name, step, att_flops, gemm_flops, tokens, cpu_fn in _layer_steps(ctx, dev):
         log(f"[bench] {name}")
         ms, kern = time_gpu(step, args.steps, args.warmup, ctx)
         total = att_flops + gemm_flops
@@ -339,6 +367,20 @@ def layer_lines(args, ctx, dev):
                                                    / F32_MFMA_PEAK, 2),
                      "tokens_per_s": round(float(tokens) / (ms * 1e-3), 1),
                      "projection_flops": gemm_flops, "attention_flops": att_flops}
+        if not args.no_cpu:
+            import oracle
+
+            cores = min(16, os.cpu_count() or 1)
+            oracle.set_threads(cores)
+            times = []
+            for _ in range(3):
+                t0 = time.perf_counter()
+                cpu_fn()
+                times.append(time.perf_counter() - t0)
+            t = statistics.median(times[1:])
+            out[name]["cpu_port_tflops"] = round(total / t / 1e12, 5)
+            out[name]["cpu_port_sample"] = (f"full workload, oracle (numpy sgemm + C op), median "
+                                            f"of 2 after 1, {cores} threads, {t * 1e3:.1f} ms")
     return out
 
 
@@ -424,7 +466,7 @@ def run_only(args):
         ctx.close()
         return {"only": "model", **res}
     if args.only.endswith("l"):
-        name, fn, att, gemm, _ = [s for s in _layer_steps(ctx, dev)
+        name, fn, att, gemm, _, _ = [s for s in _layer_steps(ctx, dev)
                                   if s[0] == f"C{args.only[1]}_layer"][0]
         ms, kern = time_gpu(fn, args.steps, args.warmup, ctx)
         ctx.close()
