@@ -401,18 +401,19 @@ def _model_step(ctx, dev):
     valid = laya_config(2, with_keep=False).valid.astype(bool)  # C2's row lengths
     pos = np.minimum(pos, 63)                                   # markers inside every row
     model = LayaModel(ckpt, ctx=ctx)
-    T = L * B
+    # Flops of the valid tokens only (projections per valid token, attention
+    # per kept (query, key) pair of valid queries): the forward computes the
+    # padded tokens that no output reads as little as it can.
+    T = int(valid.sum())
     proj = 2 * T * (d * 3 * d + d * d + d * 2 * inter + inter * d) * layers
     head = 2 * T * (d * 3 * d + d * d + 2 * d * 4 * d)
-    pairs_global = int(sum(L * int(valid[b * L:(b + 1) * L].sum()) for b in range(B)))
+    lens = [int(valid[b * L:(b + 1) * L].sum()) for b in range(B)]
+    pairs_global = sum(n * n for n in lens)
+    q = np.arange(L)
+    pairs_local = sum(int((np.abs(q[:n, None] - q[None, :n]) <= 64).sum()) for n in lens)
     att = 0
     for kind in ckpt.encoder.layer_types:
-        if kind == "full_attention":
-            att += 4 * d * pairs_global
-        else:
-            w = laya_config(2, with_keep=False)
-            w.window = 64
-            att += 4 * d * w.kept_pairs()
+        att += 4 * d * (pairs_global if kind == "full_attention" else pairs_local)
     att += 4 * d * pairs_global  # the head layer
     import torch
 
@@ -436,7 +437,7 @@ def model_line(args, ctx, dev):
             "tflops": round(flops / (ms * 1e-3) / 1e12, 3),
             "attention_ms_per_step": round(kern * att_launches, 4), "steps": steps,
             "workload": "ModernBERT-base shape (22 layers) + decision head, L 512, B 8, "
-                        "synthetic weights"}
+                        "synthetic weights; flops of the valid tokens"}
 
 
 def run_only(args):

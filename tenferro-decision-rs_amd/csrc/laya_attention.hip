@@ -489,6 +489,12 @@ __global__ __launch_bounds__(256, laya_groups_per_cu(HDP)) void laya_attention_k
     const int qx = qg0 + lane;
     const uint8_t xv = vb[min(qx, L - 1)];
     padded = __ballot(qx < L && xv == 0) != 0;
+    // A caller that reads only some queries' outputs (the model forward)
+    // skips groups without one. Every wave takes the same branch before any
+    // barrier, so the workgroup leaves as a whole.
+    if (a.qneed != nullptr &&
+        __ballot(qx < L && a.qneed[(size_t)b * L + min(qx, L - 1)] != 0) == 0)
+      return;
   }
 
   // -------- Q: rotated, in registers. Lane (col, grp) holds

@@ -94,6 +94,27 @@ __global__ __launch_bounds__(256) void geglu_kernel(const float *__restrict__ u,
   }
 }
 
+// dst[:, dst_map ? dst_map[j] : j] = src[:, src_map ? src_map[j] : j] for
+// j < n, m floats per column: the packed <-> padded column moves around the
+// attention op. One wave per column.
+__global__ __launch_bounds__(256) void copy_columns_kernel(const float *__restrict__ src,
+                                                           const int *__restrict__ src_map,
+                                                           float *__restrict__ dst,
+                                                           const int *__restrict__ dst_map, int m,
+                                                           long n) {
+  const int lane = threadIdx.x & 63;
+  const long j = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (j >= n) return;
+  const float *s = src + (long)(src_map ? src_map[j] : j) * m;
+  float *d = dst + (long)(dst_map ? dst_map[j] : j) * m;
+  if ((m & 3) == 0) {
+    for (int i = 4 * lane; i < m; i += 256)
+      *reinterpret_cast<f32x4 *>(d + i) = *reinterpret_cast<const f32x4 *>(s + i);
+  } else {
+    for (int i = lane; i < m; i += 64) d[i] = s[i];
+  }
+}
+
 // pool_host (model.rs:773-837) for batch column blockIdx.x, in the
 // reference's sequential order on one lane (K is a handful of markers), and
 // the pooled action-head input [h[:, 0, b]; top1; top1 - top2; entropy;
@@ -105,7 +126,7 @@ __global__ __launch_bounds__(64) void pool_kernel(PoolArgs a) {
   const uint8_t *mm = a.marker_mask + (size_t)b * K;
   float *lo = a.logits + (size_t)b * K;
   float *pooled = a.pooled + (size_t)b * (a.d + 4);
-  const float *h0 = a.h + (size_t)b * a.L * a.d;
+  const float *h0 = a.h + (size_t)(a.h0_col ? a.h0_col[b] : b * a.L) * a.d;
   for (int i = threadIdx.x; i < a.d; i += 64) pooled[i] = h0[i];
   if (threadIdx.x != 0) return;
   float mx = -INFINITY;
@@ -167,6 +188,14 @@ hipError_t launch_geglu(const float *u, const float *b, int inter, size_t cols, 
   if (total == 0) return hipSuccess;
   hipLaunchKernelGGL(geglu_kernel, dim3(grid_for(total)), dim3(256), 0, stream, u, b, inter, cols,
                      g);
+  return hipGetLastError();
+}
+
+hipError_t launch_copy_columns(const float *src, const int *src_map, float *dst,
+                               const int *dst_map, int m, long n, hipStream_t stream) {
+  if (n <= 0 || m <= 0) return hipSuccess;
+  hipLaunchKernelGGL(copy_columns_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, stream, src,
+                     src_map, dst, dst_map, m, n);
   return hipGetLastError();
 }
 

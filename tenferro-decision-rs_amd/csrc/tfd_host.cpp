@@ -273,7 +273,8 @@ int check_flags(tfd_ctx *c, const char *op, unsigned flags, unsigned allowed) {
 
 int laya_run(tfd_ctx *c, const char *op, const float *qkv, const uint8_t *keep,
              const uint8_t *valid, int64_t window, size_t hidden, size_t heads, size_t length,
-             size_t batch, uint32_t rope_bits, float *out, unsigned flags) {
+             size_t batch, uint32_t rope_bits, float *out, unsigned flags,
+             const uint8_t *qneed = nullptr) {
   size_t n = 0, n3 = 0, keep_len = 0, valid_len = 0;
   if (!mul_ok(hidden, length, &n) || !mul_ok(n, batch, &n) || !mul_ok(n, 3, &n3) ||
       !mul_ok(length, length, &keep_len) || !mul_ok(keep_len, batch, &keep_len) ||
@@ -310,6 +311,7 @@ int laya_run(tfd_ctx *c, const char *op, const float *qkv, const uint8_t *keep,
   a.cus = c->cus;
   a.qkv = static_cast<const float *>(qkv_d);
   a.out = static_cast<float *>(out_d);
+  a.qneed = keep ? nullptr : qneed;
   a.d = (int)hidden;
   a.hd = (int)hd;
   a.half = (int)(hd / 2);
@@ -746,96 +748,146 @@ int laya_forward(tfd_ctx *c, const tfd_laya_model *m, const int64_t *ids, const 
   if ((rc = ensure_ready(c))) return rc;
   if ((rc = blas_ready(c))) return rc;
 
-  // Host token inputs, packed: ids (T i32), marker columns (KB i32), qtype
-  // (B i32), valid (T u8), marker mask (KB u8).
+  // The columns the outputs read: every valid token (keys, and queries whose
+  // states reach the head), token 0 of every prompt (pooled, model.rs:944-948)
+  // and every marker position (gather_markers_host, 749-771), even where
+  // padded. All per-token work runs on these packed columns only; other
+  // padded tokens never reach a valid token (they are masked as keys) or an
+  // output, so skipping them changes no result.
   if (c->model_inflight) {
     TFD_HIP(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize");
     c->model_inflight = false;
   }
+  std::vector<int32_t> pidx(T, -1);
+  for (size_t t = 0; t < T; ++t)
+    if (mask[t]) pidx[t] = 0;
+  for (size_t b = 0; b < B; ++b) pidx[L * b] = 0;
+  for (size_t j = 0; j < KB; ++j)
+    pidx[(size_t)(marker_pos[j] < 0 ? 0 : marker_pos[j]) + L * (j / K)] = 0;
+  size_t Tc = 0;
+  for (size_t t = 0; t < T; ++t)
+    if (pidx[t] == 0) pidx[t] = (int32_t)Tc++;
+  // Packed host inputs: ids, padded column, qtype per packed column (Tc
+  // i32 each); packed marker columns (KB i32); packed token 0 (B i32);
+  // valid (T u8); marker mask (KB u8).
   auto up = [](size_t bytes) { return (bytes + 255) & ~(size_t)255; };
-  const size_t o_cols = up(4 * T), o_qt = o_cols + up(4 * KB), o_valid = o_qt + up(4 * B),
-               o_mm = o_valid + up(T), host_bytes = o_mm + up(KB);
+  const size_t o_cols = up(4 * Tc), o_qt = o_cols + up(4 * Tc), o_mk = o_qt + up(4 * Tc),
+               o_h0 = o_mk + up(4 * KB), o_valid = o_h0 + up(4 * B), o_mm = o_valid + up(T),
+               o_need = o_mm + up(KB), host_bytes = o_need + up(T);
   c->model_host.assign(host_bytes, 0);
   uint8_t *hb = c->model_host.data();
   int32_t *h_ids = reinterpret_cast<int32_t *>(hb), *h_cols = reinterpret_cast<int32_t *>(hb + o_cols),
-          *h_qt = reinterpret_cast<int32_t *>(hb + o_qt);
+          *h_qt = reinterpret_cast<int32_t *>(hb + o_qt), *h_mk = reinterpret_cast<int32_t *>(hb + o_mk),
+          *h_h0 = reinterpret_cast<int32_t *>(hb + o_h0);
   for (size_t t = 0; t < T; ++t) {
-    h_ids[t] = (int32_t)ids[t];
     hb[o_valid + t] = mask[t] ? 1 : 0;
+    hb[o_need + t] = pidx[t] >= 0 ? 1 : 0;
+    if (pidx[t] >= 0) {
+      h_ids[pidx[t]] = (int32_t)ids[t];
+      h_cols[pidx[t]] = (int32_t)t;
+      h_qt[pidx[t]] = (int32_t)qtype[t / L];
+    }
   }
   for (size_t j = 0; j < KB; ++j) {
-    const int64_t pos = marker_pos[j] < 0 ? 0 : marker_pos[j];
-    h_cols[j] = (int32_t)(pos + (int64_t)L * (int64_t)(j / K));
+    h_mk[j] = pidx[(size_t)(marker_pos[j] < 0 ? 0 : marker_pos[j]) + L * (j / K)];
     hb[o_mm + j] = marker_mask[j] ? 1 : 0;
   }
-  for (size_t b = 0; b < B; ++b) h_qt[b] = (int32_t)qtype[b];
+  for (size_t b = 0; b < B; ++b) h_h0[b] = pidx[L * b];
 
-  // Device workspace: the packed inputs, then float activations.
-  const size_t nf = 2 * xs + wide * T + I * T + 2 * d * KB + KB + (d + 4) * B + AH * B + A * B +
-                    KB + 64;
-  if ((rc = reserve(c, c->model, host_bytes + sizeof(float) * nf + 1024))) return rc;
+  // Device workspace: the packed inputs, then float activations (packed
+  // unless named _f, the padded layout of the attention op).
+  const size_t xp = d * Tc;
+  const size_t nf = 2 * xp + wide * Tc + I * Tc + 3 * xp + xp + 3 * xs + xs + 2 * d * KB + KB +
+                    (d + 4) * B + AH * B + A * B + KB + 16 * 64;
+  if ((rc = reserve(c, c->model, up(host_bytes) + sizeof(float) * nf + 1024))) return rc;
   uint8_t *db = static_cast<uint8_t *>(c->model.ptr);
   TFD_HIP(c, hipMemcpyAsync(db, hb, host_bytes, hipMemcpyHostToDevice, c->stream),
           "hipMemcpyAsync");
   const int *d_ids = reinterpret_cast<const int *>(db);
   const int *d_cols = reinterpret_cast<const int *>(db + o_cols);
   const int *d_qt = reinterpret_cast<const int *>(db + o_qt);
-  const uint8_t *d_valid = db + o_valid, *d_mm = db + o_mm;
+  const int *d_mk = reinterpret_cast<const int *>(db + o_mk);
+  const int *d_h0 = reinterpret_cast<const int *>(db + o_h0);
+  const uint8_t *d_valid = db + o_valid, *d_mm = db + o_mm, *d_need = db + o_need;
   float *fp = reinterpret_cast<float *>(db + up(host_bytes));
   auto take = [&](size_t n) {
     float *p = fp;
     fp += (n + 63) & ~(size_t)63;
     return p;
   };
-  float *x = take(xs), *a = take(xs), *u = take(wide * T), *g = take(I * T), *s0 = take(d * KB),
-        *s1 = take(d * KB), *raw = take(KB), *pooled = take((d + 4) * B), *a1 = take(AH * B);
+  float *x = take(xp), *a = take(xp), *u = take(wide * Tc), *g = take(I * Tc),
+        *qkv_p = take(3 * xp), *att_p = take(xp), *qkv_f = take(3 * xs), *att_f = take(xs),
+        *s0 = take(d * KB), *s1 = take(d * KB), *raw = take(KB), *pooled = take((d + 4) * B),
+        *a1 = take(AH * B);
   const bool dev_out = (flags & TFD_DEVICE_PTRS) != 0;
   float *act_d = dev_out ? action : take(A * B), *log_d = dev_out ? logits : take(KB);
+  // Padded columns of the attention input that no packed column fills stay 0.
+  TFD_HIP(c, tfd::launch_fill_zero(qkv_f, 3 * xs, c->stream), "fill launch");
+
+  // attention_block_host (model.rs:612-633) on the packed columns, its
+  // result added into `res` (the residual stream): qkv projected for the
+  // packed columns, moved into the padded (3d, L, B) layout, the fused op
+  // under the structured mask (build_mask, 467-490; 64-query groups with no
+  // packed column are skipped), its packed columns projected by W_out.
+  auto attention = [&](const float *in, size_t heads, int64_t window, const float *w_in,
+                       const float *b_in, const float *w_out, const float *b_out,
+                       uint32_t rope_bits, float *res) {
+    int r = linear_cols(c, w_in, b_in, d, 3 * d, in, Tc, qkv_p, tfd::kActNone);
+    if (r) return r;
+    TFD_HIP(c, tfd::launch_copy_columns(qkv_p, nullptr, qkv_f, d_cols, (int)(3 * d), (long)Tc,
+                                        c->stream),
+            "copy launch");
+    if ((r = laya_run(c, op, qkv_f, nullptr, d_valid, window, d, heads, L, B, rope_bits, att_f,
+                      TFD_DEVICE_PTRS | TFD_ASYNC, d_need)))
+      return r;
+    TFD_HIP(c, tfd::launch_copy_columns(att_f, d_cols, att_p, nullptr, (int)d, (long)Tc, c->stream),
+            "copy launch");
+    return linear_cols(c, w_out, b_out, d, d, att_p, Tc, res, tfd::kActNone, true);
+  };
 
   // Encoder: x = LN(tok_embeddings[:, ids]) (model.rs:671-686).
-  if ((rc = norm_cols(c, m->tok_embeddings, d_ids, (long)T, d, m->embed_norm_w, m->embed_norm_b,
+  if ((rc = norm_cols(c, m->tok_embeddings, d_ids, (long)Tc, d, m->embed_norm_w, m->embed_norm_b,
                       eps, x)))
     return rc;
   for (size_t i = 0; i < m->n_layers; ++i) {
     const tfd_laya_encoder_layer &l = m->layers[i];
     const float *ain = x;
     if (l.attn_norm_w) {
-      if ((rc = norm_cols(c, x, nullptr, (long)T, d, l.attn_norm_w, l.attn_norm_b, eps, a)))
+      if ((rc = norm_cols(c, x, nullptr, (long)Tc, d, l.attn_norm_w, l.attn_norm_b, eps, a)))
         return rc;
       ain = a;
     }
     // z = x + attention_block(attn_input) (model.rs:693-704)
-    if ((rc = laya_layer_dev(c, op, ain, d, m->heads, L, B, nullptr, d_valid,
-                             l.sliding ? (int64_t)m->window : -1, l.wqkv, l.bqkv, l.wo, l.bo,
-                             l.rope_base_bits, x, true)))
+    if ((rc = attention(ain, m->heads, l.sliding ? (int64_t)m->window : -1, l.wqkv, l.bqkv, l.wo,
+                        l.bo, l.rope_base_bits, x)))
       return rc;
     // z += Wo_mlp^T geglu(Wi^T LN(z)) (model.rs:706-710)
-    if ((rc = norm_cols(c, x, nullptr, (long)T, d, l.mlp_norm_w, l.mlp_norm_b, eps, a))) return rc;
-    if ((rc = gemm(c, true, false, 2 * I, T, d, l.wi, d, 0, a, d, 0, u, 2 * I, 0, 1))) return rc;
-    TFD_HIP(c, tfd::launch_geglu(u, l.bi, (int)I, T, g, c->stream), "geglu launch");
-    if ((rc = linear_cols(c, l.wo_mlp, l.bo_mlp, I, d, g, T, x, tfd::kActNone, true))) return rc;
+    if ((rc = norm_cols(c, x, nullptr, (long)Tc, d, l.mlp_norm_w, l.mlp_norm_b, eps, a))) return rc;
+    if ((rc = gemm(c, true, false, 2 * I, Tc, d, l.wi, d, 0, a, d, 0, u, 2 * I, 0, 1))) return rc;
+    TFD_HIP(c, tfd::launch_geglu(u, l.bi, (int)I, Tc, g, c->stream), "geglu launch");
+    if ((rc = linear_cols(c, l.wo_mlp, l.bo_mlp, I, d, g, Tc, x, tfd::kActNone, true))) return rc;
   }
   // h = final_norm(x) + type_emb[:, qtype[b]] (model.rs:706-712, 916-931)
   float *h = a, *n = x;
-  if ((rc = norm_cols(c, x, nullptr, (long)T, d, m->final_norm_w, m->final_norm_b, eps, h,
-                      m->type_emb, d_qt, L)))
+  if ((rc = norm_cols(c, x, nullptr, (long)Tc, d, m->final_norm_w, m->final_norm_b, eps, h,
+                      m->type_emb, d_qt, 1)))
     return rc;
   // Head layers, full attention without RoPE (model.rs:715-747, 932-935).
   for (size_t i = 0; i < m->n_head_layers; ++i) {
     const tfd_laya_head_layer &hl = m->head[i];
-    if ((rc = norm_cols(c, h, nullptr, (long)T, d, hl.norm1_w, hl.norm1_b, eps, n))) return rc;
-    if ((rc = laya_layer_dev(c, op, n, d, hl.heads, L, B, nullptr, d_valid, -1, hl.in_proj_w,
-                             hl.in_proj_b, hl.out_proj_w, hl.out_proj_b, 0u, h, true)))
+    if ((rc = norm_cols(c, h, nullptr, (long)Tc, d, hl.norm1_w, hl.norm1_b, eps, n))) return rc;
+    if ((rc = attention(n, hl.heads, -1, hl.in_proj_w, hl.in_proj_b, hl.out_proj_w, hl.out_proj_b,
+                        0u, h)))
       return rc;
-    if ((rc = norm_cols(c, h, nullptr, (long)T, d, hl.norm2_w, hl.norm2_b, eps, n))) return rc;
-    if ((rc = linear_cols(c, hl.linear1_w, hl.linear1_b, d, hl.ff, n, T, u, tfd::kActRelu)))
+    if ((rc = norm_cols(c, h, nullptr, (long)Tc, d, hl.norm2_w, hl.norm2_b, eps, n))) return rc;
+    if ((rc = linear_cols(c, hl.linear1_w, hl.linear1_b, d, hl.ff, n, Tc, u, tfd::kActRelu)))
       return rc;
-    if ((rc = linear_cols(c, hl.linear2_w, hl.linear2_b, hl.ff, d, u, T, h, tfd::kActNone, true)))
+    if ((rc = linear_cols(c, hl.linear2_w, hl.linear2_b, hl.ff, d, u, Tc, h, tfd::kActNone, true)))
       return rc;
   }
   // Marker scorer: LN of the gathered columns, linear + GELU, linear to one
   // logit per marker (model.rs:937-941).
-  if ((rc = norm_cols(c, h, d_cols, (long)KB, d, m->scorer_norm_w, m->scorer_norm_b, eps, s0)))
+  if ((rc = norm_cols(c, h, d_mk, (long)KB, d, m->scorer_norm_w, m->scorer_norm_b, eps, s0)))
     return rc;
   if ((rc = linear_cols(c, m->scorer1_w, m->scorer1_b, d, d, s0, KB, s1, tfd::kActGelu))) return rc;
   if ((rc = linear_cols(c, m->scorer2_w, m->scorer2_b, d, 1, s1, KB, raw, tfd::kActNone))) return rc;
@@ -843,6 +895,7 @@ int laya_forward(tfd_ctx *c, const tfd_laya_model *m, const int64_t *ids, const 
   pa.raw = raw;
   pa.marker_mask = d_mm;
   pa.h = h;
+  pa.h0_col = d_h0;
   pa.logits = log_d;
   pa.pooled = pooled;
   pa.k = (int)K;

@@ -51,6 +51,8 @@ struct LayaArgs {
   const uint8_t *any;    // kMaskBits: byte (b*ceil(L/64) + q/64)*laya_map_row(nkt) + kt, tile
                          // kt kept by any query of that 64-query group
   const uint8_t *valid;  // kMaskStruct: (L, B)
+  const uint8_t *qneed;  // kMaskStruct, or null: (L, B), a 64-query group with no
+                         // non-zero entry is skipped (its output left unwritten)
   const float *cos_t;    // (L, half) or nullptr (no RoPE)
   const float *sin_t;
   float *out;            // (d, L, B)
@@ -128,12 +130,14 @@ struct NormArgs {
   float eps;
 };
 
-// Marker pooling: raw (K, B) logits, marker_mask (K, B) bytes, h (d, L, B)
-// head output; writes the masked logits (K, B) and pooled (d + 4, B).
+// Marker pooling: raw (K, B) logits, marker_mask (K, B) bytes, h the head
+// output with token 0 of prompt b in column h0_col[b] (or b*L when null);
+// writes the masked logits (K, B) and pooled (d + 4, B).
 struct PoolArgs {
   const float *raw;
   const uint8_t *marker_mask;
   const float *h;
+  const int *h0_col;
   float *logits, *pooled;
   int k, d, L;
 };
@@ -146,5 +150,9 @@ hipError_t launch_bias_act(float *y, const float *b, int m, size_t n, int act,
 hipError_t launch_geglu(const float *u, const float *b, int inter, size_t cols, float *g,
                         hipStream_t stream);
 hipError_t launch_pool(const PoolArgs &a, int batch, hipStream_t stream);
+// dst[:, dst_map ? dst_map[j] : j] = src[:, src_map ? src_map[j] : j], j < n,
+// m floats per column.
+hipError_t launch_copy_columns(const float *src, const int *src_map, float *dst,
+                               const int *dst_map, int m, long n, hipStream_t stream);
 
 }  // namespace tfd
