@@ -36,6 +36,9 @@ __device__ __forceinline__ float activate(float x, int act) {
 // model.rs:387-422: mean, then the mean of squared deviations, then
 // (x - mean) * (1 / sqrt(var + eps)) * w (+ b)), then plus column
 // add_col[c / per] of `add` when given (the type embedding, model.rs:916-931).
+// NR > 0: the column is held in registers (d <= 64 * NR, one read);
+// NR == 0: any d, three passes over the column.
+template <int NR>
 __global__ __launch_bounds__(256) void norm_columns_kernel(NormArgs a) {
   const int lane = threadIdx.x & 63;
   const long c = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -43,24 +46,49 @@ __global__ __launch_bounds__(256) void norm_columns_kernel(NormArgs a) {
   const long src = a.map ? (long)a.map[c] : c;
   const float *x = a.x + src * (long)a.ldx;
   const int d = a.d;
+  float r[NR > 0 ? NR : 1];
   float s = 0.0f;
-  for (int i = lane; i < d; i += 64) s += x[i];
+  if constexpr (NR > 0) {
+#pragma unroll
+    for (int k = 0; k < NR; ++k) {
+      const int i = lane + 64 * k;
+      r[k] = i < d ? x[i] : 0.0f;
+      s += r[k];
+    }
+  } else {
+    for (int i = lane; i < d; i += 64) s += x[i];
+  }
   const float mean = wave_sum(s) / (float)d;
   float v = 0.0f;
-  for (int i = lane; i < d; i += 64) {
-    const float t = x[i] - mean;
-    v += t * t;
+  if constexpr (NR > 0) {
+#pragma unroll
+    for (int k = 0; k < NR; ++k) {
+      const float t = r[k] - mean;
+      v += lane + 64 * k < d ? t * t : 0.0f;
+    }
+  } else {
+    for (int i = lane; i < d; i += 64) {
+      const float t = x[i] - mean;
+      v += t * t;
+    }
   }
   const float var = wave_sum(v) / (float)d;
   const float inv = 1.0f / sqrtf(var + a.eps);
   float *y = a.y + c * (long)d;
   const float *t = a.add ? a.add + (long)a.add_col[c / a.per] * d : nullptr;
-  for (int i = lane; i < d; i += 64) {
-    float value = (x[i] - mean) * inv;
+  auto put = [&](int i, float xi) {
+    float value = (xi - mean) * inv;
     value = value * a.w[i];
     if (a.b) value = value + a.b[i];
     if (t) value = value + t[i];
     y[i] = value;
+  };
+  if constexpr (NR > 0) {
+#pragma unroll
+    for (int k = 0; k < NR; ++k)
+      if (lane + 64 * k < d) put(lane + 64 * k, r[k]);
+  } else {
+    for (int i = lane; i < d; i += 64) put(i, x[i]);
   }
 }
 
@@ -168,8 +196,13 @@ unsigned grid_for(size_t total) {
 
 hipError_t launch_norm_columns(const NormArgs &a, hipStream_t stream) {
   if (a.cols <= 0) return hipSuccess;
-  hipLaunchKernelGGL(norm_columns_kernel, dim3((unsigned)((a.cols + 3) / 4)), dim3(256), 0, stream,
-                     a);
+  const dim3 grid((unsigned)((a.cols + 3) / 4));
+  if (a.d <= 256)
+    hipLaunchKernelGGL(norm_columns_kernel<4>, grid, dim3(256), 0, stream, a);
+  else if (a.d <= 1024)
+    hipLaunchKernelGGL(norm_columns_kernel<16>, grid, dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL(norm_columns_kernel<0>, grid, dim3(256), 0, stream, a);
   return hipGetLastError();
 }
 
