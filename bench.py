@@ -34,6 +34,15 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def host_threads():
+    """(threads the CPU baseline uses, CPUs this process may run on): every
+    CPU in the process's affinity mask, capped by OMP_NUM_THREADS where the
+    host sets it (the GPU boxes give each GPU a 16-CPU share that way)."""
+    allowed = len(os.sched_getaffinity(0))
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    return (min(allowed, int(cap)) if cap.isdigit() and int(cap) > 0 else allowed), allowed
+
+
 SETTLE_S = 0.08
 _settled = {"steps": 0}
 
@@ -123,6 +132,85 @@ def cpu_jeff_rows(w, rows, threads, reps=3):
                          w.theta, w.eps)
         times.append(time.perf_counter() - t)
     return statistics.median(times)
+
+
+# The reference's own CPU micro-benchmark of this op (8 rayon threads,
+# median of 15 after 5; fixtures/bench-laya-attention-gemm-2026-10-09/
+# micro.json, produced by that directory's microbenchmark.rs:142-210): d 1024,
+# 16 heads x 64, RoPE 160000, qkv[i] = ((17 i mod 101) - 50) * 0.002,
+# keep = (k mod 13 != 7) and, sliding, |q - k| <= window. Published
+# `gemm_ms` (the tile path the op takes) per (L, B, window).
+MICRO_PUBLISHED_MS = {
+    (64, 1, None): 0.116962, (64, 1, 64): 0.113356,
+    (128, 1, None): 0.322324, (128, 1, 64): 0.283323,
+    (256, 1, None): 0.997085, (256, 1, 64): 0.636693,
+    (512, 1, None): 3.742275, (512, 1, 64): 1.444846,
+    (8, 8, None): 0.066831, (8, 8, 64): 0.067832,
+}
+# The reference's GPU figure for the same op at L 512 (its NVRTC flash
+# kernel on an RTX 3060, f32, per call; docs/agents/specs/docs/
+# 23_TENFERRO_NATIVE.md:457).
+RTX3060_L512_US = 311.5
+
+
+def micro_inputs(L, B, window):
+    import numpy as np
+
+    d = 1024
+    i = np.arange(3 * d * L * B, dtype=np.int64)
+    qkv = (((i * 17) % 101).astype(np.float32) - np.float32(50.0)) * np.float32(0.002)
+    j = np.arange(L * L * B, dtype=np.int64)
+    q, k = j % L, (j // L) % L
+    keep = (k % 13) != 7
+    if window is not None:
+        keep &= np.abs(q - k) <= window
+    return qkv, keep.astype(np.uint8)
+
+
+def micro_lines(args, ctx, dev):
+    """The reference micro-benchmark's shapes (MICRO_PUBLISHED_MS): the GPU op
+    (Laya drop-in, device pointers, ms per call) and the CPU port at the
+    reference's 8 threads with its protocol (median of 15 after 5), beside
+    the published reference medians."""
+    import numpy as np
+    import torch
+
+    import oracle
+    import tenferro_ext as te
+
+    rows = []
+    for (L, B, window), pub in MICRO_PUBLISHED_MS.items():
+        qkv, keep = micro_inputs(L, B, window)
+        d, H = 1024, 16
+        flops = 4 * (d // H) * int(keep.astype(np.int64).sum()) * H
+        tq, tk = torch.from_numpy(qkv).to(dev), torch.from_numpy(keep).to(dev)
+        to = torch.empty(d * L * B, dtype=torch.float32, device=dev)
+        shape = (3 * d, L, B)
+        ms, kern = time_gpu(lambda: te.laya_attention_block(tq, tk, d, H, 160000.0, qkv_shape=shape,
+                                                            ctx=ctx, out=to),
+                            args.steps, args.warmup, ctx)
+        row = {"length": L, "batch": B, "window": window, "gpu_ms": round(ms, 5),
+               "gpu_kernel_ms": round(kern, 5), "gpu_tflops": round(flops / (ms * 1e-3) / 1e12, 3),
+               "reference_published_ms_8_threads": pub}
+        if not args.no_cpu:
+            oracle.set_threads(8)
+            times = []
+            for it in range(20):
+                t0 = time.perf_counter()
+                oracle.laya_attention_block(qkv, keep, d, H, L, B, 160000.0)
+                if it >= 5:
+                    times.append(time.perf_counter() - t0)
+            cpu_ms = statistics.median(times) * 1e3
+            row["cpu_port_ms_8_threads"] = round(cpu_ms, 4)
+            row["cpu_port_over_published"] = round(cpu_ms / pub, 2)
+        row["published_over_gpu"] = round(pub / ms, 1)
+        if (L, B, window) == (512, 1, None):
+            row["rtx3060_published_us"] = RTX3060_L512_US
+        rows.append(row)
+        del tq, tk, to
+    return {"rows": rows, "cpu": _cpu_model(),
+            "note": "cpu_port_over_published compares this host's CPU with the reference's "
+                    "benchmark machine (x86_64, 16 logical CPUs) as well as the two codes"}
 
 
 def run(args):
@@ -221,7 +309,7 @@ def run(args):
                                                                   ctx=ctx, out=o3),
                              args.steps, args.warmup, ctx)
         if not args.no_cpu:
-            t3 = cpu_laya(w3, min(16, os.cpu_count() or 1), reps=3, warmup=1)
+            t3 = cpu_laya(w3, host_threads()[0], reps=3, warmup=1)
         also["C3"] = {"ms_per_step": round(ms3, 5), "kernel_ms": round(k3ms, 5),
                       "tflops": round(f3 / (ms3 * 1e-3) / 1e12, 3),
                       "kernel_tflops": round(f3 / (k3ms * 1e-3) / 1e12, 3),
@@ -232,7 +320,7 @@ def run(args):
         if not args.no_cpu:
             also["C3"]["cpu_port_tflops"] = round(f3 / t3 / 1e12, 5)
             also["C3"]["cpu_port_sample"] = (f"full C3 workload, median of 3 after 1, "
-                                             f"{min(16, os.cpu_count() or 1)} threads, {t3 * 1e3:.1f} ms")
+                                             f"{host_threads()[0]} threads, {t3 * 1e3:.1f} ms")
         del q3, k3, v3, o3
 
         for cfg in (4, 5):
@@ -264,13 +352,13 @@ def run(args):
                                "tokens_per_s": round(wj.valid_tokens() / (msj * 1e-3), 1),
                                "algorithmic_flops": fj}
             if cfg == 4 and not args.no_cpu:
-                cores = min(16, os.cpu_count() or 1)
+                cores = host_threads()[0]
                 t = cpu_jeff_rows(wj, 2, cores)
                 also["C4"]["cpu_port_tokens_per_s"] = round(
                     float((wj.mask[: 2 * wj.length] != 0).sum()) / t, 1)
                 also["C4"]["cpu_port_sample"] = f"2 of 16 rows, median of 3, {cores} threads"
             if cfg == 5 and not args.no_cpu:
-                cores = min(16, os.cpu_count() or 1)
+                cores = host_threads()[0]
                 ws = jeff_config(5, rows=1, length=2048)
                 t = cpu_jeff_rows(ws, 1, cores, reps=1)
                 fs = 4 * ws.head_dim * ws.kept_pairs() * ws.heads
@@ -278,18 +366,21 @@ def run(args):
                 also["C5"]["cpu_port_sample"] = (f"1 row x L 2048 of the C5 generator (f32 path), "
                                                  f"{cores} threads, {t:.2f} s")
             del tq, tk, tv, tg, tqn, tkn, tm, oj
+        log("[bench] reference micro-benchmark shapes")
+        also["micro_reference_shapes"] = micro_lines(args, ctx, dev)
         also.update(layer_lines(args, ctx, dev))
         also["laya_model_forward"] = model_line(args, ctx, dev)
     result["also"] = also
 
     # ------------------------------------------------------------ CPU baseline
     if not args.no_cpu:
-        cores = min(16, os.cpu_count() or 1)
+        cores, allowed = host_threads()
         log(f"[bench] CPU baseline: oracle port of the rayon path, {cores} threads")
         t_all = cpu_laya(w, cores)
         t_8 = cpu_laya(w, 8) if cores != 8 else t_all
         result["cpu_baseline"] = {
             "value": round(flops / t_all / 1e12, 5), "unit": "TFLOP/s", "cores": cores,
+            "cpus_allowed": allowed,
             "kind": "port",
             "sample": "full C2 workload per call, median of 15 after 5 warmups",
             "ms": round(t_all * 1e3, 3),
@@ -370,7 +461,7 @@ def layer_lines(args, ctx, dev):
         if not args.no_cpu:
             import oracle
 
-            cores = min(16, os.cpu_count() or 1)
+            cores = host_threads()[0]
             oracle.set_threads(cores)
             times = []
             for _ in range(3):

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define TFD_ABI_VERSION 1
+#define TFD_ABI_VERSION 2
 
 /* status codes */
 #define TFD_OK 0
@@ -97,6 +97,9 @@ int tfd_ctx_take_kernel_time(tfd_ctx *ctx, double *total_ms, uint64_t *launches)
  * Reference: execute_laya_attention_block_in_session, laya_attention.rs:99-176,
  * arithmetic cpu-kernels lib.rs:843-1156.
  *   qkv_shape/qkv_rank: the qkv tensor's shape; must be (3*hidden, L, B).
+ *   qkv_len:            elements of qkv storage; must be 3*hidden*L*B, else
+ *                       "qkv length" (the reference's assert_eq!, cpu-kernels
+ *                       lib.rs:864, test lib.rs:1205-1210), before any access.
  *   keep_len:           must be L*L*B.
  *   out_len:            must be hidden*L*B.
  *   rope_base_bits:     f32 bits of the RoPE base; 0.0 disables RoPE.
@@ -104,7 +107,8 @@ int tfd_ctx_take_kernel_time(tfd_ctx *ctx, double *total_ms, uint64_t *launches)
  * A query that keeps no key yields NaN, as the reference does.
  */
 int tfd_laya_attention_block_f32(tfd_ctx *ctx, const float *qkv, const size_t *qkv_shape,
-                                 size_t qkv_rank, const uint8_t *keep, size_t keep_len,
+                                 size_t qkv_rank, size_t qkv_len, const uint8_t *keep,
+                                 size_t keep_len,
                                  size_t hidden, size_t heads, uint32_t rope_base_bits,
                                  float *out, size_t out_len, unsigned flags);
 

@@ -152,22 +152,66 @@ void oracle_rope_table(size_t length, size_t hd, float base, float *cos_out, flo
 
 /* The two products of the Laya tile path, in the row-major shapes the
  * reference passes to matrixmultiply::sgemm (lib.rs:1037-1052, 1081-1096).
- * Both are written as "C row += a * B row" so the inner loop runs over
- * independent output lanes and vectorizes without reassociating any sum;
- * every output is accumulated over k in order. */
+ * Every output is accumulated over k in order, acc = fma(a, b, acc) from 0,
+ * so the blocked kernel below and the plain loop give the same bits.
+ *
+ * The FMA path is a packed, register-tiled kernel in the manner of
+ * matrixmultiply 0.3.11 (the reference's sgemm): B is packed into panels
+ * of 16 columns (k x 16, contiguous), and a 6 x 16 block of C lives in
+ * twelve 8-wide registers for the whole k loop (two B loads and six A
+ * broadcasts per twelve FMAs). k is never split (at most the span length
+ * or the head dim), which keeps the summation order above. Edge rows and
+ * columns run the same in-order FMA chain one element at a time. */
 #if defined(__x86_64__)
+#include <immintrin.h>
+
 __attribute__((target("avx2,fma")))
-static void axpy_rows_fma(size_t m, size_t k, size_t n, const float *a, size_t lda,
-                          const float *b, size_t ldb, float *c, size_t ldc) {
-    for (size_t i = 0; i < m; ++i) {
-        float *ci = c + i * ldc;
-        for (size_t j = 0; j < n; ++j) ci[j] = 0.0f;
+static void gemm_block_6x16(size_t rows, size_t k, const float *a, size_t lda, const float *bp,
+                            float *c, size_t ldc) {
+    __m256 acc[6][2];
+    for (int r = 0; r < 6; ++r) acc[r][0] = acc[r][1] = _mm256_setzero_ps();
+    if (rows == 6) {
         for (size_t p = 0; p < k; ++p) {
-            float av = a[i * lda + p];
-            const float *bp = b + p * ldb;
-            for (size_t j = 0; j < n; ++j) ci[j] = fmaf(av, bp[j], ci[j]);
+            const __m256 b0 = _mm256_loadu_ps(bp + 16 * p), b1 = _mm256_loadu_ps(bp + 16 * p + 8);
+            for (int r = 0; r < 6; ++r) {
+                const __m256 av = _mm256_broadcast_ss(a + r * lda + p);
+                acc[r][0] = _mm256_fmadd_ps(av, b0, acc[r][0]);
+                acc[r][1] = _mm256_fmadd_ps(av, b1, acc[r][1]);
+            }
+        }
+    } else {
+        for (size_t p = 0; p < k; ++p) {
+            const __m256 b0 = _mm256_loadu_ps(bp + 16 * p), b1 = _mm256_loadu_ps(bp + 16 * p + 8);
+            for (size_t r = 0; r < rows; ++r) {
+                const __m256 av = _mm256_broadcast_ss(a + r * lda + p);
+                acc[r][0] = _mm256_fmadd_ps(av, b0, acc[r][0]);
+                acc[r][1] = _mm256_fmadd_ps(av, b1, acc[r][1]);
+            }
         }
     }
+    for (size_t r = 0; r < rows; ++r) {
+        _mm256_storeu_ps(c + r * ldc, acc[r][0]);
+        _mm256_storeu_ps(c + r * ldc + 8, acc[r][1]);
+    }
+}
+
+__attribute__((target("avx2,fma")))
+static void gemm_packed_fma(size_t m, size_t k, size_t n, const float *a, size_t lda,
+                            const float *b, size_t ldb, float *c, size_t ldc) {
+    const size_t full = n / 16 * 16;
+    float *bp = (float *)aligned_alloc(64, sizeof(float) * 16 * (k ? k : 1));
+    for (size_t j = 0; j < full; j += 16) {
+        for (size_t p = 0; p < k; ++p) memcpy(bp + 16 * p, b + p * ldb + j, sizeof(float) * 16);
+        for (size_t i = 0; i < m; i += 6)
+            gemm_block_6x16(m - i < 6 ? m - i : 6, k, a + i * lda, lda, bp, c + i * ldc + j, ldc);
+    }
+    free(bp);
+    for (size_t i = 0; i < m; ++i)
+        for (size_t j = full; j < n; ++j) {
+            float acc = 0.0f;
+            for (size_t p = 0; p < k; ++p) acc = fmaf(a[i * lda + p], b[p * ldb + j], acc);
+            c[i * ldc + j] = acc;
+        }
 }
 #endif
 
@@ -195,7 +239,7 @@ static void sgemm_rows(size_t m, size_t k, size_t n, const float *a, size_t lda,
         g_have_fma = __builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma");
     }
     if (g_have_fma) {
-        axpy_rows_fma(m, k, n, a, lda, b, ldb, c, ldc);
+        gemm_packed_fma(m, k, n, a, lda, b, ldb, c, ldc);
         return;
     }
 #endif

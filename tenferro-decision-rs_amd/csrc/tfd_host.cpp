@@ -1023,7 +1023,8 @@ int tfd_ctx_take_kernel_time(tfd_ctx *c, double *total_ms, uint64_t *launches) {
 }
 
 int tfd_laya_attention_block_f32(tfd_ctx *c, const float *qkv, const size_t *qkv_shape,
-                                 size_t qkv_rank, const uint8_t *keep, size_t keep_len,
+                                 size_t qkv_rank, size_t qkv_len, const uint8_t *keep,
+                                 size_t keep_len,
                                  size_t hidden, size_t heads, uint32_t rope_base_bits,
                                  float *out, size_t out_len, unsigned flags) {
   if (!c) return TFD_EINVAL;
@@ -1036,6 +1037,11 @@ int tfd_laya_attention_block_f32(tfd_ctx *c, const float *qkv, const size_t *qkv
     return invalid(c, kLayaOp, "shape", "attention block expects (3d, L, B)");
   const size_t length = qkv_shape[1], batch = qkv_shape[2];
   size_t expect = 0;
+  // cpu-kernels lib.rs:855-864: a slice shorter (or longer) than the shape
+  // says is rejected before any access ("qkv length").
+  if (!mul_ok(qkv_shape[0], length, &expect) || !mul_ok(expect, batch, &expect) ||
+      qkv_len != expect)
+    return invalid(c, kLayaOp, "qkv", "qkv length");
   // laya_attention.rs:138-140
   if (!mul_ok(length, length, &expect) || !mul_ok(expect, batch, &expect) || keep_len != expect)
     return invalid(c, kLayaOp, "keep", "keep must be (L, L, B)");

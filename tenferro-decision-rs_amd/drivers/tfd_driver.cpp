@@ -116,7 +116,7 @@ int check(tfd_ctx *ctx) {
     for (size_t k = 0; k < L; ++k)
       for (size_t q = 0; q < L; ++q) keep[q + L * (k + L * b)] = (b == 0 || k < 20) ? 1 : 0;
   auto laya = [&](unsigned flags, std::vector<const void *> &in, float *out) {
-    return tfd_laya_attention_block_f32(ctx, (const float *)in[0], shape, 3,
+    return tfd_laya_attention_block_f32(ctx, (const float *)in[0], shape, 3, qkv.size(),
                                         (const uint8_t *)in[1], keep.size(), d, H,
                                         bits(160000.0f), out, d * L * B, flags);
   };
@@ -180,11 +180,17 @@ int check(tfd_ctx *ctx) {
 
   // ---------------------------------------------------------------- errors
   const size_t bad_shape[3] = {3 * d + 1, L, B};
-  const int rc = tfd_laya_attention_block_f32(ctx, qkv.data(), bad_shape, 3, keep.data(),
-                                              keep.size(), d, H, bits(160000.0f), ho.data(),
-                                              d * L * B, TFD_HOST_PTRS);
+  const int rc = tfd_laya_attention_block_f32(ctx, qkv.data(), bad_shape, 3, qkv.size(),
+                                              keep.data(), keep.size(), d, H, bits(160000.0f),
+                                              ho.data(), d * L * B, TFD_HOST_PTRS);
   expect(rc == TFD_EINVAL && std::strstr(tfd_last_error(ctx), "attention block expects") != nullptr,
          "laya: a (3d+1, L, B) input is rejected with the reference's message");
+  // cpu-kernels lib.rs:1205-1210: short storage is rejected before any access.
+  const int rs = tfd_laya_attention_block_f32(ctx, qkv.data(), shape, 3, qkv.size() - 1,
+                                              keep.data(), keep.size(), d, H, bits(160000.0f),
+                                              ho.data(), d * L * B, TFD_HOST_PTRS);
+  expect(rs == TFD_EINVAL && std::strstr(tfd_last_error(ctx), "qkv length") != nullptr,
+         "laya: qkv storage one element short is rejected (\"qkv length\")");
   std::printf("%d failure(s)\n", failures);
   return failures == 0 ? 0 : 1;
 }
@@ -215,7 +221,7 @@ int bench(tfd_ctx *ctx) {
   hip_ok(hipMemcpy(dq, qkv.data(), qkv.size() * 4, hipMemcpyHostToDevice));
   hip_ok(hipMemcpy(dk, keep.data(), keep.size(), hipMemcpyHostToDevice));
   auto call = [&] {
-    return tfd_laya_attention_block_f32(ctx, dq, shape, 3, dk, keep.size(), d, H,
+    return tfd_laya_attention_block_f32(ctx, dq, shape, 3, qkv.size(), dk, keep.size(), d, H,
                                         bits(160000.0f), dout, d * L * B,
                                         TFD_DEVICE_PTRS | TFD_ASYNC);
   };
@@ -265,8 +271,8 @@ int main(int argc, char **argv) {
     // run (there is no CPU fallback).
     const size_t bad_shape[3] = {193, 32, 2};
     float x[4] = {0, 0, 0, 0};
-    const int v = tfd_laya_attention_block_f32(ctx, x, bad_shape, 3, nullptr, 0, 64, 4, 0, x, 4,
-                                               TFD_HOST_PTRS);
+    const int v = tfd_laya_attention_block_f32(ctx, x, bad_shape, 3, 4, nullptr, 0, 64, 4, 0, x,
+                                               4, TFD_HOST_PTRS);
     std::printf("no GPU: validation %s (%s); compute checks need a GPU\n",
                 v == TFD_EINVAL ? "works" : "FAILED", tfd_last_error(ctx));
     tfd_ctx_destroy(ctx);

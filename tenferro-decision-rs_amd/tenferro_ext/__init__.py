@@ -133,7 +133,7 @@ def load_library(path: Optional[str] = None) -> ctypes.CDLL:
         "tfd_ctx_set_timing": (I, [P, I]),
         "tfd_ctx_take_kernel_time": (I, [P, ctypes.POINTER(ctypes.c_double),
                                          ctypes.POINTER(ctypes.c_uint64)]),
-        "tfd_laya_attention_block_f32": (I, [P, P, SP, S, P, S, S, S, U32, P, S, F]),
+        "tfd_laya_attention_block_f32": (I, [P, P, SP, S, S, P, S, S, S, U32, P, S, F]),
         "tfd_laya_attention_structured_f32": (I, [P, P, S, S, S, S, P, ctypes.c_int64, U32, P, F]),
         "tfd_jeff_full_attention_f32": (
             I, [P, P, SP, S, P, S, P, S, P, S, P, S, P, S, P, S, S, S, S, U32, U32, P, S, F]),
@@ -240,15 +240,36 @@ def _is_torch(x) -> bool:
     return type(x).__module__.startswith("torch")
 
 
-class _Arg:
-    """A flat buffer argument: host numpy array or torch CUDA tensor."""
+# torch dtypes accepted for each host dtype: f32 operands, keep/valid bytes,
+# bf16 bits (any 16-bit type, read as raw bits).
+_TORCH_DTYPES = {
+    np.dtype(np.float32): ("float32",),
+    np.dtype(np.uint8): ("uint8", "bool"),
+    np.dtype(np.uint16): ("uint16", "int16", "bfloat16"),
+}
 
-    def __init__(self, x, dtype, name):
+
+class _Arg:
+    """A flat buffer argument: host numpy array or torch tensor (CUDA: device
+    pointer; CPU: host pointer).
+
+    ``count`` is the element count the call's shape implies; entries whose C
+    ABI carries no lengths pass it, so a short buffer is rejected here before
+    any device access. A torch tensor must already have the element type the
+    entry reads (no silent reinterpretation of a half-width type)."""
+
+    def __init__(self, x, dtype, name, count: Optional[int] = None):
         self.obj = x
+        self.name = name
         if x is None:
             self.ptr, self.n, self.device = None, 0, None
             return
         if _is_torch(x):
+            allowed = _TORCH_DTYPES[np.dtype(dtype)]
+            got = str(x.dtype).replace("torch.", "")
+            if got not in allowed:
+                raise InvalidArgument(
+                    TFD_EINVAL, f"{name}: tensor dtype {got}, expected {' or '.join(allowed)}")
             if not x.is_contiguous():
                 raise InvalidArgument(TFD_EINVAL, f"{name}: tensor must be contiguous")
             self.ptr = x.data_ptr()
@@ -260,6 +281,9 @@ class _Arg:
             self.ptr = arr.ctypes.data
             self.n = arr.size
             self.device = False
+        if count is not None and self.n != count:
+            raise InvalidArgument(
+                TFD_EINVAL, f"{name}: {self.n} elements, the shape needs {count}")
 
 
 _async = False
@@ -278,13 +302,56 @@ class asynchronous:
         _async = self._prev
 
 
-def _flags(args: Sequence[_Arg]) -> int:
+def _flags(args: Sequence[_Arg], ctx: Optional["Context"] = None) -> int:
     kinds = {a.device for a in args if a.obj is not None}
     if len(kinds) > 1:
         raise InvalidArgument(TFD_EINVAL, "mix of host arrays and device tensors")
     if kinds == {True}:
+        if ctx is not None:
+            for a in args:
+                if a.obj is not None and a.obj.device.index not in (None, ctx.device):
+                    raise InvalidArgument(
+                        TFD_EINVAL, f"{a.name}: tensor on cuda:{a.obj.device.index}, "
+                        f"the context runs on device {ctx.device}")
         return TFD_DEVICE_PTRS | (TFD_ASYNC if _async else 0)
     return TFD_HOST_PTRS
+
+
+class _StreamOrder:
+    """Orders a device-pointer call against torch's current stream.
+
+    The library runs on the context's own stream. Before the call, that
+    stream waits for the work torch has queued so far (the kernels that
+    produce the inputs); after an asynchronous call, torch's current stream
+    waits for the context stream (so later torch work sees the outputs and
+    the caching allocator does not reuse them early). A synchronous call
+    returns after its stream has drained, so nothing more is needed then."""
+
+    def __init__(self, ctx: "Context", flags: int):
+        self.stream = None
+        if not flags & TFD_DEVICE_PTRS:
+            return
+        import torch
+
+        cur = torch.cuda.current_stream(ctx.device)
+        handle = ctx.stream()
+        if not handle or handle == cur.cuda_stream:
+            return
+        self.torch_stream = cur
+        self.stream = torch.cuda.ExternalStream(handle, device=ctx.device)
+        self.stream.wait_stream(cur)
+        self.flags = flags
+
+    def done(self) -> None:
+        if self.stream is not None and self.flags & TFD_ASYNC:
+            self.torch_stream.wait_stream(self.stream)
+
+
+def _call(ctx: "Context", flags: int, fn, *args) -> None:
+    """Runs one C ABI call with stream ordering and error mapping."""
+    order = _StreamOrder(ctx, flags)
+    ctx.check(fn(*args))
+    order.done()
 
 
 def _shape_arr(shape):
@@ -339,16 +406,18 @@ class LayaAttentionBlockOp:
         ctx = ctx or default_context()
         a_qkv = _Arg(qkv, np.float32, "qkv")
         a_keep = _Arg(keep, np.uint8, "keep")
-        flags = _flags([a_qkv, a_keep])
         n = self.hidden * (qkv_shape[1] if len(qkv_shape) == 3 else 0) * (
             qkv_shape[2] if len(qkv_shape) == 3 else 0)
         if out is None:
             out = _new_out(a_qkv, n)
         a_out = _Arg(out, np.float32, "out")
+        flags = _flags([a_qkv, a_keep, a_out], ctx)
         shape = _shape_arr(qkv_shape)
-        ctx.check(ctx._lib.tfd_laya_attention_block_f32(
-            ctx.handle, a_qkv.ptr, shape, len(qkv_shape), a_keep.ptr, a_keep.n,
-            self.hidden, self.heads, self.rope_base_bits, a_out.ptr, a_out.n, flags))
+        # The storage lengths go to the library, which rejects a short qkv
+        # ("qkv length"), keep or out with the reference's messages.
+        _call(ctx, flags, ctx._lib.tfd_laya_attention_block_f32,
+              ctx.handle, a_qkv.ptr, shape, len(qkv_shape), a_qkv.n, a_keep.ptr, a_keep.n,
+              self.hidden, self.heads, self.rope_base_bits, a_out.ptr, a_out.n, flags)
         return a_out.obj
 
 
@@ -392,22 +461,23 @@ class JeffFullAttentionOp:
                 ctx: Optional[Context] = None, out=None):
         """execute_jeff_full_attention_in_session (jeff_attention.rs:103-184)."""
         ctx = ctx or default_context()
-        args = [_Arg(x, np.float32, nm) for x, nm in
-                ((q, "q"), (k, "k"), (v, "v"), (gate, "gate"),
-                 (q_norm, "q_norm"), (k_norm, "k_norm"), (mask, "mask"))]
-        flags = _flags(args)
         n = 1
         for s in q_shape:
             n *= s
+        # q's storage length is not an ABI argument (its shape is): checked here.
+        args = [_Arg(x, np.float32, nm, c) for x, nm, c in
+                ((q, "q", n), (k, "k", None), (v, "v", None), (gate, "gate", None),
+                 (q_norm, "q_norm", None), (k_norm, "k_norm", None), (mask, "mask", None))]
         if out is None:
             out = _new_out(args[0], n)
         a_out = _Arg(out, np.float32, "out")
+        flags = _flags(args + [a_out], ctx)
         shape = _shape_arr(q_shape)
         aq, ak, av, ag, aqn, akn, am = args
-        ctx.check(ctx._lib.tfd_jeff_full_attention_f32(
-            ctx.handle, aq.ptr, shape, len(q_shape), ak.ptr, ak.n, av.ptr, av.n, ag.ptr, ag.n,
-            aqn.ptr, aqn.n, akn.ptr, akn.n, am.ptr, am.n, self.heads, self.head_dim,
-            self.rotary_dim, self.theta_bits, self.eps_bits, a_out.ptr, a_out.n, flags))
+        _call(ctx, flags, ctx._lib.tfd_jeff_full_attention_f32,
+              ctx.handle, aq.ptr, shape, len(q_shape), ak.ptr, ak.n, av.ptr, av.n, ag.ptr, ag.n,
+              aqn.ptr, aqn.n, akn.ptr, akn.n, am.ptr, am.n, self.heads, self.head_dim,
+              self.rotary_dim, self.theta_bits, self.eps_bits, a_out.ptr, a_out.n, flags)
         return a_out.obj
 
 
@@ -437,15 +507,16 @@ def laya_attention_structured(qkv, valid, hidden: int, heads: int, length: int, 
                               ctx: Optional[Context] = None, out=None):
     """Laya with ``valid (L, B)`` + ``window`` (-1 = global) instead of keep."""
     ctx = ctx or default_context()
-    a_qkv = _Arg(qkv, np.float32, "qkv")
-    a_valid = _Arg(valid, np.uint8, "valid")
-    flags = _flags([a_qkv, a_valid])
+    n = hidden * length * batch
+    a_qkv = _Arg(qkv, np.float32, "qkv", 3 * n)
+    a_valid = _Arg(valid, np.uint8, "valid", length * batch)
     if out is None:
-        out = _new_out(a_qkv, hidden * length * batch)
-    a_out = _Arg(out, np.float32, "out")
-    ctx.check(ctx._lib.tfd_laya_attention_structured_f32(
-        ctx.handle, a_qkv.ptr, hidden, heads, length, batch, a_valid.ptr, int(window),
-        f32_bits(rope_base), a_out.ptr, flags))
+        out = _new_out(a_qkv, n)
+    a_out = _Arg(out, np.float32, "out", n)
+    flags = _flags([a_qkv, a_valid, a_out], ctx)
+    _call(ctx, flags, ctx._lib.tfd_laya_attention_structured_f32,
+          ctx.handle, a_qkv.ptr, hidden, heads, length, batch, a_valid.ptr, int(window),
+          f32_bits(rope_base), a_out.ptr, flags)
     return a_out.obj
 
 
@@ -471,19 +542,23 @@ def jeff_full_attention_rows(q, k, v, gate, q_norm, k_norm, mask, rows: int, len
     as uint16 bf16 bits."""
     ctx = ctx or default_context()
     dt = np.uint16 if bf16 else np.float32
-    aq, ak, av, ag = (_Arg(x, dt, nm) for x, nm in ((q, "q"), (k, "k"), (v, "v"), (gate, "gate")))
-    aqn, akn, am = (_Arg(x, np.float32, nm) for x, nm in
-                    ((q_norm, "q_norm"), (k_norm, "k_norm"), (mask, "mask")))
-    flags = _flags([aq, ak, av, ag, aqn, akn, am])
+    nq = rows * length * heads * head_dim
+    nkv = rows * length * kv_heads * head_dim
+    aq, ak, av, ag = (_Arg(x, dt, nm, c) for x, nm, c in
+                      ((q, "q", nq), (k, "k", nkv), (v, "v", nkv), (gate, "gate", nq)))
+    aqn, akn, am = (_Arg(x, np.float32, nm, c) for x, nm, c in
+                    ((q_norm, "q_norm", head_dim), (k_norm, "k_norm", head_dim),
+                     (mask, "mask", rows * length)))
+    if out is None:
+        out = _new_out(aq, nq)
+    a_out = _Arg(out, np.float32, "out", nq)
+    flags = _flags([aq, ak, av, ag, aqn, akn, am, a_out], ctx)
     if trim_leading:
         flags |= TFD_TRIM_LEADING
-    if out is None:
-        out = _new_out(aq, rows * length * heads * head_dim)
-    a_out = _Arg(out, np.float32, "out")
     fn = ctx._lib.tfd_jeff_full_attention_rows_bf16 if bf16 else ctx._lib.tfd_jeff_full_attention_rows_f32
-    ctx.check(fn(ctx.handle, rows, length, heads, kv_heads, head_dim, rotary_dim,
-                 aq.ptr, ak.ptr, av.ptr, ag.ptr, aqn.ptr, akn.ptr, am.ptr,
-                 f32_bits(theta), f32_bits(eps), a_out.ptr, flags))
+    _call(ctx, flags, fn, ctx.handle, rows, length, heads, kv_heads, head_dim, rotary_dim,
+          aq.ptr, ak.ptr, av.ptr, ag.ptr, aqn.ptr, akn.ptr, am.ptr,
+          f32_bits(theta), f32_bits(eps), a_out.ptr, flags)
     return a_out.obj
 
 
@@ -508,16 +583,19 @@ def laya_attention_layer(x, keep, w_in, b_in, w_out, b_out, hidden: int, heads: 
     (+ b_out). x and out are (hidden, L, B) flat, W_in (hidden, 3*hidden) and
     W_out (hidden, hidden) column-major; biases may be None."""
     ctx = ctx or default_context()
-    ax, ak = _Arg(x, np.float32, "x"), _Arg(keep, np.uint8, "keep")
-    awi, awo = _Arg(w_in, np.float32, "w_in"), _Arg(w_out, np.float32, "w_out")
-    abi, abo = _Arg(b_in, np.float32, "b_in"), _Arg(b_out, np.float32, "b_out")
-    flags = _flags([ax, ak, awi, awo, abi, abo])
+    n = hidden * length * batch
+    ax, ak = _Arg(x, np.float32, "x", n), _Arg(keep, np.uint8, "keep", length * length * batch)
+    awi = _Arg(w_in, np.float32, "w_in", hidden * 3 * hidden)
+    awo = _Arg(w_out, np.float32, "w_out", hidden * hidden)
+    abi = _Arg(b_in, np.float32, "b_in", 3 * hidden if b_in is not None else None)
+    abo = _Arg(b_out, np.float32, "b_out", hidden if b_out is not None else None)
     if out is None:
-        out = _new_out(ax, hidden * length * batch)
-    a_out = _Arg(out, np.float32, "out")
-    ctx.check(ctx._lib.tfd_laya_attention_layer_f32(
-        ctx.handle, ax.ptr, hidden, heads, length, batch, ak.ptr, awi.ptr, abi.ptr, awo.ptr,
-        abo.ptr, f32_bits(rope_base), a_out.ptr, flags))
+        out = _new_out(ax, n)
+    a_out = _Arg(out, np.float32, "out", n)
+    flags = _flags([ax, ak, awi, awo, abi, abo, a_out], ctx)
+    _call(ctx, flags, ctx._lib.tfd_laya_attention_layer_f32,
+          ctx.handle, ax.ptr, hidden, heads, length, batch, ak.ptr, awi.ptr, abi.ptr, awo.ptr,
+          abo.ptr, f32_bits(rope_base), a_out.ptr, flags)
     return a_out.obj
 
 
@@ -530,16 +608,19 @@ def jeff_full_attention_layer_rows(x, w_q, w_gate, w_k, w_v, w_o, q_norm, k_norm
     path): q/gate/k/v = x W, the fused rows op with native GQA, out = merged
     W_o. x and out are rows x (L, hidden) flat; weights (in, out) column-major."""
     ctx = ctx or default_context()
-    args = [_Arg(a, np.float32, nm) for a, nm in
-            ((x, "x"), (w_q, "w_q"), (w_gate, "w_gate"), (w_k, "w_k"), (w_v, "w_v"),
-             (w_o, "w_o"), (q_norm, "q_norm"), (k_norm, "k_norm"), (mask, "mask"))]
-    flags = _flags(args)
+    W, KW, n = heads * head_dim, kv_heads * head_dim, rows * length * hidden
+    args = [_Arg(a, np.float32, nm, c) for a, nm, c in
+            ((x, "x", n), (w_q, "w_q", hidden * W), (w_gate, "w_gate", hidden * W),
+             (w_k, "w_k", hidden * KW), (w_v, "w_v", hidden * KW), (w_o, "w_o", W * hidden),
+             (q_norm, "q_norm", head_dim), (k_norm, "k_norm", head_dim),
+             (mask, "mask", rows * length))]
+    if out is None:
+        out = _new_out(args[0], n)
+    a_out = _Arg(out, np.float32, "out", n)
+    flags = _flags(args + [a_out], ctx)
     if trim_leading:
         flags |= TFD_TRIM_LEADING
-    if out is None:
-        out = _new_out(args[0], rows * length * hidden)
-    a_out = _Arg(out, np.float32, "out")
-    ctx.check(ctx._lib.tfd_jeff_full_attention_layer_rows_f32(
-        ctx.handle, rows, length, hidden, heads, kv_heads, head_dim, rotary_dim,
-        *[a.ptr for a in args], f32_bits(theta), f32_bits(eps), a_out.ptr, flags))
+    _call(ctx, flags, ctx._lib.tfd_jeff_full_attention_layer_rows_f32,
+          ctx.handle, rows, length, hidden, heads, kv_heads, head_dim, rotary_dim,
+          *[a.ptr for a in args], f32_bits(theta), f32_bits(eps), a_out.ptr, flags)
     return a_out.obj

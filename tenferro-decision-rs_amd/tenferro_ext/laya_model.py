@@ -22,7 +22,8 @@ from typing import Dict, List, Optional
 
 import numpy as np
 
-from . import TFD_EINVAL, Context, InvalidArgument, _Arg, default_context, f32_bits
+from . import (TFD_EINVAL, Context, InvalidArgument, _Arg, _call, _flags,
+               default_context, f32_bits)
 
 ACTION_HIDDEN = 256  # checkpoint.rs:33
 
@@ -305,6 +306,9 @@ class LayaModel:
         dev = torch.device("cuda", device)
         self._dev = {k: (torch.from_numpy(v).to(dev) if v is not None else None)
                      for k, v in ckpt.weights.items()}
+        # The uploads run on torch's stream; the forward reads the weights on
+        # the context's stream, so they must have landed first.
+        torch.cuda.synchronize(dev)
         ptr = lambda k: self._dev[k].data_ptr() if self._dev.get(k) is not None else None
         enc, agent = ckpt.encoder, ckpt.agent
         d = enc.hidden_size
@@ -364,17 +368,20 @@ class LayaModel:
         L = len(ids) // B if B else 0
         K = len(marker_pos) // B if B else 0
         A = self.ckpt.agent.action_count()
-        flags = 0
-        if logits is None:
+        if logits is None and action is None:
             logits = np.zeros(K * B, np.float32)
             action = np.zeros(A * B, np.float32)
-        else:
-            from . import TFD_DEVICE_PTRS
-            flags = TFD_DEVICE_PTRS
-        a_log, a_act = _Arg(logits, np.float32, "logits"), _Arg(action, np.float32, "action")
+        elif logits is None or action is None:
+            raise _invalid("laya.logits", "pass both outputs (logits and action) or neither")
+        # Outputs decide the pointer kind (token inputs are always host arrays):
+        # both host arrays, or both CUDA tensors on the model's device; checked
+        # before any device call.
+        a_log = _Arg(logits, np.float32, "logits", K * B)
+        a_act = _Arg(action, np.float32, "action", A * B)
+        flags = _flags([a_log, a_act], self.ctx)
         c = self.ctx
-        c.check(c._lib.tfd_laya_forward_f32(
-            c.handle, ctypes.byref(self._model), ids.ctypes.data, mask.ctypes.data, L, B,
-            marker_pos.ctypes.data, marker_mask.ctypes.data, K, qtype.ctypes.data, a_log.ptr,
-            a_act.ptr, flags))
+        _call(c, flags, c._lib.tfd_laya_forward_f32,
+              c.handle, ctypes.byref(self._model), ids.ctypes.data, mask.ctypes.data, L, B,
+              marker_pos.ctypes.data, marker_mask.ctypes.data, K, qtype.ctypes.data, a_log.ptr,
+              a_act.ptr, flags)
         return a_log.obj, a_act.obj

@@ -45,7 +45,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_family_ids(lib):
-    assert lib.tfd_abi_version() == 1
+    assert lib.tfd_abi_version() == 2
     # laya_attention.rs:25 and jeff_attention.rs:24
     assert lib.tfd_laya_attention_block_family_id().decode() == "tenferro-decision.laya_attention_block.v1"
     assert lib.tfd_jeff_full_attention_family_id().decode() == "tenferro-decision.jeff_full_attention.v1"
@@ -56,14 +56,16 @@ def test_context_does_not_touch_gpu_on_create(ctx):
     ctx.synchronize()  # nothing enqueued yet: a no-op
 
 
-def _laya_call(ctx, shape, keep_len, hidden=8, heads=2, out_len=None):
+def _laya_call(ctx, shape, keep_len, hidden=8, heads=2, out_len=None, qkv_len=None):
     qkv = np.zeros(max(1, int(np.prod(shape))), np.float32)
+    qkv_len = int(np.prod(shape)) if qkv_len is None else qkv_len
     keep = np.ones(max(1, keep_len), np.uint8)
     out = np.zeros(max(1, out_len if out_len is not None else hidden * (shape[1] if len(shape) == 3 else 1)
                        * (shape[2] if len(shape) == 3 else 1)), np.float32)
     arr = (ctypes.c_size_t * len(shape))(*shape)
     rc = ctx._lib.tfd_laya_attention_block_f32(
-        ctx.handle, qkv.ctypes.data, arr, len(shape), keep.ctypes.data, keep_len, hidden, heads,
+        ctx.handle, qkv.ctypes.data, arr, len(shape), qkv_len, keep.ctypes.data, keep_len, hidden,
+        heads,
         te.f32_bits(160000.0), out.ctypes.data,
         out_len if out_len is not None else out.size, 0)
     return rc, ctx._lib.tfd_last_error(ctx.handle).decode()
@@ -75,6 +77,22 @@ def test_laya_rejects_bad_rank_and_width(ctx):
     assert rc == te.TFD_EINVAL and "attention block expects (3d, L, B)" in msg
     rc, msg = _laya_call(ctx, (23, 4, 1), 16)
     assert rc == te.TFD_EINVAL and "attention block expects (3d, L, B)" in msg
+
+
+def test_laya_rejects_short_qkv_storage(ctx):
+    """cpu-kernels lib.rs:1205-1210: storage shorter than the shape is rejected
+    ("qkv length") before any access -- here with an empty slice, as there,
+    and one element short; no device is touched (the no-GPU error would
+    otherwise come back)."""
+    rc, msg = _laya_call(ctx, (24, 32, 1), 32 * 32, hidden=8, heads=1, qkv_len=0)
+    assert rc == te.TFD_EINVAL and "qkv length" in msg
+    rc, msg = _laya_call(ctx, (24, 4, 1), 16, qkv_len=24 * 4 - 1)
+    assert rc == te.TFD_EINVAL and "qkv length" in msg
+    rc, msg = _laya_call(ctx, (24, 4, 1), 16, qkv_len=24 * 4 + 1)
+    assert rc == te.TFD_EINVAL and "qkv length" in msg
+    op = te.LayaAttentionBlockOp(8, 2, te.f32_bits(0.0))
+    with pytest.raises(te.InvalidArgument, match="qkv length"):
+        op.execute(np.zeros(24 * 4 - 1, np.float32), (24, 4, 1), np.ones(16, np.uint8), ctx=ctx)
 
 
 def test_laya_rejects_bad_keep_length(ctx):
@@ -180,3 +198,82 @@ def test_bf16_round_to_nearest_even():
     assert list(te.bf16_bits_to_f32(b)[:4]) == [1.0, 1.0, 1.015625, -2.5]
     y = np.random.default_rng(0).standard_normal(1000).astype(np.float32)
     assert np.abs(te.bf16_bits_to_f32(te.to_bf16_bits(y)) - y).max() <= np.abs(y).max() * 2 ** -8
+
+
+# ------------------------------------------------ host-side argument checks
+#
+# Entries whose C ABI carries no storage lengths (structured, rows, layers,
+# the model forward) and torch tensors of the wrong element type are
+# rejected by the Python mirror before any device call. torch CPU tensors
+# stand in for device tensors here: the checks run before the pointer kind
+# matters, and nothing reaches the library.
+
+def test_wrapper_rejects_short_buffers(ctx):
+    with pytest.raises(te.InvalidArgument, match="qkv: 95 elements"):
+        te.laya_attention_structured(np.zeros(95, np.float32), np.ones(4, np.uint8), 8, 2, 4, 1,
+                                     -1, 0.0, ctx=ctx)
+    with pytest.raises(te.InvalidArgument, match="valid: 3 elements"):
+        te.laya_attention_structured(np.zeros(96, np.float32), np.ones(3, np.uint8), 8, 2, 4, 1,
+                                     -1, 0.0, ctx=ctx)
+    R, L, H, KV, hd = 2, 4, 4, 2, 8
+    f = lambda n: np.zeros(n, np.float32)
+    nq, nkv = R * L * H * hd, R * L * KV * hd
+    good = dict(q=f(nq), k=f(nkv), v=f(nkv), gate=f(nq), q_norm=f(hd), k_norm=f(hd), mask=f(R * L))
+    for name, short in (("q", nq - 1), ("k", nkv - 1), ("v", nkv + 1), ("gate", nq - 4),
+                        ("q_norm", hd - 1), ("mask", R * L - 1)):
+        bad = dict(good, **{name: f(short)})
+        with pytest.raises(te.InvalidArgument, match=f"{name}: {short} elements"):
+            te.jeff_full_attention_rows(*bad.values(), R, L, H, KV, hd, hd, 1e7, 1e-6, ctx=ctx)
+    with pytest.raises(te.InvalidArgument, match="q: 63 elements"):
+        te.jeff_full_attention(f(63), f(64), f(64), f(64), f(8), f(8), f(8), 1, 8, 8, 1e7, 1e-6,
+                               q_shape=(8, 8), ctx=ctx)
+
+
+def test_wrapper_rejects_wrong_tensor_dtypes(ctx):
+    import torch
+
+    R, L, H, KV, hd = 1, 4, 2, 1, 8
+    t = lambda n, dt=torch.float32: torch.zeros(n, dtype=dt)
+    nq, nkv = R * L * H * hd, R * L * KV * hd
+    # a bf16 tensor handed to an f32 entry: half the bytes the kernel reads
+    with pytest.raises(te.InvalidArgument, match="q: tensor dtype bfloat16, expected float32"):
+        te.jeff_full_attention_rows(t(nq, torch.bfloat16), t(nkv), t(nkv), t(nq), t(hd), t(hd),
+                                    t(R * L), R, L, H, KV, hd, hd, 1e7, 1e-6, ctx=ctx)
+    # the drop-in's k_len compares element counts, so a half-width k passes that check
+    with pytest.raises(te.InvalidArgument, match="k: tensor dtype float16"):
+        te.jeff_full_attention(t(64), t(64, torch.float16), t(64), t(64), t(8), t(8), t(8), 1, 8,
+                               8, 1e7, 1e-6, q_shape=(8, 8), ctx=ctx)
+    with pytest.raises(te.InvalidArgument, match="keep: tensor dtype int32"):
+        te.laya_attention_block(t(96), t(16, torch.int32), 8, 2, 0.0, qkv_shape=(24, 4, 1),
+                                ctx=ctx)
+    # bf16 entry: 16-bit types only
+    with pytest.raises(te.InvalidArgument, match="gate: tensor dtype float32"):
+        te.jeff_full_attention_rows(t(nq, torch.bfloat16), t(nkv, torch.bfloat16),
+                                    t(nkv, torch.bfloat16), t(nq), t(hd), t(hd), t(R * L), R, L,
+                                    H, KV, hd, hd, 1e7, 1e-6, bf16=True, ctx=ctx)
+
+
+def test_wrapper_rejects_host_device_mix(ctx):
+    """Host arrays and device tensors in one call are refused before any device
+    call (a stand-in object reports itself as a CUDA tensor)."""
+
+    class FakeCuda:
+        __module__ = "torch.fake"
+
+        def __init__(self, n):
+            self.dtype = "torch.float32"
+            self._n = n
+            self.is_cuda = True
+
+        def is_contiguous(self):
+            return True
+
+        def data_ptr(self):
+            return 1 << 40
+
+        def numel(self):
+            return self._n
+
+    with pytest.raises(te.InvalidArgument, match="mix of host arrays and device tensors"):
+        te.laya_attention_structured(FakeCuda(96), np.ones(4, np.uint8), 8, 2, 4, 1, -1, 0.0,
+                                     ctx=ctx, out=np.zeros(32, np.float32))

@@ -21,7 +21,7 @@ def test_driver_reports_the_abi():
     assert os.path.exists(DRIVER), "build the library first (make -C tenferro-decision-rs_amd)"
     r = run("abi")
     assert r.returncode == 0
-    assert r.stdout.split() == ["abi", "1", "tenferro-decision.laya_attention_block.v1",
+    assert r.stdout.split() == ["abi", "2", "tenferro-decision.laya_attention_block.v1",
                                 "tenferro-decision.jeff_full_attention.v1"]
 
 

@@ -2,6 +2,7 @@
 CPU oracle on identical seeded inputs. Tolerances are the north star's:
 max-abs <= 2e-5 for f32, <= 1e-2 for bf16; NaN positions must match exactly.
 """
+import os
 import sys
 
 import numpy as np
@@ -588,19 +589,62 @@ def test_jeff_c5_reduced_matches_oracle(gpu_ctx):
     print(f"C5 (L 1024) bf16 max abs error vs oracle {err:.3e}")
 
 
-def test_jeff_c5_full_bf16_matches_f32_gpu(gpu_ctx):
-    """C5 at full size (2 rows x 8192): the bf16 kernel against the f32 kernel
-    (itself parity-tested against the oracle) on the same bf16-valued inputs."""
+@pytest.fixture(scope="module")
+def c5_full():
+    """C5 at full size (2 rows x 8192, GQA 8/2 x 256, causal, all active) and
+    the oracle's output on its bf16-valued inputs, computed on every host
+    core the process may use (about 10-20 s)."""
+    w = jeff_config(5)
+    threads = oracle.get_threads()
+    oracle.set_threads(len(os.sched_getaffinity(0)))
+    try:
+        print(f"[c5] oracle on 2 x 8192 with {oracle.get_threads()} threads", flush=True)
+        want = oracle.jeff_rows(w.q, w.k, w.v, w.gate, w.q_norm, w.k_norm, w.mask, w.rows,
+                                w.length, w.heads, w.kv_heads, w.head_dim, w.rotary_dim, w.theta,
+                                w.eps)
+    finally:
+        oracle.set_threads(threads)
+    return w, want
+
+
+def _c5_device_inputs(w):
     import torch
 
-    w = jeff_config(5)
     dev = torch.device("cuda:0")
     bits = [torch.from_numpy(te.to_bf16_bits(getattr(w, n)).view(np.int16)).to(dev)
             for n in ("q", "k", "v", "gate")]
     vals = [torch.from_numpy(getattr(w, n)).to(dev) for n in ("q", "k", "v", "gate")]
     rest = [torch.from_numpy(getattr(w, n)).to(dev) for n in ("q_norm", "k_norm", "mask")]
-    torch.cuda.synchronize()
     args = (w.rows, w.length, w.heads, w.kv_heads, w.head_dim, w.rotary_dim, w.theta, w.eps)
+    return bits, vals, rest, args
+
+
+def test_jeff_c5_full_bf16_matches_oracle(gpu_ctx, c5_full):
+    """C5 at its workload size: the bf16 kernel (512 query tiles per row, walks
+    of up to 8192 keys) against the oracle (cpu-kernels lib.rs:609-763
+    restated) on the same bf16-valued inputs, north_star tolerance 1e-2."""
+    w, want = c5_full
+    bits, _vals, rest, args = _c5_device_inputs(w)
+    got = te.jeff_full_attention_rows(*bits, *rest, *args, bf16=True, ctx=gpu_ctx)
+    err = assert_close(got.cpu().numpy(), want, BF16_TOL)
+    print(f"C5 full (2 x 8192) bf16 max abs error vs oracle {err:.3e}")
+
+
+def test_jeff_c5_full_f32_matches_oracle(gpu_ctx, c5_full):
+    """The f32 hd-256 path at C5's size (L 8192) against the oracle on the same
+    values: f32 tolerance 2e-5."""
+    w, want = c5_full
+    _bits, vals, rest, args = _c5_device_inputs(w)
+    got = te.jeff_full_attention_rows(*vals, *rest, *args, ctx=gpu_ctx)
+    err = assert_close(got.cpu().numpy(), want, F32_TOL)
+    print(f"C5 full (2 x 8192) f32 max abs error vs oracle {err:.3e}")
+
+
+def test_jeff_c5_full_bf16_matches_f32_gpu(gpu_ctx, c5_full):
+    """The bf16 kernel against the f32 kernel at full C5 size (an extra
+    comparison beside the oracle's)."""
+    w, _want = c5_full
+    bits, vals, rest, args = _c5_device_inputs(w)
     got = te.jeff_full_attention_rows(*bits, *rest, *args, bf16=True, ctx=gpu_ctx)
     ref = te.jeff_full_attention_rows(*vals, *rest, *args, ctx=gpu_ctx)
     err = assert_close(got.cpu().numpy(), ref.cpu().numpy(), BF16_TOL)

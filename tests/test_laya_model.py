@@ -232,6 +232,45 @@ def test_forward_validates_before_gpu(case, field, msg):
     ctx.close()
 
 
+def test_forward_output_kinds_checked_before_gpu(tiny):
+    """LayaModel.forward picks host or device pointers from its outputs: a
+    missing output, a short one, or a host array next to a device tensor is
+    refused before any device call (the model is assembled without uploading
+    weights; a stand-in object reports itself as a CUDA tensor)."""
+
+    class FakeCuda:
+        __module__ = "torch.fake"
+        dtype = "torch.float32"
+        is_cuda = True
+
+        def __init__(self, n):
+            self._n = n
+
+        def is_contiguous(self):
+            return True
+
+        def data_ptr(self):
+            return 1 << 40
+
+        def numel(self):
+            return self._n
+
+    ckpt = tiny[0]
+    model = tlm.LayaModel.__new__(tlm.LayaModel)
+    model.ckpt, model.ctx = ckpt, te.Context(0)
+    ids, mask, pos, mm, qt = laya_model_batch(8, 1, 3, ckpt.encoder.vocab_size, seed=3)
+    A = ckpt.agent.action_count()
+    with pytest.raises(te.InvalidArgument, match="both outputs"):
+        model.forward(ids, mask, pos, mm, qt, logits=np.zeros(3, np.float32))
+    with pytest.raises(te.InvalidArgument, match="logits: 2 elements"):
+        model.forward(ids, mask, pos, mm, qt, logits=np.zeros(2, np.float32),
+                      action=np.zeros(A, np.float32))
+    with pytest.raises(te.InvalidArgument, match="mix of host arrays and device tensors"):
+        model.forward(ids, mask, pos, mm, qt, logits=np.zeros(3, np.float32),
+                      action=FakeCuda(A))
+    model.ctx.close()
+
+
 # ------------------------------------------------------------------ GPU
 
 
