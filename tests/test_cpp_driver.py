@@ -40,7 +40,8 @@ def test_driver_closed_form_checks_gpu():
     print("[driver] check", flush=True)
     r = run("check")
     assert r.returncode == 0, r.stdout + r.stderr
-    assert "FAIL" not in r.stdout and r.stdout.count("PASS") == 8
+    assert "FAIL" not in r.stdout and r.stdout.count("PASS") == 9
+    assert "0 failure(s)" in r.stdout
 
 
 @pytest.mark.gpu
