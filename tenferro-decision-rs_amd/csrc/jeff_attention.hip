@@ -224,58 +224,71 @@ __global__ __launch_bounds__(256) void jeff_k_prep_kernel(const JeffArgs a, OutT
   }
 }
 
-// K prep for the split-head kernel (f32, HDP = 256): one workgroup = one
-// 16-key tile of one (row, kv head), written in the split layout above. K
-// arrives along keys (16-byte loads, four per thread) and is transposed
-// through LDS; thread (key tid & 15, part tid >> 4) then owns features
-// 16*part .. + 15 of its key: RMSNorm (lib.rs:676-691) with the sum of
-// squares reduced over parts by lane swaps and LDS, partial RoPE (692-709)
-// in registers when the partner feature i + rot/2 sits in the same lane
-// (rot/2 = 32: part p pairs with part p + 2, lane + 32), else through LDS.
-// Workgroups with blockIdx.x == 0 and kv head 0 also write the row's
-// active-key bits and key span.
+// K prep for the split-head kernel (f32, HDP = 256): one workgroup = 32 keys
+// (two 16-key tiles) of one (row, kv head), written in the split layout
+// above. K arrives along keys as whole 128-byte rows (feature d, keys
+// k0 .. k0 + 31: eight 16-byte loads per feature, eight per thread) and is
+// transposed through LDS; thread (key tid & 31, part tid >> 5) then owns
+// features 32 part .. + 31 of its key: RMSNorm (lib.rs:676-691) with the
+// sum of squares reduced over the eight parts (lane swap, then LDS),
+// partial RoPE (692-709) in registers when the partner feature i + rot/2
+// sits in the same wave (rot/2 = 32: part p pairs with part p + 1, lane
+// + 32), else through LDS. Workgroups with blockIdx.x == 0 and kv head 0
+// also write the row's active-key bits and key span.
 __global__ __launch_bounds__(256) void jeff_k_prep_split_kernel(const JeffArgs a,
                                                                 float *__restrict__ kp,
                                                                 int *__restrict__ spans,
                                                                 uint32_t *__restrict__ kbits) {
-  constexpr int HDP = 256, KS = HDP + 4;
-  __shared__ __attribute__((aligned(16))) float Kt[16 * KS];
-  __shared__ float s_red[4 * 16];
+  constexpr int HDP = 256, KB = 32, KS = HDP + 4;
+  __shared__ __attribute__((aligned(16))) float Kt[KB * KS];
+  __shared__ float s_red[4 * KB];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int row = blockIdx.z, kvh = blockIdx.y, kt = blockIdx.x;
+  const int row = blockIdx.z, kvh = blockIdx.y;
   const int L = a.L, hd = a.hd, rh = a.rot_half;
-  const int k0 = kt * 16;
+  const int k0 = blockIdx.x * KB;
   const float *maskr = a.mask + (size_t)row * L;
   const float *K = static_cast<const float *>(a.k) + row * a.kv_row + (size_t)kvh * hd * L;
 
-  // Raw tile along keys: task (feature d, keys k0 + 4*g4 .. + 3), L % 4 == 0;
-  // features past hd and keys past L read as 0.
-  const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(K, (uint32_t)((size_t)hd * L * 4));
-  f32x4 x[4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const int e = tid + 256 * t, d = e >> 2, g4 = e & 3;
-    x[t] = buffer_load4(rk, (d * L + 4 * g4) * 4, k0 * 4);
+  // A block with no active key is never read: the attention kernel walks
+  // only from the row's first active key on, and inside that range it skips
+  // (or masks whole) tiles without active keys. Such blocks leave their
+  // workspace untouched, except the one that also writes the row's bits.
+  if (!(blockIdx.x == 0 && kvh == 0)) {
+    const int kl = min(k0 + (lane & 31), L - 1);
+    const bool act = k0 + (lane & 31) < L && maskr[kl] != 0.0f;
+    if (__ballot(act) == 0) return;  // the same in every wave
   }
-  const int key = k0 + (tid & 15), part = tid >> 4;
+
+  // Raw block along keys: task (feature d, keys k0 + 4 g8 .. + 3), L % 4 == 0;
+  // features past hd and keys past L read as 0 (keys past L of this feature
+  // are the next feature's and are zeroed below).
+  const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(K, (uint32_t)((size_t)hd * L * 4));
+  f32x4 x[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const int e = tid + 256 * t, d = e >> 3, g8 = e & 7;
+    x[t] = buffer_load4(rk, (d * L + 4 * g8) * 4, k0 * 4);
+  }
+  const int kk = tid & 31, part = tid >> 5;  // this thread's key and 32-feature part
+  const int key = k0 + kk;
   const bool kin = key < L;
   const __amdgpu_buffer_rsrc_t rn = buffer_rsrc(a.k_norm, (uint32_t)(hd * 4));
-  f32x4 wn[4];
+  f32x4 wn[8];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) wn[c] = buffer_load4(rn, (16 * part + 4 * c) * 4, 0);
+  for (int c = 0; c < 8; ++c) wn[c] = buffer_load4(rn, (32 * part + 4 * c) * 4, 0);
   const bool rope = a.cos_t != nullptr && rh > 0;
   const int start = a.trim ? wave_first_active(maskr, L, lane) : 0;
   const size_t pos = (size_t)min(max(key - start, 0), L - 1) * rh;
-  f32x4 tc[4], ts[4];  // rot/2 == 32, wave 0: pairs i = 16*(part & 1) + 4c + e
-  if (rope && rh == 32 && wave == 0) {
+  f32x4 tc[8], ts[8];  // rot/2 == 32, parts 0 and 1 (wave 0): pairs i = 4c + e of its key
+  if (rope && rh == 32 && part < 2) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      tc[c] = *reinterpret_cast<const f32x4 *>(a.cos_t + pos + 16 * (part & 1) + 4 * c);
-      ts[c] = *reinterpret_cast<const f32x4 *>(a.sin_t + pos + 16 * (part & 1) + 4 * c);
+    for (int c = 0; c < 8; ++c) {
+      tc[c] = *reinterpret_cast<const f32x4 *>(a.cos_t + pos + 4 * c);
+      ts[c] = *reinterpret_cast<const f32x4 *>(a.sin_t + pos + 4 * c);
     }
   }
 
-  if (kt == 0 && kvh == 0 && wave == 0) {
+  if (blockIdx.x == 0 && kvh == 0 && wave == 0) {
     // The row's active keys: one bit per key (zero past L) and the (first,
     // last) span, (0, -1) for a row with none.
     uint32_t *bits = kbits + (size_t)row * ((L + 31) / 32);
@@ -305,59 +318,56 @@ __global__ __launch_bounds__(256) void jeff_k_prep_split_kernel(const JeffArgs a
   }
 
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const int e = tid + 256 * t, d = e >> 2, g4 = e & 3;
+  for (int t = 0; t < 8; ++t) {
+    const int e = tid + 256 * t, d = e >> 3, g8 = e & 7;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) Kt[(4 * g4 + i) * KS + d] = x[t][i];
+    for (int i = 0; i < 4; ++i) Kt[(4 * g8 + i) * KS + d] = x[t][i];
   }
   __syncthreads();
-  float kv[16];
+  float kv[32];
   float ss = 0.0f;
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const f32x4 y = *reinterpret_cast<const f32x4 *>(&Kt[(tid & 15) * KS + 16 * part + 4 * c]);
+  for (int c = 0; c < 8; ++c) {
+    const f32x4 y = *reinterpret_cast<const f32x4 *>(&Kt[kk * KS + 32 * part + 4 * c]);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       kv[4 * c + e] = kin ? y[e] : 0.0f;
       ss += kv[4 * c + e] * kv[4 * c + e];
     }
   }
-  ss = pair_sum(pair16_sum(ss));  // the wave's four parts of this key
-  if (lane < 16) s_red[wave * 16 + lane] = ss;
+  ss = pair_sum(ss);  // the wave's two parts of this key
+  if (lane < 32) s_red[wave * KB + lane] = ss;
   __syncthreads();
-  const int kk = tid & 15;
-  const float tot = s_red[kk] + s_red[16 + kk] + s_red[32 + kk] + s_red[48 + kk];
+  const float tot = s_red[kk] + s_red[KB + kk] + s_red[2 * KB + kk] + s_red[3 * KB + kk];
   const float scale = rms_scale(tot, hd, a.eps);
 #pragma unroll
-  for (int c = 0; c < 4; ++c)
+  for (int c = 0; c < 8; ++c)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int d = 16 * part + 4 * c + e;
+      const int d = 32 * part + 4 * c + e;
       kv[4 * c + e] = (kin && d < hd) ? rms_apply(kv[4 * c + e], scale, wn[c][e]) : 0.0f;
     }
   if (rope && rh == 32) {
-    // Part p < 2 holds pairs i = 16p + j, part p + 2 (lane + 32, same wave)
-    // their partners i + 32.
+    // Part 0 (lanes 0..31 of wave 0) holds pairs i = j, part 1 (lanes
+    // 32..63 of the same wave) their partners i + 32.
+    if (wave == 0) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      // r[1] holds lanes 32..63 in both halves, r[0] lanes 0..31: the
-      // partner of lane l < 32 is r[1], of lane l >= 32 r[0].
-      const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(kv[j]), __float_as_uint(kv[j]),
-                                                      false, false);
-      const float other = __uint_as_float(lane < 32 ? r[1] : r[0]);
-      const float xl = part < 2 ? kv[j] : other, yh = part < 2 ? other : kv[j];
-      if (kin && wave == 0) {
+      for (int j = 0; j < 32; ++j) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(kv[j]),
+                                                        __float_as_uint(kv[j]), false, false);
+        const float other = __uint_as_float(lane < 32 ? r[1] : r[0]);
+        const float xl = part == 0 ? kv[j] : other, yh = part == 0 ? other : kv[j];
         const float cc = tc[j >> 2][j & 3], sn = ts[j >> 2][j & 3];
-        kv[j] = part < 2 ? rope_lo(xl, yh, cc, sn) : rope_hi(xl, yh, cc, sn);
+        if (kin) kv[j] = part == 0 ? rope_lo(xl, yh, cc, sn) : rope_hi(xl, yh, cc, sn);
       }
     }
   } else if (rope) {
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < 16; ++j) Kt[kk * KS + 16 * part + j] = kv[j];
+    for (int j = 0; j < 32; ++j) Kt[kk * KS + 32 * part + j] = kv[j];
     __syncthreads();
     if (kin) {
-      for (int i = part; i < rh; i += 16) {
+      for (int i = part; i < rh; i += 8) {
         const float xl = Kt[kk * KS + i], yh = Kt[kk * KS + i + rh];
         const float cc = a.cos_t[pos + i], sn = a.sin_t[pos + i];
         Kt[kk * KS + i] = rope_lo(xl, yh, cc, sn);
@@ -366,14 +376,16 @@ __global__ __launch_bounds__(256) void jeff_k_prep_split_kernel(const JeffArgs a
     }
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < 16; ++j) kv[j] = Kt[kk * KS + 16 * part + j];
+    for (int j = 0; j < 32; ++j) kv[j] = Kt[kk * KS + 32 * part + j];
   }
   const int Lp = (L + 15) & ~15;
-  float *unit = kp + ((size_t)row * a.kv_heads + kvh) * (size_t)Lp * HDP;
+  if (key < Lp) {
+    float *unit = kp + ((size_t)row * a.kv_heads + kvh) * (size_t)Lp * HDP;
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const f32x4 o = {kv[4 * c], kv[4 * c + 1], kv[4 * c + 2], kv[4 * c + 3]};
-    *reinterpret_cast<f32x4 *>(unit + split_kp_offset(key, 16 * part + 4 * c)) = o;
+    for (int c = 0; c < 8; ++c) {
+      const f32x4 o = {kv[4 * c], kv[4 * c + 1], kv[4 * c + 2], kv[4 * c + 3]};
+      *reinterpret_cast<f32x4 *>(unit + split_kp_offset(key, 32 * part + 4 * c)) = o;
+    }
   }
 }
 
@@ -1776,7 +1788,7 @@ static hipError_t launch_jeff_f32_hd(const JeffArgs &a, int rows, float *kp, hip
       int *spans = reinterpret_cast<int *>(reinterpret_cast<char *>(kp) +
                                            jeff_kp_main_bytes(a, rows, HDP, false));
       uint32_t *kbits = reinterpret_cast<uint32_t *>(spans + 2 * rows);
-      const dim3 sp((a.L + 15) / 16, a.kv_heads, rows);
+      const dim3 sp((a.L + 31) / 32, a.kv_heads, rows);
       hipExtLaunchKernelGGL(jeff_k_prep_split_kernel, sp, dim3(256), 0, stream, ev.start, nullptr,
                             0, a, kp, spans, kbits);
       hipError_t e = hipGetLastError();
