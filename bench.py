@@ -351,6 +351,9 @@ def run(args):
                                "peak": peak, "dtype": "bf16" if bf else "f32",
                                "tokens_per_s": round(wj.valid_tokens() / (msj * 1e-3), 1),
                                "algorithmic_flops": fj}
+            if cfg == 4:
+                also["C4_dropin_per_row"] = dropin_rows_line(args, ctx, wj, tq, tk, tv, tg, tqn,
+                                                             tkn, tm, kj)
             if cfg == 4 and not args.no_cpu:
                 cores = host_threads()[0]
                 t = cpu_jeff_rows(wj, 2, cores)
@@ -391,6 +394,41 @@ def run(args):
         result["gpu_over_cpu"] = round(value / (flops / t_all / 1e12), 1)
     ctx.close()
     return result
+
+
+def dropin_rows_line(args, ctx, w, tq, tk, tv, tg, tqn, tkn, tm, rows_kernel_ms):
+    """C4 through the drop-in op the way jeff-infer calls it (model.rs:755-768):
+    one call per question row, q/gate (L, 2048) and K/V expanded to all 8
+    heads (checkpoint.rs:307-319), with TFD_KV_HEADS(2) (one head per GQA
+    group read) and without (every copy read). Kernel time per row (the
+    calls' own dispatch events) beside the rows entry's per-row share."""
+    import torch
+
+    import tenferro_ext as te
+
+    R, L, H, KV, hd = w.rows, w.length, w.heads, w.kv_heads, w.head_dim
+    W, G = H * hd, H // KV
+    # (row, kv head, hd, L) -> every kv head repeated G times: the expansion
+    expand = lambda t: t.view(R, KV, hd * L).repeat_interleave(G, dim=1).reshape(-1).contiguous()
+    ke, ve = expand(tk), expand(tv)
+    oj = torch.empty(R * L * W, dtype=torch.float32, device=tq.device)
+    out = {}
+    for name, kvh in (("kv_heads_flag", KV), ("every_copy", None)):
+        def step():
+            for r in range(R):
+                sl = slice(r * L * W, (r + 1) * L * W)
+                te.jeff_full_attention(tq[sl], ke[sl], ve[sl], tg[sl], tqn, tkn,
+                                       tm[r * L:(r + 1) * L], H, hd, w.rotary_dim, w.theta, w.eps,
+                                       q_shape=(L, W), ctx=ctx, out=oj[sl], kv_heads=kvh)
+        ms, kern = time_gpu(step, max(5, args.steps // 5), max(2, args.warmup // 5), ctx)
+        out[name] = {"kernel_us_per_row": round(kern * 1e3, 3),
+                     "wall_us_per_row": round(ms * 1e3 / R, 3)}
+    out["rows_entry_kernel_us_per_row"] = round(rows_kernel_ms * 1e3 / R, 3)
+    out["flag_over_rows_entry"] = round(out["kv_heads_flag"]["kernel_us_per_row"]
+                                        / out["rows_entry_kernel_us_per_row"], 2)
+    out["note"] = ("one launch pair (K prep, attention) per 256-token row: a row fills 128 "
+                   "workgroups of 256 CUs, so per-call latency, not the GQA reads, bounds it")
+    return out
 
 
 def _layer_steps(ctx, dev):

@@ -55,6 +55,14 @@ extern "C" {
 #define TFD_ASYNC 2u       /* with TFD_DEVICE_PTRS: enqueue on the context stream and return */
 #define TFD_TRIM_LEADING 4u /* Jeff rows: drop each row's leading inactive keys and
                                restart RoPE positions at the first active one */
+/* Jeff drop-in on GQA-expanded K/V: the caller states kv_heads (bits 16..31),
+ * heads / kv_heads consecutive heads of K and V being identical copies, as
+ * jeff-infer's checkpoint expansion makes them (checkpoint.rs:307-319; the
+ * reference's raw CUDA path recovers the same grouping from the weights,
+ * dedupe_kv, cuda_raw.rs:243-279). The op then reads only the first head of
+ * each group. 0 (the default) treats every head as distinct. */
+#define TFD_KV_HEADS(kv_heads) ((((unsigned)(kv_heads)) & 0xffffu) << 16)
+#define TFD_KV_HEADS_MASK 0xffff0000u
 
 typedef struct tfd_ctx tfd_ctx;
 
@@ -135,6 +143,8 @@ int tfd_laya_attention_structured_f32(tfd_ctx *ctx, const float *qkv, size_t hid
  *       debug-asserts these; the ABI checks them).
  *   q_norm_len, k_norm_len: must be head_dim; mask_len: must be length.
  * A query with no active key at or before it yields 0 (times the gate).
+ * flags may carry TFD_KV_HEADS(kv_heads) for expanded GQA K/V (see above):
+ * same results, 1/(heads/kv_heads) of the K/V reads.
  */
 int tfd_jeff_full_attention_f32(tfd_ctx *ctx, const float *q, const size_t *q_shape,
                                 size_t q_rank, const float *k, size_t k_len, const float *v,

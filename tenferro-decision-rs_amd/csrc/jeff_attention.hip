@@ -144,7 +144,7 @@ __global__ __launch_bounds__(256) void jeff_k_prep_kernel(const JeffArgs a, OutT
   const int L = a.L, hd = a.hd, rh = a.rot_half;
   const int k0 = blockIdx.x * kKeyTile;
   const bool bf = sizeof(OutT) == 2;
-  const size_t kv_off = row * a.kv_row + (size_t)kvh * hd * L;
+  const size_t kv_off = row * a.kv_row + (size_t)kvh * a.kv_head;
   const int kk = tid & 31, part = tid >> 5;
   const int key = k0 + kk;
   const bool kin = key < L;
@@ -247,7 +247,7 @@ __global__ __launch_bounds__(256) void jeff_k_prep_split_kernel(const JeffArgs a
   const int L = a.L, hd = a.hd, rh = a.rot_half;
   const int k0 = blockIdx.x * KB;
   const float *maskr = a.mask + (size_t)row * L;
-  const float *K = static_cast<const float *>(a.k) + row * a.kv_row + (size_t)kvh * hd * L;
+  const float *K = static_cast<const float *>(a.k) + row * a.kv_row + (size_t)kvh * a.kv_head;
 
   // A block with no active key is never read: the attention kernel walks
   // only from the row's first active key on, and inside that range it skips
@@ -739,7 +739,7 @@ __global__ __launch_bounds__(kJeffF32Waves * 64, 1) void jeff_attention_f32_kern
   const float *maskr = a.mask + (size_t)row * L;
   const float *Q = static_cast<const float *>(a.q) + row * a.q_row + (size_t)head * hd * L;
   const float *Gt = static_cast<const float *>(a.gate) + row * a.q_row + (size_t)head * hd * L;
-  const float *V = static_cast<const float *>(a.v) + row * a.kv_row + (size_t)kvh * hd * L;
+  const float *V = static_cast<const float *>(a.v) + row * a.kv_row + (size_t)kvh * a.kv_head;
   const float *KP = kp + ((size_t)row * a.kv_heads + kvh) * L * HDP;
   float *OUT = a.out + row * a.q_row + (size_t)head * hd * L;
   float *qw = smem + wave * (kJeffWaveQueries * QP);
@@ -917,7 +917,7 @@ __device__ __noinline__ void jeff_redo_wave(const JeffArgs *ap, const float *__r
   const float *maskr = a.mask + (size_t)row * L;
   const float *Q = static_cast<const float *>(a.q) + row * a.q_row + (size_t)head * hd * L;
   const float *Gt = static_cast<const float *>(a.gate) + row * a.q_row + (size_t)head * hd * L;
-  const float *V = static_cast<const float *>(a.v) + row * a.kv_row + (size_t)kvh * hd * L;
+  const float *V = static_cast<const float *>(a.v) + row * a.kv_row + (size_t)kvh * a.kv_head;
   constexpr bool SPLIT = TAG == 1;
   const size_t Lu = SPLIT ? (size_t)((L + 15) & ~15) : (size_t)L;
   const float *KP = kp + ((size_t)row * a.kv_heads + kvh) * Lu * HDP;
@@ -1077,7 +1077,7 @@ __global__ __launch_bounds__(256, 4) void jeff_split_f32_kernel(const JeffArgs a
   const int q0 = qt * 16, q = q0 + col;
   const float *Q = static_cast<const float *>(a.q) + row * a.q_row + (size_t)head * hd * L;
   const float *Gt = static_cast<const float *>(a.gate) + row * a.q_row + (size_t)head * hd * L;
-  const float *V = static_cast<const float *>(a.v) + row * a.kv_row + (size_t)kvh * hd * L;
+  const float *V = static_cast<const float *>(a.v) + row * a.kv_row + (size_t)kvh * a.kv_head;
   const int Lp = (L + 15) & ~15;
   const float *KP = kp + ((size_t)row * a.kv_heads + kvh) * (size_t)Lp * HDP;
   const uint32_t *rbits = kbits + (size_t)row * ((L + 31) / 32);
@@ -1523,7 +1523,7 @@ __global__ __launch_bounds__(256, 2) void jeff_attention_bf16_kernel(const JeffA
   const float *maskr = a.mask + (size_t)row * L;
   const uint16_t *Q = static_cast<const uint16_t *>(a.q) + row * a.q_row + (size_t)head * hd * L;
   const uint16_t *Gt = static_cast<const uint16_t *>(a.gate) + row * a.q_row + (size_t)head * hd * L;
-  const uint16_t *V = static_cast<const uint16_t *>(a.v) + row * a.kv_row + (size_t)kvh * hd * L;
+  const uint16_t *V = static_cast<const uint16_t *>(a.v) + row * a.kv_row + (size_t)kvh * a.kv_head;
   const uint16_t *KP = kp + ((size_t)row * a.kv_heads + kvh) * L * HDP;
   float *OUT = a.out + row * a.q_row + (size_t)head * hd * L;
   const bool rope = a.cos_t != nullptr && rh > 0;

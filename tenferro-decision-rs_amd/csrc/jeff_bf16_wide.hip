@@ -128,7 +128,7 @@ __global__ __launch_bounds__(256, kWideBlocks == 1 ? 2 : 1) void jeff_bf16_wide_
   const uint16_t *Gh =
       static_cast<const uint16_t *>(a.gate) + row * a.q_row + (size_t)head * kWideHd * L;
   const uint16_t *Vh =
-      static_cast<const uint16_t *>(a.v) + row * a.kv_row + (size_t)kvh * kWideHd * L;
+      static_cast<const uint16_t *>(a.v) + row * a.kv_row + (size_t)kvh * a.kv_head;
   const uint16_t *Kh = kp + ((size_t)row * a.kv_heads + kvh) * (size_t)L * kWideHd;
   float *Oh = a.out + row * a.q_row + (size_t)head * kWideHd * L;
 

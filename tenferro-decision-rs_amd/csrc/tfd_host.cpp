@@ -355,13 +355,18 @@ int laya_run(tfd_ctx *c, const char *op, const float *qkv, const uint8_t *keep,
 
 // ------------------------------------------------------------------ Jeff run
 
+// kv_copies > 1: K and V hold kv_heads * kv_copies heads, each group of
+// kv_copies consecutive heads identical copies (GQA weights expanded as
+// jeff-infer checkpoint.rs:307-319 does); only the first head of each group
+// is read.
 int jeff_run(tfd_ctx *c, const char *op, bool bf16, size_t rows, size_t length, size_t heads,
              size_t kv_heads, size_t head_dim, size_t rotary_dim, const void *q, const void *k,
              const void *v, const void *gate, const float *q_norm, const float *k_norm,
              const float *mask, uint32_t theta_bits, uint32_t eps_bits, float *out,
-             unsigned flags) {
-  size_t width = 0, kv_width = 0, qn = 0, kvn = 0, mn = 0;
-  if (!mul_ok(heads, head_dim, &width) || !mul_ok(kv_heads, head_dim, &kv_width) ||
+             unsigned flags, size_t kv_copies = 1) {
+  size_t width = 0, kv_width = 0, qn = 0, kvn = 0, mn = 0, kv_stored = 0;
+  if (!mul_ok(heads, head_dim, &width) || !mul_ok(kv_heads, kv_copies, &kv_stored) ||
+      !mul_ok(kv_stored, head_dim, &kv_width) ||
       !mul_ok(width, length, &qn) || !mul_ok(qn, rows, &qn) || !mul_ok(kv_width, length, &kvn) ||
       !mul_ok(kvn, rows, &kvn) || !mul_ok(rows, length, &mn))
     return invalid(c, op, "shape", "attention dimensions overflow");
@@ -410,6 +415,7 @@ int jeff_run(tfd_ctx *c, const char *op, bool bf16, size_t rows, size_t length, 
   a.c1 = (1.0f / sqrtf((float)head_dim)) * kLog2e;
   a.q_row = qn / rows;
   a.kv_row = kvn / rows;
+  a.kv_head = kv_copies * head_dim * length;
   if (a.rot_half > 0) {
     if ((rc = rope_table(c, 1, length, rotary_dim, bits_to_f32(theta_bits), theta_bits, &a.cos_t,
                          &a.sin_t)))
@@ -1078,6 +1084,8 @@ int tfd_jeff_full_attention_f32(tfd_ctx *c, const float *q, const size_t *q_shap
                                 size_t out_len, unsigned flags) {
   if (!c) return TFD_EINVAL;
   c->err.clear();
+  const size_t kv_groups = (flags & TFD_KV_HEADS_MASK) >> 16;  // 0: every head distinct
+  flags &= ~TFD_KV_HEADS_MASK;
   int rc = check_flags(c, kJeffOp, flags, TFD_DEVICE_PTRS | TFD_ASYNC);
   if (rc) return rc;
   // jeff_attention.rs:116-125
@@ -1101,8 +1109,11 @@ int tfd_jeff_full_attention_f32(tfd_ctx *c, const float *q, const size_t *q_shap
     return invalid(c, kJeffOp, "rotary_dim", "rotary_dim must not exceed head_dim");
   if (n != 0 && (!q || !k || !v || !gate || !q_norm || !k_norm || !mask || !out))
     return invalid(c, kJeffOp, "inputs", "null buffer");
-  return jeff_run(c, kJeffOp, false, 1, length, heads, heads, head_dim, rotary_dim, q, k, v, gate,
-                  q_norm, k_norm, mask, theta_bits, eps_bits, out, flags);
+  if (kv_groups != 0 && heads % kv_groups != 0)
+    return invalid(c, kJeffOp, "flags", "TFD_KV_HEADS(kv_heads): kv_heads must divide heads");
+  const size_t kvh = kv_groups ? kv_groups : heads;
+  return jeff_run(c, kJeffOp, false, 1, length, heads, kvh, head_dim, rotary_dim, q, k, v, gate,
+                  q_norm, k_norm, mask, theta_bits, eps_bits, out, flags, heads / kvh);
 }
 
 int tfd_jeff_full_attention_rows_f32(tfd_ctx *c, size_t rows, size_t length, size_t heads,

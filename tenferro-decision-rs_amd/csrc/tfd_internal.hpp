@@ -73,7 +73,10 @@ struct JeffArgs {
   int cus;                       // compute units of the device (grid shapes)
   float c1;                      // (1/sqrt(hd)) * log2(e)
   float eps;
-  size_t q_row, kv_row;          // elements per row: L*heads*hd and L*kv_heads*hd
+  size_t q_row, kv_row;          // elements per row: L*heads*hd and L*kv_heads*hd (times
+                                 // the copies of an expanded K/V, see kv_head)
+  size_t kv_head;                // elements between consecutive kv heads of K/V: L*hd, or
+                                 // L*hd*G when each of G expanded copies is skipped
 };
 
 // Timing of an op's attention kernel(s): `start` is recorded when the first

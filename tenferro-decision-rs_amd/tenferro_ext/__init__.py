@@ -44,6 +44,12 @@ TFD_HOST_PTRS = 0
 TFD_DEVICE_PTRS = 1
 TFD_ASYNC = 2
 TFD_TRIM_LEADING = 4
+TFD_KV_HEADS_MASK = 0xFFFF0000
+
+
+def TFD_KV_HEADS(kv_heads: int) -> int:
+    """Flag for the Jeff drop-in on GQA-expanded K/V (include/tfd_attention.h)."""
+    return (int(kv_heads) & 0xFFFF) << 16
 
 # Every entry point the header declares, in declaration order.
 EXPORTED_SYMBOLS = (
@@ -458,8 +464,12 @@ class JeffFullAttentionOp:
         return tuple(q_shape)
 
     def execute(self, q, q_shape, k, v, gate, q_norm, k_norm, mask, *,
-                ctx: Optional[Context] = None, out=None):
-        """execute_jeff_full_attention_in_session (jeff_attention.rs:103-184)."""
+                ctx: Optional[Context] = None, out=None, kv_heads: Optional[int] = None):
+        """execute_jeff_full_attention_in_session (jeff_attention.rs:103-184).
+
+        kv_heads: k and v are GQA-expanded (heads / kv_heads consecutive heads
+        are copies, jeff-infer checkpoint.rs:307-319); only the first head
+        of each group is read (TFD_KV_HEADS)."""
         ctx = ctx or default_context()
         n = 1
         for s in q_shape:
@@ -472,6 +482,8 @@ class JeffFullAttentionOp:
             out = _new_out(args[0], n)
         a_out = _Arg(out, np.float32, "out")
         flags = _flags(args + [a_out], ctx)
+        if kv_heads is not None:
+            flags |= TFD_KV_HEADS(kv_heads)
         shape = _shape_arr(q_shape)
         aq, ak, av, ag, aqn, akn, am = args
         _call(ctx, flags, ctx._lib.tfd_jeff_full_attention_f32,
@@ -523,15 +535,18 @@ def laya_attention_structured(qkv, valid, hidden: int, heads: int, length: int, 
 def jeff_full_attention(q, k, v, gate, q_norm, k_norm, mask, heads: int, head_dim: int,
                         rotary_dim: int, theta: float, eps: float, *,
                         q_shape: Optional[Sequence[int]] = None,
-                        ctx: Optional[Context] = None, out=None):
+                        ctx: Optional[Context] = None, out=None,
+                        kv_heads: Optional[int] = None):
     """``session.jeff_full_attention(q, k, v, gate, q_norm, k_norm, mask, heads,
-    head_dim, rotary_dim, theta, eps)``; q/k/v/gate are (length, width)."""
+    head_dim, rotary_dim, theta, eps)``; q/k/v/gate are (length, width).
+    kv_heads: k/v are GQA-expanded copies; read one head per group."""
     if q_shape is None:
         q_shape = tuple(q.shape)
         if not _is_torch(q):
             q, k, v, gate = (np.asarray(x).reshape(-1, order="F") for x in (q, k, v, gate))
     op = JeffFullAttentionOp(heads, head_dim, rotary_dim, f32_bits(theta), f32_bits(eps))
-    return op.execute(q, q_shape, k, v, gate, q_norm, k_norm, mask, ctx=ctx, out=out)
+    return op.execute(q, q_shape, k, v, gate, q_norm, k_norm, mask, ctx=ctx, out=out,
+                      kv_heads=kv_heads)
 
 
 def jeff_full_attention_rows(q, k, v, gate, q_norm, k_norm, mask, rows: int, length: int,

@@ -161,6 +161,20 @@ def test_jeff_rejects_like_reference(ctx):
     assert rc == te.TFD_EINVAL and "rotary_dim" in msg
 
 
+def test_jeff_dropin_kv_heads_flag_validated(ctx):
+    """TFD_KV_HEADS(kv) must divide heads; rejected before any device access."""
+    n = 8 * 16
+    buf = np.zeros(n, np.float32)
+    vec = np.zeros(8, np.float32)
+    arr = (ctypes.c_size_t * 2)(8, 16)
+    p = buf.ctypes.data
+    rc = ctx._lib.tfd_jeff_full_attention_f32(
+        ctx.handle, p, arr, 2, p, n, p, n, p, n, vec.ctypes.data, 4, vec.ctypes.data, 4,
+        vec.ctypes.data, 8, 4, 4, 4, te.f32_bits(1e7), te.f32_bits(1e-6), p, n, te.TFD_KV_HEADS(3))
+    assert rc == te.TFD_EINVAL and "kv_heads must divide heads" in ctx._lib.tfd_last_error(
+        ctx.handle).decode()
+
+
 def test_jeff_rows_rejects_bad_gqa_and_flags(ctx):
     f = np.zeros(64, np.float32)
     p = f.ctypes.data

@@ -323,6 +323,38 @@ def test_jeff_dropin_matches_oracle(gpu_ctx, length, hd, rot):
         assert_close(got, want, F32_TOL)
 
 
+@pytest.mark.parametrize("length,hd,heads,kv_heads,rot", [
+    (256, 256, 8, 2, 64),   # one C4 row: the split-head path
+    (70, 64, 8, 2, 16),     # the general kernel (L % 4 != 0)
+    (33, 128, 6, 3, 0),
+    (48, 256, 4, 1, 32),
+])
+def test_jeff_dropin_gqa_flag_matches_oracle(gpu_ctx, length, hd, heads, kv_heads, rot):
+    """The drop-in on GQA-expanded K/V (jeff-infer checkpoint.rs:307-319) with
+    TFD_KV_HEADS(kv_heads): reads one head per group, results as the oracle on
+    the expanded inputs, and bitwise equal to the call that reads every copy."""
+    rng = Lcg(1000 + length + hd + heads)
+    W, KW = heads * hd, kv_heads * hd
+    q = rng.normal(length * W).astype(np.float32)
+    g = rng.normal(length * W).astype(np.float32)
+    kc = rng.normal(length * KW).astype(np.float32)
+    vc = rng.normal(length * KW).astype(np.float32)
+    qn = (rng.normal(hd) * 0.1).astype(np.float32)
+    kn = (rng.normal(hd) * 0.1).astype(np.float32)
+    mask = np.ones(length, np.float32)
+    mask[: length // 5] = 0.0       # left padding
+    mask[length // 2] = 0.0         # an interior hole
+    k = oracle.expand_kv(kc.reshape(KW, length), length, heads, kv_heads, hd).reshape(-1)
+    v = oracle.expand_kv(vc.reshape(KW, length), length, heads, kv_heads, hd).reshape(-1)
+    want = oracle.jeff_full_attention(q, k, v, g, qn, kn, mask, length, heads, hd, rot, 1e7, 1e-6)
+    got = te.jeff_full_attention(q, k, v, g, qn, kn, mask, heads, hd, rot, 1e7, 1e-6,
+                                 q_shape=(length, W), ctx=gpu_ctx, kv_heads=kv_heads)
+    assert_close(got, want, F32_TOL)
+    every = te.jeff_full_attention(q, k, v, g, qn, kn, mask, heads, hd, rot, 1e7, 1e-6,
+                                   q_shape=(length, W), ctx=gpu_ctx)
+    assert np.array_equal(np.asarray(got).view(np.uint32), np.asarray(every).view(np.uint32))
+
+
 @pytest.mark.parametrize("heads,kv_heads", [(8, 2), (4, 4), (6, 3), (8, 1), (2, 1)])
 def test_jeff_rows_gqa_matches_oracle(gpu_ctx, heads, kv_heads):
     rows, length, hd, rot = 3, 70, 64, 16
