@@ -121,6 +121,28 @@ int tfd_laya_attention_block_f32(tfd_ctx *ctx, const float *qkv, const size_t *q
                                  float *out, size_t out_len, unsigned flags);
 
 /*
+ * The Laya drop-in without any allocation (no counterpart in the reference:
+ * an entry for callers that cannot allocate device memory -- code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, checks and results as tfd_laya_attention_block_f32, but:
+ *   - operands must be device pointers (TFD_DEVICE_PTRS; TFD_ASYNC allowed);
+ *   - its workspace (RoPE tables, packed keep words, tile map) lives in one
+ *     static 16 MiB device array per GPU, held until the process ends: it
+ *     needs 4*L*hd + 4*L*B*ceil(L/32) bytes plus a small tile map (L 2048,
+ *     B 8, hd 128: 5 MiB); a call that needs more returns TFD_EUNSUPPORTED
+ *     before any device access;
+ *   - no timing events are recorded (tfd_ctx_set_timing is ignored).
+ * Every call on a GPU shares that GPU's array: calls that overlap on one GPU
+ * (several threads or streams) race. A context made by tfd_ctx_create creates
+ * its stream on first use; tfd_ctx_create_on_stream adopts the caller's.
+ */
+int tfd_laya_attention_block_noalloc_f32(tfd_ctx *ctx, const float *qkv, const size_t *qkv_shape,
+                                         size_t qkv_rank, size_t qkv_len, const uint8_t *keep,
+                                         size_t keep_len, size_t hidden, size_t heads,
+                                         uint32_t rope_base_bits, float *out, size_t out_len,
+                                         unsigned flags);
+
+/*
  * Laya with a structured mask instead of the (L, L, B) keep tensor: the keep
  * tensor is the one build_mask (laya-infer model.rs:465-490) makes from
  * valid (L, B) (one byte per token, l + L*b) and window:

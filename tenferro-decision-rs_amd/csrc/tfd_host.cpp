@@ -232,6 +232,47 @@ int rope_table(tfd_ctx *c, int kind, size_t length, size_t dim, float base, uint
   return TFD_OK;
 }
 
+// The no-allocation entry's RoPE tables: computed on the host exactly as
+// rope_table() does, into a static host buffer, and copied into the start of
+// the device scratch; the (length, dim, base) last copied to each device is
+// remembered, and an unchanged table is not copied again.
+constexpr size_t kNoallocRopeMax = (size_t)1 << 19;  // floats per table (L * hd / 2)
+float g_noalloc_rope_host[2 * kNoallocRopeMax];
+struct NoallocRopeKey {
+  bool valid = false;
+  size_t length = 0, dim = 0;
+  uint32_t bits = 0;
+};
+NoallocRopeKey g_noalloc_rope_key[64];
+
+int noalloc_rope_table(tfd_ctx *c, size_t length, size_t dim, float base, uint32_t bits,
+                       float *dev, const float **cos_d, const float **sin_d) {
+  const size_t half = dim / 2, n = length * half;
+  *cos_d = dev;
+  *sin_d = dev + n;
+  NoallocRopeKey &key = g_noalloc_rope_key[c->device];
+  if (key.valid && key.length == length && key.dim == dim && key.bits == bits) return TFD_OK;
+  key.valid = false;
+  for (size_t l = 0; l < length; ++l) {
+    for (size_t i = 0; i < half; ++i) {
+      volatile float expo = -2.0f * (float)i / (float)dim;
+      volatile float angle = (float)l * powf(base, expo);
+      g_noalloc_rope_host[l * half + i] = cosf(angle);
+      g_noalloc_rope_host[n + l * half + i] = sinf(angle);
+    }
+  }
+  TFD_HIP(c, hipMemcpyAsync(dev, g_noalloc_rope_host, 2 * n * sizeof(float), hipMemcpyHostToDevice,
+                            c->stream),
+          "hipMemcpyAsync rope");
+  // The host buffer is reused by the next table: let this copy drain first.
+  TFD_HIP(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  key.length = length;
+  key.dim = dim;
+  key.bits = bits;
+  key.valid = true;
+  return TFD_OK;
+}
+
 // Event pair for the next op's attention kernel(s), recorded by their
 // dispatches (timing enabled only; both null otherwise).
 int timing_events(tfd_ctx *c, tfd::KernelEvents *ev) {
@@ -271,10 +312,13 @@ int check_flags(tfd_ctx *c, const char *op, unsigned flags, unsigned allowed) {
 
 // ------------------------------------------------------------------ Laya run
 
+// noalloc: device pointers only, and every workspace (RoPE tables, packed
+// keep words, tile map) lives in the static device scratch: nothing is
+// allocated and no timing events are created.
 int laya_run(tfd_ctx *c, const char *op, const float *qkv, const uint8_t *keep,
              const uint8_t *valid, int64_t window, size_t hidden, size_t heads, size_t length,
              size_t batch, uint32_t rope_bits, float *out, unsigned flags,
-             const uint8_t *qneed = nullptr) {
+             const uint8_t *qneed = nullptr, bool noalloc = false) {
   size_t n = 0, n3 = 0, keep_len = 0, valid_len = 0;
   if (!mul_ok(hidden, length, &n) || !mul_ok(n, batch, &n) || !mul_ok(n, 3, &n3) ||
       !mul_ok(length, length, &keep_len) || !mul_ok(keep_len, batch, &keep_len) ||
@@ -290,8 +334,27 @@ int laya_run(tfd_ctx *c, const char *op, const float *qkv, const uint8_t *keep,
     return fail(c, TFD_EUNSUPPORTED, "%s: length/hidden too large for the kernels", op);
   if (heads > 65535 || batch > 65535 || (length + tfd::kKeyTile - 1) / tfd::kKeyTile > 65535)
     return fail(c, TFD_EUNSUPPORTED, "%s: heads/batch/length exceed the launch grid", op);
+  // No-allocation layout: the RoPE tables (2 * L * hd/2 floats, rounded up
+  // to 256 bytes), then the packed keep words and the tile map.
+  const size_t nkt = (length + tfd::kKeyTile - 1) / tfd::kKeyTile;
+  const size_t rope_bytes =
+      (bits_to_f32(rope_bits) != 0.0f && !zero_fill) ? ((2 * length * (hd / 2) * 4 + 255) & ~(size_t)255) : 0;
+  if (noalloc) {
+    const size_t words = nkt * batch * length, groups = (size_t)tfd::laya_map_row((int)nkt) * batch * ((length + 63) / 64);
+    const size_t need = rope_bytes + ((sizeof(uint32_t) * words + 255) & ~(size_t)255) + groups;
+    if (length * (hd / 2) > kNoallocRopeMax || need > tfd::kNoallocScratchBytes)
+      return fail(c, TFD_EUNSUPPORTED,
+                  "%s: needs %zu bytes of workspace; this entry has %zu (use "
+                  "tfd_laya_attention_block_f32)", op, need, tfd::kNoallocScratchBytes);
+  }
   int rc = ensure_ready(c);
   if (rc) return rc;
+  unsigned char *scratch = nullptr;
+  if (noalloc) {
+    hipError_t e = hipSuccess;
+    scratch = static_cast<unsigned char *>(tfd::noalloc_scratch(c->device, &e));
+    if (!scratch) return hip_fail(c, e, "hipGetSymbolAddress(scratch)");
+  }
   void *out_d = nullptr;
   if ((rc = output(c, flags, 0, out, sizeof(float) * n, &out_d))) return rc;
   if (zero_fill) {
@@ -322,7 +385,10 @@ int laya_run(tfd_ctx *c, const char *op, const float *qkv, const uint8_t *keep,
   a.c1 = scale * kLog2e;
   const float base = bits_to_f32(rope_bits);
   if (base != 0.0f) {
-    if ((rc = rope_table(c, 0, length, hd, base, rope_bits, &a.cos_t, &a.sin_t))) return rc;
+    rc = noalloc ? noalloc_rope_table(c, length, hd, base, rope_bits,
+                                      reinterpret_cast<float *>(scratch), &a.cos_t, &a.sin_t)
+                 : rope_table(c, 0, length, hd, base, rope_bits, &a.cos_t, &a.sin_t);
+    if (rc) return rc;
   }
   int mode = tfd::kMaskStruct;
   if (keep) {
@@ -334,8 +400,13 @@ int laya_run(tfd_ctx *c, const char *op, const float *qkv, const uint8_t *keep,
         words > SIZE_MAX / 8)
       return invalid(c, op, "shape", "attention dimensions overflow");
     const size_t map_off = (sizeof(uint32_t) * words + 255) & ~(size_t)255;
-    if ((rc = reserve(c, c->bits, map_off + groups))) return rc;
-    uint8_t *base = static_cast<uint8_t *>(c->bits.ptr);
+    uint8_t *base = nullptr;
+    if (noalloc) {
+      base = scratch + rope_bytes;
+    } else {
+      if ((rc = reserve(c, c->bits, map_off + groups))) return rc;
+      base = static_cast<uint8_t *>(c->bits.ptr);
+    }
     a.bits = reinterpret_cast<const uint32_t *>(base);
     a.any = base + map_off;
     TFD_HIP(c,
@@ -347,7 +418,7 @@ int laya_run(tfd_ctx *c, const char *op, const float *qkv, const uint8_t *keep,
     a.valid = static_cast<const uint8_t *>(mask_d);
   }
   tfd::KernelEvents ev;
-  if ((rc = timing_events(c, &ev))) return rc;
+  if (!noalloc && (rc = timing_events(c, &ev))) return rc;
   TFD_HIP(c, tfd::launch_laya_attention(a, (int)heads, (int)batch, hd_pad, mode, c->stream, ev),
           "laya_attention launch");
   return finish(c, flags, out, out_d, sizeof(float) * n);
@@ -1028,35 +1099,64 @@ int tfd_ctx_take_kernel_time(tfd_ctx *c, double *total_ms, uint64_t *launches) {
   return TFD_OK;
 }
 
-int tfd_laya_attention_block_f32(tfd_ctx *c, const float *qkv, const size_t *qkv_shape,
-                                 size_t qkv_rank, size_t qkv_len, const uint8_t *keep,
-                                 size_t keep_len,
-                                 size_t hidden, size_t heads, uint32_t rope_base_bits,
-                                 float *out, size_t out_len, unsigned flags) {
+}  // extern "C"
+
+namespace {
+
+// execute_laya_attention_block_in_session's checks (laya_attention.rs:99-176)
+// and the run, shared by the drop-in and its no-allocation variant.
+int laya_block(tfd_ctx *c, const char *op, const float *qkv, const size_t *qkv_shape,
+               size_t qkv_rank, size_t qkv_len, const uint8_t *keep, size_t keep_len,
+               size_t hidden, size_t heads, uint32_t rope_base_bits, float *out, size_t out_len,
+               unsigned flags, bool noalloc) {
   if (!c) return TFD_EINVAL;
   c->err.clear();
-  int rc = check_flags(c, kLayaOp, flags, TFD_DEVICE_PTRS | TFD_ASYNC);
+  int rc = check_flags(c, op, flags, TFD_DEVICE_PTRS | TFD_ASYNC);
   if (rc) return rc;
+  if (noalloc && !(flags & TFD_DEVICE_PTRS))
+    return invalid(c, op, "flags", "this entry takes device pointers only (TFD_DEVICE_PTRS)");
   // laya_attention.rs:111-114 (and infer_output_meta 80-83)
   if (qkv_shape == nullptr || qkv_rank != 3 || hidden > SIZE_MAX / 3 ||
       qkv_shape[0] != 3 * hidden)
-    return invalid(c, kLayaOp, "shape", "attention block expects (3d, L, B)");
+    return invalid(c, op, "shape", "attention block expects (3d, L, B)");
   const size_t length = qkv_shape[1], batch = qkv_shape[2];
   size_t expect = 0;
   // cpu-kernels lib.rs:855-864: a slice shorter (or longer) than the shape
   // says is rejected before any access ("qkv length").
   if (!mul_ok(qkv_shape[0], length, &expect) || !mul_ok(expect, batch, &expect) ||
       qkv_len != expect)
-    return invalid(c, kLayaOp, "qkv", "qkv length");
+    return invalid(c, op, "qkv", "qkv length");
   // laya_attention.rs:138-140
   if (!mul_ok(length, length, &expect) || !mul_ok(expect, batch, &expect) || keep_len != expect)
-    return invalid(c, kLayaOp, "keep", "keep must be (L, L, B)");
+    return invalid(c, op, "keep", "keep must be (L, L, B)");
   if (!mul_ok(hidden, length, &expect) || !mul_ok(expect, batch, &expect) || out_len != expect)
-    return invalid(c, kLayaOp, "out", "out must be (d, L, B)");
+    return invalid(c, op, "out", "out must be (d, L, B)");
   if (expect != 0 && (!qkv || !out || (keep_len && !keep)))
-    return invalid(c, kLayaOp, "inputs", "null buffer");
-  return laya_run(c, kLayaOp, qkv, keep, nullptr, -1, hidden, heads, length, batch,
-                  rope_base_bits, out, flags);
+    return invalid(c, op, "inputs", "null buffer");
+  return laya_run(c, op, qkv, keep, nullptr, -1, hidden, heads, length, batch, rope_base_bits,
+                  out, flags, nullptr, noalloc);
+}
+
+}  // namespace
+
+extern "C" {
+
+int tfd_laya_attention_block_f32(tfd_ctx *c, const float *qkv, const size_t *qkv_shape,
+                                 size_t qkv_rank, size_t qkv_len, const uint8_t *keep,
+                                 size_t keep_len, size_t hidden, size_t heads,
+                                 uint32_t rope_base_bits, float *out, size_t out_len,
+                                 unsigned flags) {
+  return laya_block(c, kLayaOp, qkv, qkv_shape, qkv_rank, qkv_len, keep, keep_len, hidden, heads,
+                    rope_base_bits, out, out_len, flags, false);
+}
+
+int tfd_laya_attention_block_noalloc_f32(tfd_ctx *c, const float *qkv, const size_t *qkv_shape,
+                                         size_t qkv_rank, size_t qkv_len, const uint8_t *keep,
+                                         size_t keep_len, size_t hidden, size_t heads,
+                                         uint32_t rope_base_bits, float *out, size_t out_len,
+                                         unsigned flags) {
+  return laya_block(c, "tfd_laya_attention_block_noalloc_f32", qkv, qkv_shape, qkv_rank, qkv_len,
+                    keep, keep_len, hidden, heads, rope_base_bits, out, out_len, flags, true);
 }
 
 int tfd_laya_attention_structured_f32(tfd_ctx *c, const float *qkv, size_t hidden, size_t heads,

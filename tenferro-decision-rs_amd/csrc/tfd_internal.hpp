@@ -114,6 +114,16 @@ size_t jeff_bf16_flags_offset(const JeffArgs &a, int rows);
 hipError_t launch_jeff_bf16_wide(const JeffArgs &a, int rows, const uint16_t *kp, int *flags,
                                  hipStream_t stream);
 
+// ------------------------------------------------ no-allocation entry
+
+// Bytes of the static device scratch of tfd_laya_attention_block_noalloc_f32
+// (RoPE tables, packed keep words and tile map of one call).
+constexpr size_t kNoallocScratchBytes = (size_t)16 << 20;
+// The scratch array's address on `device`, which must be current: looked up
+// once per device (hipGetSymbolAddress) and kept; null with *err set on
+// failure. Device code only ever sees this address, never the array's name.
+void *noalloc_scratch(int device, hipError_t *err);
+
 // ------------------------------------------------ Laya decision-model forward
 
 enum Activation : int { kActNone = 0, kActRelu = 1, kActGelu = 2 };

@@ -66,6 +66,7 @@ EXPORTED_SYMBOLS = (
     "tfd_ctx_set_timing",
     "tfd_ctx_take_kernel_time",
     "tfd_laya_attention_block_f32",
+    "tfd_laya_attention_block_noalloc_f32",
     "tfd_laya_attention_structured_f32",
     "tfd_jeff_full_attention_f32",
     "tfd_jeff_full_attention_rows_f32",
@@ -140,6 +141,7 @@ def load_library(path: Optional[str] = None) -> ctypes.CDLL:
         "tfd_ctx_take_kernel_time": (I, [P, ctypes.POINTER(ctypes.c_double),
                                          ctypes.POINTER(ctypes.c_uint64)]),
         "tfd_laya_attention_block_f32": (I, [P, P, SP, S, S, P, S, S, S, U32, P, S, F]),
+        "tfd_laya_attention_block_noalloc_f32": (I, [P, P, SP, S, S, P, S, S, S, U32, P, S, F]),
         "tfd_laya_attention_structured_f32": (I, [P, P, S, S, S, S, P, ctypes.c_int64, U32, P, F]),
         "tfd_jeff_full_attention_f32": (
             I, [P, P, SP, S, P, S, P, S, P, S, P, S, P, S, P, S, S, S, S, U32, U32, P, S, F]),
@@ -512,6 +514,26 @@ def laya_attention_block(qkv, keep, hidden: int, heads: int, rope_base: float, *
             keep = np.asarray(keep).reshape(-1, order="F")
     op = LayaAttentionBlockOp(hidden, heads, f32_bits(rope_base))
     return op.execute(qkv, qkv_shape, keep, ctx=ctx, out=out)
+
+
+def laya_attention_block_noalloc(qkv, keep, hidden: int, heads: int, rope_base: float, *,
+                                 qkv_shape: Sequence[int], ctx: Optional[Context] = None,
+                                 out=None):
+    """The Laya drop-in's no-allocation variant (device tensors only; its
+    workspace is a static 16 MiB device array per GPU, shared by every call
+    on that GPU, so overlapping calls on one GPU race)."""
+    ctx = ctx or default_context()
+    a_qkv = _Arg(qkv, np.float32, "qkv")
+    a_keep = _Arg(keep, np.uint8, "keep")
+    n = hidden * qkv_shape[1] * qkv_shape[2] if len(qkv_shape) == 3 else 0
+    if out is None:
+        out = _new_out(a_qkv, n)
+    a_out = _Arg(out, np.float32, "out")
+    flags = _flags([a_qkv, a_keep, a_out], ctx)
+    _call(ctx, flags, ctx._lib.tfd_laya_attention_block_noalloc_f32,
+          ctx.handle, a_qkv.ptr, _shape_arr(qkv_shape), len(qkv_shape), a_qkv.n, a_keep.ptr,
+          a_keep.n, hidden, heads, f32_bits(rope_base), a_out.ptr, a_out.n, flags)
+    return a_out.obj
 
 
 def laya_attention_structured(qkv, valid, hidden: int, heads: int, length: int, batch: int,
