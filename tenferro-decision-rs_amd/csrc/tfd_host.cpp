@@ -327,9 +327,12 @@ int laya_run(tfd_ctx *c, const char *op, const float *qkv, const uint8_t *keep,
   if (n == 0) return TFD_OK;
   const bool zero_fill = heads == 0 || hidden % heads != 0;
   const size_t hd = zero_fill ? 0 : hidden / heads;
-  int hd_pad = zero_fill ? 32 : pad_head_dim(hd, 128);
-  if (!hd_pad)
-    return fail(c, TFD_EUNSUPPORTED, "%s: head_dim %zu exceeds the supported 128", op, hd);
+  // hd_pad 0: past the tiled kernels, the one-wavefront-per-query path
+  // (its LDS holds a query row and one score per key).
+  const int hd_pad = zero_fill ? 32 : pad_head_dim(hd, tfd::kLayaTiledMaxHd);
+  if (!hd_pad && hd + length > 16384)
+    return fail(c, TFD_EUNSUPPORTED, "%s: head_dim %zu with length %zu exceeds the LDS of the "
+                "path for head dims past %d", op, hd, length, tfd::kLayaTiledMaxHd);
   if (length > (size_t)INT32_MAX / 4 || hidden > (size_t)INT32_MAX / 4)
     return fail(c, TFD_EUNSUPPORTED, "%s: length/hidden too large for the kernels", op);
   if (heads > 65535 || batch > 65535 || (length + tfd::kKeyTile - 1) / tfd::kKeyTile > 65535)
@@ -391,6 +394,17 @@ int laya_run(tfd_ctx *c, const char *op, const float *qkv, const uint8_t *keep,
     if (rc) return rc;
   }
   int mode = tfd::kMaskStruct;
+  if (!hd_pad) {
+    if (keep)
+      mode = tfd::kMaskBits;
+    else
+      a.valid = static_cast<const uint8_t *>(mask_d);
+    TFD_HIP(c,
+            tfd::launch_laya_generic(a, keep ? static_cast<const uint8_t *>(mask_d) : nullptr,
+                                     (int)heads, (int)batch, mode, c->stream),
+            "laya_generic launch");
+    return finish(c, flags, out, out_d, sizeof(float) * n);
+  }
   if (keep) {
     mode = tfd::kMaskBits;
     // Workspace: the packed words, then the per-(tile, 64-query group) map.
@@ -443,10 +457,11 @@ int jeff_run(tfd_ctx *c, const char *op, bool bf16, size_t rows, size_t length, 
     return invalid(c, op, "shape", "attention dimensions overflow");
   // cpu-kernels lib.rs:643-645: nothing to do for an empty problem.
   if (qn == 0 || head_dim == 0) return TFD_OK;
-  const int hd_pad = pad_head_dim(head_dim, 256);
-  if (!hd_pad)
-    return fail(c, TFD_EUNSUPPORTED, "%s: head_dim %zu exceeds the supported 256", op,
-                head_dim);
+  // hd_pad 0: past the tiled kernels, the one-wavefront-per-query path.
+  const int hd_pad = pad_head_dim(head_dim, tfd::kJeffTiledMaxHd);
+  if (!hd_pad && head_dim + length > 16384)
+    return fail(c, TFD_EUNSUPPORTED, "%s: head_dim %zu with length %zu exceeds the LDS of the "
+                "path for head dims past %d", op, head_dim, length, tfd::kJeffTiledMaxHd);
   if (length > (size_t)INT32_MAX / 4 || width > (size_t)INT32_MAX / 4)
     return fail(c, TFD_EUNSUPPORTED, "%s: length/width too large for the kernels", op);
   if (heads > 65535 || rows > 65535)
@@ -491,6 +506,16 @@ int jeff_run(tfd_ctx *c, const char *op, bool bf16, size_t rows, size_t length, 
     if ((rc = rope_table(c, 1, length, rotary_dim, bits_to_f32(theta_bits), theta_bits, &a.cos_t,
                          &a.sin_t)))
       return rc;
+  }
+  if (!hd_pad) {
+    if ((rc = reserve(c, c->kp, tfd::jeff_generic_kn_bytes(a, (int)rows)))) return rc;
+    tfd::KernelEvents ev;
+    if ((rc = timing_events(c, &ev))) return rc;
+    TFD_HIP(c,
+            tfd::launch_jeff_generic(a, (int)rows, bf16, static_cast<float *>(c->kp.ptr),
+                                     c->stream, ev),
+            "jeff_generic launch");
+    return finish(c, flags, out, out_d, sizeof(float) * qn);
   }
   if ((rc = reserve(c, c->kp, tfd::jeff_kp_bytes(a, (int)rows, hd_pad, bf16)))) return rc;
   tfd::KernelEvents ev;

@@ -114,6 +114,20 @@ size_t jeff_bf16_flags_offset(const JeffArgs &a, int rows);
 hipError_t launch_jeff_bf16_wide(const JeffArgs &a, int rows, const uint16_t *kp, int *flags,
                                  hipStream_t stream);
 
+// Head dims past the tiled kernels (Laya hd > 128, Jeff hd > 256): one
+// wavefront per query in the reference's scalar order. Laya reads `keep`
+// (kMaskBits) or a.valid + a.window (kMaskStruct) directly; Jeff prepares
+// the keys into `kn` (jeff_generic_kn_bytes) first.
+constexpr int kLayaTiledMaxHd = 128;
+constexpr int kJeffTiledMaxHd = 256;
+hipError_t launch_laya_generic(const LayaArgs &a, const uint8_t *keep, int heads, int batch,
+                               int mode, hipStream_t stream);
+inline size_t jeff_generic_kn_bytes(const JeffArgs &a, int rows) {
+  return (size_t)rows * a.kv_heads * a.L * a.hd * sizeof(float);
+}
+hipError_t launch_jeff_generic(const JeffArgs &a, int rows, bool bf16, float *kn,
+                               hipStream_t stream, const KernelEvents &ev);
+
 // ------------------------------------------------ no-allocation entry
 
 // Bytes of the static device scratch of tfd_laya_attention_block_noalloc_f32

@@ -681,3 +681,65 @@ def test_jeff_c5_full_bf16_matches_f32_gpu(gpu_ctx, c5_full):
     ref = te.jeff_full_attention_rows(*vals, *rest, *args, ctx=gpu_ctx)
     err = assert_close(got.cpu().numpy(), ref.cpu().numpy(), BF16_TOL)
     print(f"C5 full bf16 vs f32 max abs error {err:.3e}")
+
+
+# ------------------------------------------------------------------ head dims past the tiles
+
+@pytest.mark.parametrize("hd,heads,length,batch", [(160, 2, 40, 2), (256, 1, 70, 1), (129, 2, 33, 2),
+                                                    (512, 2, 20, 1)])
+def test_laya_wide_head_dims_match_oracle(gpu_ctx, hd, heads, length, batch):
+    """Head dims past 128 (the reference computes any head dim,
+    cpu-kernels lib.rs:843-1156): global and windowed masks with padded and
+    sparse rows, RoPE on and off, both entries, against the oracle."""
+    d = heads * hd
+    rng = Lcg(5000 + hd + length)
+    qkv = (rng.uniform(3 * d * length * batch) * 2.0 - 1.0).astype(np.float32)
+    for sparse in (False, True):
+        valid = encoder_valid(length, batch, sparse)
+        for window, base in ((-1, 160000.0), (4, 10000.0), (-1, 0.0)):
+            keep = oracle.laya_build_mask(valid, length, batch, window)
+            want = oracle.laya_attention_block(qkv, keep, d, heads, length, batch, base)
+            got = laya_gpu(gpu_ctx, qkv, keep, d, heads, length, batch, base)
+            assert_close(got, want, F32_TOL)
+            st = te.laya_attention_structured(qkv, valid, d, heads, length, batch, window, base,
+                                              ctx=gpu_ctx)
+            assert_close(st, want, F32_TOL)
+
+
+@pytest.mark.parametrize("hd,heads,kv_heads,rot,length", [(320, 4, 2, 64, 50), (512, 2, 1, 0, 33),
+                                                          (288, 3, 3, 288, 17)])
+def test_jeff_wide_head_dims_match_oracle(gpu_ctx, hd, heads, kv_heads, rot, length):
+    """Head dims past 256 (jeff_full_attention_into takes any head dim,
+    lib.rs:609-763): rows with left padding and holes, GQA, trim on and off,
+    f32 and bf16, against the oracle."""
+    rows = 2
+    rng = Lcg(7000 + hd + length)
+    W, KW = heads * hd, kv_heads * hd
+    q = rng.normal(rows * length * W).astype(np.float32)
+    g = rng.normal(rows * length * W).astype(np.float32)
+    k = rng.normal(rows * length * KW).astype(np.float32)
+    v = rng.normal(rows * length * KW).astype(np.float32)
+    qn = (rng.normal(hd) * 0.1).astype(np.float32)
+    kn = (rng.normal(hd) * 0.1).astype(np.float32)
+    mask = np.ones(rows * length, np.float32)
+    mask[length:length + length // 3] = 0.0
+    mask[length // 2] = 0.0
+    for trim in (False, True):
+        want = oracle.jeff_rows(q, k, v, g, qn, kn, mask, rows, length, heads, kv_heads, hd, rot,
+                                1e7, 1e-6, trim_leading=trim)
+        got = te.jeff_full_attention_rows(q, k, v, g, qn, kn, mask, rows, length, heads, kv_heads,
+                                          hd, rot, 1e7, 1e-6, trim_leading=trim, ctx=gpu_ctx)
+        assert_close(got, want, F32_TOL)
+    bits = [te.to_bf16_bits(x) for x in (q, k, v, g)]
+    vals = [te.bf16_bits_to_f32(b) for b in bits]
+    want = oracle.jeff_rows(*vals, qn, kn, mask, rows, length, heads, kv_heads, hd, rot, 1e7, 1e-6)
+    got = te.jeff_full_attention_rows(*bits, qn, kn, mask, rows, length, heads, kv_heads, hd, rot,
+                                      1e7, 1e-6, bf16=True, ctx=gpu_ctx)
+    assert_close(got, want, BF16_TOL)
+    if kv_heads == heads:  # the drop-in, one row
+        q0, k0, v0, g0 = (x[: length * W] for x in (q, k, v, g))
+        want = oracle.jeff_full_attention(q0, k0, v0, g0, qn, kn, mask[:length], length, heads, hd,
+                                          rot, 1e7, 1e-6)
+        got = te.jeff_full_attention(q0, k0, v0, g0, qn, kn, mask[:length], heads, hd, rot, 1e7,
+                                     1e-6, q_shape=(length, W), ctx=gpu_ctx)
+        assert_close(got, want, F32_TOL)
