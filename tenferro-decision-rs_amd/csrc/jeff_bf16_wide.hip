@@ -37,7 +37,7 @@ namespace {
 constexpr int kWideHd = 256;     // head dim (fixed)
 constexpr int kWideKeys = 32;    // keys per tile
 constexpr int kWideWaves = 4;    // wavefronts per workgroup
-constexpr int kWideBlocks = 2;   // 32-query blocks per wavefront
+constexpr int kWideBlocks = 1;   // 32-query blocks per wavefront
 constexpr int kWideQueries = 32 * kWideBlocks;  // queries per wavefront
 // Staged tiles, 16-byte chunks (8 bf16): K as 2 blocks of 16 keys x 32
 // chunks, V as 16 blocks of 16 features x 4 chunks, each block chunk-major
