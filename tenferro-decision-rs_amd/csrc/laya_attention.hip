@@ -131,6 +131,35 @@ __global__ __launch_bounds__(256) void laya_keep_bits_kernel(const uint8_t *__re
     any[((size_t)b * ((L + 63) / 64) + q / 64) * laya_map_row(nkt) + kt] = some;
 }
 
+// The tile map of the structured mask (valid (L, B) + window, laya-infer
+// model.rs:465-490), in laya_keep_bits_kernel's layout, for the placement
+// plan: flag (b, g, kt) is 1 when some query of 64-query group g keeps a key
+// of tile kt. A valid query keeps the valid keys within the window (all
+// valid keys without one), a padded query every valid key; so a group with
+// a padded query, or any group without a window, keeps every tile holding a
+// valid key, and otherwise the tiles holding a valid key within the window
+// of the group's first or last query. One thread per flag.
+__global__ __launch_bounds__(256) void laya_valid_map_kernel(const uint8_t *__restrict__ valid,
+                                                             uint8_t *__restrict__ any, int L,
+                                                             int B, int nkt, int window) {
+  const int ng = (L + 63) / 64;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= B * ng * nkt) return;
+  const int kt = i % nkt, g = (i / nkt) % ng, b = i / (nkt * ng);
+  const uint8_t *vb = valid + (size_t)b * L;
+  const int q0 = 64 * g, q1 = min(q0 + 63, L - 1);
+  bool padded = false;
+  for (int q = q0; q <= q1; ++q) padded |= vb[q] == 0;
+  int k0 = kt * kKeyTile, k1 = min(k0 + kKeyTile - 1, L - 1);
+  if (window >= 0 && !padded) {
+    k0 = max(k0, q0 - window);
+    k1 = min(k1, q1 + window);
+  }
+  bool some = false;
+  for (int k = k0; k <= k1; ++k) some |= vb[k] != 0;
+  any[((size_t)b * ng + g) * laya_map_row(nkt) + kt] = some;
+}
+
 // ------------------------------------------------------------------ helpers
 
 // Element dd of the head's RoPE-rotated row (lib.rs:991-1010): pairs
@@ -430,8 +459,9 @@ __global__ __launch_bounds__(256, laya_groups_per_cu(HDP)) void laya_attention_k
   // to CU slot p % (CUs): when the counts allow it (laya_xcd_layout), each
   // XCD gets an equal share of every batch row (consecutive (head, block)
   // items, so a head's keys and values are read by at most two XCDs). The
-  // keep-bits kernel's plan, when given, also balances the key tiles per CU
-  // and carries the item's key span; otherwise the workgroups of a CU come
+  // placement plan, when a tile map is given (laya_keep_bits_kernel's, or
+  // laya_valid_map_kernel's for the structured mask), also balances the key
+  // tiles per CU and carries the item's key span; otherwise the workgroups of a CU come
   // from different rows (r, r + 3, r + 6). Beyond one dispatch round,
   // workgroups start where others end and the grid order is the better
   // schedule.
@@ -439,7 +469,7 @@ __global__ __launch_bounds__(256, laya_groups_per_cu(HDP)) void laya_attention_k
   int kt_begin = 0, kt_end = 0;
   const int nqb = gridDim.x, H = gridDim.y, B = gridDim.z;
   const bool xcd = laya_xcd_layout(nqb, H, B, laya_groups_per_cu(HDP), a.cus);
-  const bool planned = MODE == kMaskBits && xcd && nqb * B <= kLayaPlanMax;
+  const bool planned = a.any != nullptr && xcd && nqb * B <= kLayaPlanMax;
   {
     const int p = blockIdx.x + nqb * (blockIdx.y + H * blockIdx.z);
     if (planned) {
@@ -869,6 +899,14 @@ hipError_t launch_laya_keep_bits(const uint8_t *keep, uint32_t *bits, uint8_t *a
                                  int nkt, hipStream_t stream) {
   dim3 grid((L + 255) / 256, nkt, B);
   hipLaunchKernelGGL(laya_keep_bits_kernel, grid, dim3(256), 0, stream, keep, bits, any, L, nkt);
+  return hipGetLastError();
+}
+
+hipError_t launch_laya_valid_map(const uint8_t *valid, uint8_t *any, int L, int B, int nkt,
+                                 int window, hipStream_t stream) {
+  const long n = (long)B * ((L + 63) / 64) * nkt;
+  hipLaunchKernelGGL(laya_valid_map_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     stream, valid, any, L, B, nkt, window);
   return hipGetLastError();
 }
 

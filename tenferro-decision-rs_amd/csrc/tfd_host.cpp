@@ -430,6 +430,17 @@ int laya_run(tfd_ctx *c, const char *op, const float *qkv, const uint8_t *keep,
             "laya_keep_bits launch");
   } else {
     a.valid = static_cast<const uint8_t *>(mask_d);
+    if (!noalloc && tfd::laya_planned(a.L, (int)heads, (int)batch, hd_pad, c->cus)) {
+      // The tile map of valid + window feeds the placement plan.
+      const size_t groups = (size_t)tfd::laya_map_row(a.nkt) * batch * ((length + 63) / 64);
+      if ((rc = reserve(c, c->bits, groups))) return rc;
+      uint8_t *map = static_cast<uint8_t *>(c->bits.ptr);
+      a.any = map;
+      TFD_HIP(c,
+              tfd::launch_laya_valid_map(a.valid, map, a.L, (int)batch, a.nkt, a.window,
+                                         c->stream),
+              "laya_valid_map launch");
+    }
   }
   tfd::KernelEvents ev;
   if (!noalloc && (rc = timing_events(c, &ev))) return rc;

@@ -48,8 +48,9 @@ enum LayaMaskMode : int {
 struct LayaArgs {
   const float *qkv;      // (3d, L, B)
   const uint32_t *bits;  // kMaskBits: word (b*nkt + kt)*L + q, bit j = key 32*kt + j kept
-  const uint8_t *any;    // kMaskBits: byte (b*ceil(L/64) + q/64)*laya_map_row(nkt) + kt, tile
-                         // kt kept by any query of that 64-query group
+  const uint8_t *any;    // byte (b*ceil(L/64) + q/64)*laya_map_row(nkt) + kt: tile kt kept by
+                         // any query of that 64-query group (kMaskBits; optional in
+                         // kMaskStruct, where it only feeds the placement plan)
   const uint8_t *valid;  // kMaskStruct: (L, B)
   const uint8_t *qneed;  // kMaskStruct, or null: (L, B), a 64-query group with no
                          // non-zero entry is skipped (its output left unwritten)
@@ -95,6 +96,17 @@ hipError_t launch_fill_zero(float *out, size_t n, hipStream_t stream);
 hipError_t launch_add_row_bias(float *c, const float *b, int m, size_t n, hipStream_t stream);
 hipError_t launch_laya_keep_bits(const uint8_t *keep, uint32_t *bits, uint8_t *any, int L, int B,
                                  int nkt, hipStream_t stream);
+// The structured mask's tile map (valid (L, B) + window; window < 0: none)
+// in laya_keep_bits_kernel's `any` layout.
+hipError_t launch_laya_valid_map(const uint8_t *valid, uint8_t *any, int L, int B, int nkt,
+                                 int window, hipStream_t stream);
+// Whether a grid of (L, heads, batch) at padded head dim hd_pad gets the
+// placement plan from a tile map (one dispatch round, laya_xcd_layout).
+inline bool laya_planned(int L, int heads, int batch, int hd_pad, int cus) {
+  const int nqb = (L + kLayaGroupQueries - 1) / kLayaGroupQueries;
+  return laya_xcd_layout(nqb, heads, batch, laya_groups_per_cu(hd_pad), cus) &&
+         nqb * batch <= kLayaPlanMax;
+}
 hipError_t launch_laya_attention(const LayaArgs &a, int heads, int batch, int hd_pad, int mode,
                                  hipStream_t stream, const KernelEvents &ev);
 // Jeff launchers run a K prep kernel into `kp` (workspace of

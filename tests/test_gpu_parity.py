@@ -257,8 +257,9 @@ def test_laya_planned_grids(gpu_ctx, batch, heads, hd, window):
     """Grids that fit one dispatch round follow a placement plan that each
     workgroup derives from the tile map (rows longest first over the CUs of
     each XCD). Ragged rows with an empty row and an interior hole; each shape
-    runs twice, after another planned shape. The drop-in (planned) must equal
-    the structured entry (never planned) bitwise, and the oracle within
+    runs twice, after another planned shape. The drop-in (plan from the keep
+    tensor's tile map) must equal the structured entry (plan from the tile
+    map of valid + window, the same map) bitwise, and the oracle within
     tolerance on the first shape."""
     import torch
 
