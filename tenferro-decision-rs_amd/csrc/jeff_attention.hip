@@ -1473,52 +1473,67 @@ struct JeffStageBf16 {
   }
 };
 
+// LDS bytes of the bf16 kernel's workgroup (two K/V tiles or the Q scratch).
+template <int HDP>
+__host__ __device__ constexpr int jeff_bf16_smem_bytes() {
+  constexpr int KT = 32, KSB = HDP + 8, VSB = KT + 8;
+  constexpr int TILE_BYTES = 2 * (KT * KSB + HDP * VSB) * 2;
+  constexpr int QSCR_BYTES = kWavesPerGroup * kJeffWaveQueries * (HDP + 1) * 4;
+  return TILE_BYTES > QSCR_BYTES ? TILE_BYTES : QSCR_BYTES;
+}
+
 // Same arithmetic as jeff_attention_f32_kernel with q, k, v and gate in bf16:
 // normalized/rotated q and k and the probabilities are rounded to bf16 for
 // v_mfma_f32_16x16x32_bf16; softmax, accumulation and output stay f32.
 // A 32-key tile is two 16-key S^T blocks (lane group g holds keys 4g + r and
 // 16 + 4g + r of its query), which together are exactly the B operand of one
 // P.V MFMA per 16-row block of O^T.
+// Whether jeff_bf16_wide_kernel flagged (non-finite values) a query tile of
+// redo_qt queries that unit (bx, by, bz) of the bf16 grid covers, for any
+// head of its group.
+__device__ __forceinline__ bool jeff_bf16_unit_flagged(const JeffArgs &a, const int *redo,
+                                                       int redo_qt, int bx, int by, int bz) {
+  const int hg = a.heads_per_group, QT = kJeffWaveQueries * (kWavesPerGroup / hg);
+  const int L = a.L, qa = bx * QT;
+  const int nqt = (L + redo_qt - 1) / redo_qt;
+  const int t_lo = qa / redo_qt, t_hi = (min(qa + QT, L) - 1) / redo_qt;
+  int any = 0;
+  for (int h = by * hg; h < by * hg + hg; ++h)
+    for (int t = t_lo; t <= t_hi; ++t) any |= redo[((size_t)bz * a.heads + h) * nqt + t];
+  return any != 0;
+}
+
+// One workgroup's unit (bx, by, bz) of the grid (query tile, head group,
+// row); smem_raw: jeff_bf16_smem_bytes() of LDS, s_span: two ints.
 template <int HDP, bool VEC>
-__global__ __launch_bounds__(256, 2) void jeff_attention_bf16_kernel(const JeffArgs a,
-                                                                     const uint16_t *__restrict__ kp,
-                                                                     const int *__restrict__ redo,
-                                                                     int redo_qt) {
+__device__ __forceinline__ void jeff_bf16_unit(const JeffArgs &a, const uint16_t *__restrict__ kp,
+                                               const int bx, const int by, const int bz,
+                                               unsigned char *smem_raw, int *s_span) {
   constexpr int KT = 32;
   constexpr int QS8 = HDP / 32;  // bf16x8 B operands of Q per lane
   constexpr int NB = HDP / 16;   // 16-row blocks of O^T
   constexpr int KSB = HDP + 8, VSB = KT + 8;
   constexpr int KBUF = KT * KSB, VBUF = HDP * VSB;  // uint16 elements
   constexpr int QP = HDP + 1;
-  constexpr int TILE_BYTES = 2 * (KBUF + VBUF) * 2;
-  constexpr int QSCR_BYTES = kWavesPerGroup * kJeffWaveQueries * QP * 4;
-  constexpr int SMEM = TILE_BYTES > QSCR_BYTES ? TILE_BYTES : QSCR_BYTES;
-  __shared__ __attribute__((aligned(16))) unsigned char smem_raw[SMEM];
   uint16_t *const lds16 = reinterpret_cast<uint16_t *>(smem_raw);
   float *const qscr = reinterpret_cast<float *>(smem_raw);
-  __shared__ int s_span[2];
 
-  const int tid = threadIdx.x, lane = tid & 63;
+  // The thread index goes through an opaque move: the exact pass runs units
+  // in a loop, and what is derived from the index stays inside the unit
+  // instead of being hoisted (and held live) across the whole loop.
+  int tid;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(tid) : "v"((int)threadIdx.x));
+  const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform, in a scalar register
   const int col = lane & 15, grp = lane >> 4;
   const int hg = a.heads_per_group, qsubs = kWavesPerGroup / hg;
-  const int row = blockIdx.z;
-  const int head = blockIdx.y * hg + wave % hg;
+  const int row = bz;
+  const int head = by * hg + wave % hg;
   const int kvh = min(head / a.groups, a.kv_heads - 1);
   const int L = a.L, hd = a.hd, rh = a.rot_half;
   const int QT = kJeffWaveQueries * qsubs;
-  const int qa = blockIdx.x * QT;
+  const int qa = bx * QT;
   const int q = qa + (wave / hg) * kJeffWaveQueries + col;
-  if (redo != nullptr) {
-    // Exact pass after jeff_bf16_wide_kernel: only the (head, query tile of
-    // redo_qt) units it flagged, for every query of this workgroup.
-    const int nqt = (L + redo_qt - 1) / redo_qt;
-    const int t_lo = qa / redo_qt, t_hi = (min(qa + QT, L) - 1) / redo_qt;
-    int any = 0;
-    for (int h = blockIdx.y * hg; h < blockIdx.y * hg + hg; ++h)
-      for (int t = t_lo; t <= t_hi; ++t) any |= redo[((size_t)row * a.heads + h) * nqt + t];
-    if (any == 0) return;  // uniform over the workgroup
-  }
   const bool qin = q < L;
   const float *maskr = a.mask + (size_t)row * L;
   const uint16_t *Q = static_cast<const uint16_t *>(a.q) + row * a.q_row + (size_t)head * hd * L;
@@ -1753,6 +1768,45 @@ __global__ __launch_bounds__(256, 2) void jeff_attention_bf16_kernel(const JeffA
   }
 }
 
+template <int HDP, bool VEC>
+__global__ __launch_bounds__(256, 2) void jeff_attention_bf16_kernel(const JeffArgs a,
+                                                                     const uint16_t *__restrict__ kp) {
+  __shared__ __attribute__((aligned(16))) unsigned char smem_raw[jeff_bf16_smem_bytes<HDP>()];
+  __shared__ int s_span[2];
+  jeff_bf16_unit<HDP, VEC>(a, kp, blockIdx.x, blockIdx.y, blockIdx.z, smem_raw, s_span);
+}
+
+// The exact pass after jeff_bf16_wide_kernel: the same units over a grid of
+// gx x gy x gz, each run only where the wide kernel flagged one of its
+// query tiles. A resident grid of workgroups walks the units (workgroup p
+// takes p, p + gridDim.x, ...; the flags of up to 64 of them read in one
+// round trip), so a call with nothing flagged costs one dispatch round of
+// flag reads rather than a full grid of workgroups.
+template <int HDP, bool VEC>
+__global__ __launch_bounds__(256, 2) void jeff_bf16_exact_kernel(const JeffArgs a,
+                                                                 const uint16_t *__restrict__ kp,
+                                                                 const int *__restrict__ redo,
+                                                                 int redo_qt, int gx, int gy,
+                                                                 int gz) {
+  __shared__ __attribute__((aligned(16))) unsigned char smem_raw[jeff_bf16_smem_bytes<HDP>()];
+  __shared__ int s_span[2];
+  const int n = gx * gy * gz, lane = threadIdx.x & 63, stride = gridDim.x;
+  for (int v0 = blockIdx.x; v0 < n; v0 += 64 * stride) {
+    // Lane k reads the flags of unit v0 + k*stride, all at once; every wave
+    // gets the same ballot, so the loop below is uniform over the workgroup.
+    const int v = v0 + lane * stride;
+    const bool f = v < n && jeff_bf16_unit_flagged(a, redo, redo_qt, v % gx, (v / gx) % gy,
+                                                   v / (gx * gy));
+    uint64_t m = __ballot(f);
+    while (m != 0) {
+      const int u = v0 + (int)__builtin_ctzll(m) * stride;
+      m &= m - 1;
+      __syncthreads();  // the previous unit is done with the LDS
+      jeff_bf16_unit<HDP, VEC>(a, kp, u % gx, (u / gx) % gy, u / (gx * gy), smem_raw, s_span);
+    }
+  }
+}
+
 // ----------------------------------------------------------------- launchers
 
 // Workspace: the prepared keys (per row and kv head, keys rounded up to 16
@@ -1847,28 +1901,39 @@ static hipError_t launch_jeff_bf16_hd(const JeffArgs &a, int rows, uint16_t *kp,
                         nullptr, 0, a, kp);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  // Head dim 256: the 32x32x16 kernel, then this one as the exact pass over
-  // the query tiles it flagged (non-finite values).
-  const int *redo = nullptr;
-  int redo_qt = 0;
-  if (HDP == 256 && jeff_bf16_wide_fits(a)) {
-    int *flags = reinterpret_cast<int *>(reinterpret_cast<char *>(kp) + jeff_bf16_flags_offset(a, rows));
-    e = launch_jeff_bf16_wide(a, rows, kp, flags, stream);
-    if (e != hipSuccess) return e;
-    redo = flags;
-    redo_qt = jeff_bf16_wide_query_tile(a);
-  }
   const int qsubs = kWavesPerGroup / a.heads_per_group;
   const int qt = kJeffWaveQueries * qsubs;
   dim3 grid((a.L + qt - 1) / qt, a.heads / a.heads_per_group, rows);
   // 16-byte V loads along tokens need L % 8 == 0 and an aligned base.
   const bool vec = a.L % 8 == 0 && (reinterpret_cast<uintptr_t>(a.v) & 15) == 0;
+  if constexpr (HDP == 256) {
+    // The 32x32x16 kernel, then the exact pass over the query tiles it
+    // flagged (non-finite values) on a resident grid (two workgroups per CU).
+    if (jeff_bf16_wide_fits(a)) {
+      int *flags = reinterpret_cast<int *>(reinterpret_cast<char *>(kp) + jeff_bf16_flags_offset(a, rows));
+      e = launch_jeff_bf16_wide(a, rows, kp, flags, stream);
+      if (e != hipSuccess) return e;
+      const int redo_qt = jeff_bf16_wide_query_tile(a);
+      const long units = (long)grid.x * grid.y * grid.z;
+      const long slots = 2L * (a.cus > 0 ? a.cus : 1);
+      const dim3 egrid((unsigned)(units < slots ? units : slots));
+      if (vec)
+        hipExtLaunchKernelGGL((jeff_bf16_exact_kernel<HDP, true>), egrid, dim3(256), 0, stream,
+                              nullptr, ev.stop, 0, a, kp, flags, redo_qt, (int)grid.x,
+                              (int)grid.y, (int)grid.z);
+      else
+        hipExtLaunchKernelGGL((jeff_bf16_exact_kernel<HDP, false>), egrid, dim3(256), 0, stream,
+                              nullptr, ev.stop, 0, a, kp, flags, redo_qt, (int)grid.x,
+                              (int)grid.y, (int)grid.z);
+      return hipGetLastError();
+    }
+  }
   if (vec)
     hipExtLaunchKernelGGL((jeff_attention_bf16_kernel<HDP, true>), grid, dim3(256), 0, stream,
-                          nullptr, ev.stop, 0, a, kp, redo, redo_qt);
+                          nullptr, ev.stop, 0, a, kp);
   else
     hipExtLaunchKernelGGL((jeff_attention_bf16_kernel<HDP, false>), grid, dim3(256), 0, stream,
-                          nullptr, ev.stop, 0, a, kp, redo, redo_qt);
+                          nullptr, ev.stop, 0, a, kp);
   return hipGetLastError();
 }
 
