@@ -131,26 +131,37 @@ __global__ __launch_bounds__(256) void laya_keep_bits_kernel(const uint8_t *__re
     any[((size_t)b * ((L + 63) / 64) + q / 64) * laya_map_row(nkt) + kt] = some;
 }
 
-// The tile map of the structured mask (valid (L, B) + window, laya-infer
-// model.rs:465-490), in laya_keep_bits_kernel's layout, for the placement
-// plan: flag (b, g, kt) is 1 when some query of 64-query group g keeps a key
-// of tile kt. A valid query keeps the valid keys within the window (all
-// valid keys without one), a padded query every valid key; so a group with
-// a padded query, or any group without a window, keeps every tile holding a
-// valid key, and otherwise the tiles holding a valid key within the window
-// of the group's first or last query. One thread per flag.
-__global__ __launch_bounds__(256) void laya_valid_map_kernel(const uint8_t *__restrict__ valid,
-                                                             uint8_t *__restrict__ any, int L,
-                                                             int B, int nkt, int window) {
-  const int ng = (L + 63) / 64;
+// The structured mask (valid (L, B) + window, laya-infer model.rs:465-490)
+// in the attention kernel's terms: words[b*nkt + kt], bit j set when key
+// 32*kt + j is valid (the keys any query of row b may keep; the window is
+// applied per query in the kernel), and, when `any` is given, the tile map in
+// laya_keep_bits_kernel's layout for the placement plan: flag (b, g, kt) is 1
+// when some query of 64-query group g keeps a key of tile kt. A valid query
+// keeps the valid keys within the window (all valid keys without one), a
+// padded query every valid key; so a group with a padded query, or any group
+// without a window, keeps every tile holding a valid key, and otherwise the
+// tiles holding a valid key within the window of the group's first or last
+// query. One thread per (b, g, kt) (g = 0 only without a map).
+__global__ __launch_bounds__(256) void laya_valid_prep_kernel(const uint8_t *__restrict__ valid,
+                                                              uint32_t *__restrict__ words,
+                                                              uint8_t *__restrict__ any, int L,
+                                                              int B, int nkt, int window) {
+  const int ng = any != nullptr ? (L + 63) / 64 : 1;
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= B * ng * nkt) return;
   const int kt = i % nkt, g = (i / nkt) % ng, b = i / (nkt * ng);
   const uint8_t *vb = valid + (size_t)b * L;
+  const int t0 = kt * kKeyTile, t1 = min(t0 + kKeyTile - 1, L - 1);
+  if (g == 0) {
+    uint32_t w = 0u;
+    for (int k = t0; k <= t1; ++k) w |= (uint32_t)(vb[k] != 0) << (k - t0);
+    words[(size_t)b * nkt + kt] = w;
+  }
+  if (any == nullptr) return;
   const int q0 = 64 * g, q1 = min(q0 + 63, L - 1);
   bool padded = false;
   for (int q = q0; q <= q1; ++q) padded |= vb[q] == 0;
-  int k0 = kt * kKeyTile, k1 = min(k0 + kKeyTile - 1, L - 1);
+  int k0 = t0, k1 = t1;
   if (window >= 0 && !padded) {
     k0 = max(k0, q0 - window);
     k1 = min(k1, q1 + window);
@@ -438,7 +449,7 @@ __device__ __noinline__ void laya_redo_wave(const LayaArgs *ap, int b, int head,
 // ALU share the SIMD (they never run at the same time), so the walk keeps its
 // vector work per tile small and relies on other waves to cover memory and
 // barrier waits.
-template <int HDP, int MODE, bool VEC, bool ROPE>
+template <int HDP, int MODE, bool VEC, bool ROPE, bool VW>
 __global__ __launch_bounds__(256, laya_groups_per_cu(HDP)) void laya_attention_kernel(
     const LayaArgs a) {
   using Stage = LayaStage<HDP, VEC, ROPE>;
@@ -460,7 +471,7 @@ __global__ __launch_bounds__(256, laya_groups_per_cu(HDP)) void laya_attention_k
   // XCD gets an equal share of every batch row (consecutive (head, block)
   // items, so a head's keys and values are read by at most two XCDs). The
   // placement plan, when a tile map is given (laya_keep_bits_kernel's, or
-  // laya_valid_map_kernel's for the structured mask), also balances the key
+  // laya_valid_prep_kernel's for the structured mask), also balances the key
   // tiles per CU and carries the item's key span; otherwise the workgroups of a CU come
   // from different rows (r, r + 3, r + 6). Beyond one dispatch round,
   // workgroups start where others end and the grid order is the better
@@ -628,9 +639,13 @@ __global__ __launch_bounds__(256, laya_groups_per_cu(HDP)) void laya_attention_k
   // word or validity byte is fetched one tile ahead (mask_of) and turned
   // into the word (keep_word) only after that tile's barrier, so waiting on
   // it never stalls the tile prefetch issued beside it.
+  // kMaskStruct reads the rows' valid-key words (VW: the prep gave them,
+  // planned grids), else the validity bytes of the tile's keys.
+  constexpr bool vwords = MODE == kMaskStruct && VW;
   auto mask_of = [&](int kt) -> uint32_t {
     if (MODE == kMaskBits)
       return a.bits[((size_t)b * nkt + min(kt, nkt - 1)) * L + min(q, L - 1)];
+    if (vwords) return a.bits[(size_t)b * nkt + min(kt, nkt - 1)];  // uniform
     return a.valid[(size_t)b * L + min(kt * kKeyTile + (lane & 31), L - 1)];
   };
 
@@ -683,9 +698,8 @@ __global__ __launch_bounds__(256, laya_groups_per_cu(HDP)) void laya_attention_k
       w = qin ? x : 0u;
     } else {
       const int k0 = kt * kKeyTile;
-      const int key = k0 + (lane & 31);
-      const bool kv = key < L && x != 0;
-      const uint32_t vbits = (uint32_t)__ballot(kv);  // lanes 0..31 = keys of the tile
+      // The tile's valid keys (lanes 0..31 of the ballot = keys of the tile).
+      const uint32_t vbits = vwords ? x : (uint32_t)__ballot(k0 + (lane & 31) < L && x != 0);
       if (qin) {
         w = vbits;
         if (a.window >= 0 && q_valid) w &= range_bits(q - a.window - k0, q + a.window - k0);
@@ -902,11 +916,11 @@ hipError_t launch_laya_keep_bits(const uint8_t *keep, uint32_t *bits, uint8_t *a
   return hipGetLastError();
 }
 
-hipError_t launch_laya_valid_map(const uint8_t *valid, uint8_t *any, int L, int B, int nkt,
-                                 int window, hipStream_t stream) {
-  const long n = (long)B * ((L + 63) / 64) * nkt;
-  hipLaunchKernelGGL(laya_valid_map_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
-                     stream, valid, any, L, B, nkt, window);
+hipError_t launch_laya_valid_prep(const uint8_t *valid, uint32_t *words, uint8_t *any, int L,
+                                  int B, int nkt, int window, hipStream_t stream) {
+  const long n = (long)B * (any != nullptr ? (L + 63) / 64 : 1) * nkt;
+  hipLaunchKernelGGL(laya_valid_prep_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     stream, valid, words, any, L, B, nkt, window);
   return hipGetLastError();
 }
 
@@ -915,11 +929,14 @@ static hipError_t launch_laya_hd(const LayaArgs &a, int heads, int batch, int mo
                                  hipStream_t stream, const KernelEvents &ev) {
   dim3 grid((a.L + kLayaGroupQueries - 1) / kLayaGroupQueries, heads, batch);
   if (mode == kMaskBits)
-    hipExtLaunchKernelGGL((laya_attention_kernel<HDP, kMaskBits, VEC, ROPE>), grid, dim3(256), 0,
-                          stream, ev.start, ev.stop, 0, a);
+    hipExtLaunchKernelGGL((laya_attention_kernel<HDP, kMaskBits, VEC, ROPE, false>), grid,
+                          dim3(256), 0, stream, ev.start, ev.stop, 0, a);
+  else if (a.bits != nullptr)
+    hipExtLaunchKernelGGL((laya_attention_kernel<HDP, kMaskStruct, VEC, ROPE, true>), grid,
+                          dim3(256), 0, stream, ev.start, ev.stop, 0, a);
   else
-    hipExtLaunchKernelGGL((laya_attention_kernel<HDP, kMaskStruct, VEC, ROPE>), grid, dim3(256),
-                          0, stream, ev.start, ev.stop, 0, a);
+    hipExtLaunchKernelGGL((laya_attention_kernel<HDP, kMaskStruct, VEC, ROPE, false>), grid,
+                          dim3(256), 0, stream, ev.start, ev.stop, 0, a);
   return hipGetLastError();
 }
 

@@ -430,16 +430,26 @@ int laya_run(tfd_ctx *c, const char *op, const float *qkv, const uint8_t *keep,
             "laya_keep_bits launch");
   } else {
     a.valid = static_cast<const uint8_t *>(mask_d);
-    if (!noalloc && tfd::laya_planned(a.L, (int)heads, (int)batch, hd_pad, c->cus)) {
-      // The tile map of valid + window feeds the placement plan.
+    if (tfd::laya_planned(a.L, (int)heads, (int)batch, hd_pad, c->cus)) {
+      // A grid that gets the placement plan: the rows' valid-key words, then
+      // the tile map of valid + window.
+      const size_t words = (size_t)a.nkt * batch;
+      const size_t map_off = (sizeof(uint32_t) * words + 255) & ~(size_t)255;
       const size_t groups = (size_t)tfd::laya_map_row(a.nkt) * batch * ((length + 63) / 64);
-      if ((rc = reserve(c, c->bits, groups))) return rc;
-      uint8_t *map = static_cast<uint8_t *>(c->bits.ptr);
-      a.any = map;
+      uint8_t *base = nullptr;
+      if (noalloc) {
+        base = scratch + rope_bytes;
+      } else {
+        if ((rc = reserve(c, c->bits, map_off + groups))) return rc;
+        base = static_cast<uint8_t *>(c->bits.ptr);
+      }
+      a.bits = reinterpret_cast<const uint32_t *>(base);
+      a.any = base + map_off;
       TFD_HIP(c,
-              tfd::launch_laya_valid_map(a.valid, map, a.L, (int)batch, a.nkt, a.window,
-                                         c->stream),
-              "laya_valid_map launch");
+              tfd::launch_laya_valid_prep(a.valid, reinterpret_cast<uint32_t *>(base),
+                                          base + map_off, a.L, (int)batch, a.nkt, a.window,
+                                          c->stream),
+              "laya_valid_prep launch");
     }
   }
   tfd::KernelEvents ev;

@@ -47,7 +47,8 @@ enum LayaMaskMode : int {
 
 struct LayaArgs {
   const float *qkv;      // (3d, L, B)
-  const uint32_t *bits;  // kMaskBits: word (b*nkt + kt)*L + q, bit j = key 32*kt + j kept
+  const uint32_t *bits;  // kMaskBits: word (b*nkt + kt)*L + q, bit j = key 32*kt + j kept;
+                         // kMaskStruct (optional): word b*nkt + kt, bit j = key 32*kt + j valid
   const uint8_t *any;    // byte (b*ceil(L/64) + q/64)*laya_map_row(nkt) + kt: tile kt kept by
                          // any query of that 64-query group (kMaskBits; optional in
                          // kMaskStruct, where it only feeds the placement plan)
@@ -96,10 +97,11 @@ hipError_t launch_fill_zero(float *out, size_t n, hipStream_t stream);
 hipError_t launch_add_row_bias(float *c, const float *b, int m, size_t n, hipStream_t stream);
 hipError_t launch_laya_keep_bits(const uint8_t *keep, uint32_t *bits, uint8_t *any, int L, int B,
                                  int nkt, hipStream_t stream);
-// The structured mask's tile map (valid (L, B) + window; window < 0: none)
+// The structured mask's valid-key words (LayaArgs::bits, kMaskStruct) and,
+// when `any` is given, its tile map (valid (L, B) + window; window < 0: none)
 // in laya_keep_bits_kernel's `any` layout.
-hipError_t launch_laya_valid_map(const uint8_t *valid, uint8_t *any, int L, int B, int nkt,
-                                 int window, hipStream_t stream);
+hipError_t launch_laya_valid_prep(const uint8_t *valid, uint32_t *words, uint8_t *any, int L,
+                                  int B, int nkt, int window, hipStream_t stream);
 // Whether a grid of (L, heads, batch) at padded head dim hd_pad gets the
 // placement plan from a tile map (one dispatch round, laya_xcd_layout).
 inline bool laya_planned(int L, int heads, int batch, int hd_pad, int cus) {
