@@ -603,15 +603,22 @@ def run_only(args):
         return {"only": name, "ms_per_step": round(ms, 5), "attention_kernel_ms": round(kern, 5),
                 "tflops": round((att + gemm) / (ms * 1e-3) / 1e12, 3)}
     cfg = int(args.only[1])
+    structured = args.only.endswith("s")
     if cfg in (2, 3):
-        w = laya_config(cfg)
+        w = laya_config(cfg, with_keep=not structured)
         flops = 4 * w.head_dim * w.kept_pairs() * w.heads
         qkv = torch.from_numpy(w.qkv).to(dev)
-        keep = torch.from_numpy(w.keep).to(dev)
         out = torch.empty(w.hidden * w.length * w.batch, dtype=torch.float32, device=dev)
-        shape = (3 * w.hidden, w.length, w.batch)
-        fn = lambda: te.laya_attention_block(qkv, keep, w.hidden, w.heads, w.rope_base,
-                                             qkv_shape=shape, ctx=ctx, out=out)
+        if structured:
+            valid = torch.from_numpy(w.valid).to(dev)
+            fn = lambda: te.laya_attention_structured(qkv, valid, w.hidden, w.heads, w.length,
+                                                      w.batch, w.window, w.rope_base, ctx=ctx,
+                                                      out=out)
+        else:
+            keep = torch.from_numpy(w.keep).to(dev)
+            shape = (3 * w.hidden, w.length, w.batch)
+            fn = lambda: te.laya_attention_block(qkv, keep, w.hidden, w.heads, w.rope_base,
+                                                 qkv_shape=shape, ctx=ctx, out=out)
     else:
         w = jeff_config(cfg)
         flops = 4 * w.head_dim * w.kept_pairs() * w.heads
@@ -625,7 +632,8 @@ def run_only(args):
                                                  bf16=w.bf16, ctx=ctx, out=out)
     ms, kern = time_gpu(fn, args.steps, args.warmup, ctx)
     ctx.close()
-    return {"only": f"C{cfg}", "ms_per_step": round(ms, 5), "kernel_ms": round(kern, 5),
+    return {"only": f"C{cfg}" + ("_structured" if structured else ""),
+            "ms_per_step": round(ms, 5), "kernel_ms": round(kern, 5),
             "kernel_tflops": round(flops / (kern * 1e-3) / 1e12, 3), "algorithmic_flops": flops}
 
 
@@ -658,7 +666,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="only the C2 headline")
-    ap.add_argument("--only", choices=["c2", "c3", "c4", "c5", "c2l", "c4l", "model", "copy"], default=None,
+    ap.add_argument("--only", choices=["c2", "c3", "c4", "c5", "c2s", "c3s", "c2l", "c4l", "model", "copy"], default=None,
                     help="profiling aid: run one configuration's op (steps + warmup calls), "
                          "print its timing line and skip everything else")
     args = ap.parse_args()

@@ -132,43 +132,49 @@ __global__ __launch_bounds__(256) void laya_keep_bits_kernel(const uint8_t *__re
 }
 
 // The structured mask (valid (L, B) + window, laya-infer model.rs:465-490)
-// in the attention kernel's terms: words[b*nkt + kt], bit j set when key
-// 32*kt + j is valid (the keys any query of row b may keep; the window is
-// applied per query in the kernel), and, when `any` is given, the tile map in
-// laya_keep_bits_kernel's layout for the placement plan: flag (b, g, kt) is 1
-// when some query of 64-query group g keeps a key of tile kt. A valid query
-// keeps the valid keys within the window (all valid keys without one), a
-// padded query every valid key; so a group with a padded query, or any group
-// without a window, keeps every tile holding a valid key, and otherwise the
-// tiles holding a valid key within the window of the group's first or last
-// query. One thread per (b, g, kt) (g = 0 only without a map).
-__global__ __launch_bounds__(256) void laya_valid_prep_kernel(const uint8_t *__restrict__ valid,
-                                                              uint32_t *__restrict__ words,
-                                                              uint8_t *__restrict__ any, int L,
-                                                              int B, int nkt, int window) {
-  const int ng = any != nullptr ? (L + 63) / 64 : 1;
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= B * ng * nkt) return;
-  const int kt = i % nkt, g = (i / nkt) % ng, b = i / (nkt * ng);
+// in the attention kernel's terms, for a grid that gets the placement plan:
+// words[b*nkt + kt], bit j set when key 32*kt + j is valid (the keys any
+// query of row b may keep; the kernel applies the window per query), and the
+// tile map in laya_keep_bits_kernel's layout: flag (b, g, kt) is 1 when some
+// query of 64-query group g keeps a key of tile kt. A valid query keeps the
+// valid keys within the window (all valid keys without one), a padded query
+// every valid key; so a group with a padded query, or any group without a
+// window, keeps every tile holding a valid key, and otherwise the tiles
+// holding a valid key within the window of the group's first or last query.
+// One wave per (row b, group g): lane l reads query 64g + l, then the row's
+// keys 64 at a time (all loads independent); the g == 0 wave also writes the
+// row's words.
+__global__ __launch_bounds__(64) void laya_valid_prep_kernel(const uint8_t *__restrict__ valid,
+                                                             uint32_t *__restrict__ words,
+                                                             uint8_t *__restrict__ any, int L,
+                                                             int nkt, int window) {
+  const int ng = (L + 63) / 64, g = blockIdx.x, b = blockIdx.y;
+  const int lane = threadIdx.x;
   const uint8_t *vb = valid + (size_t)b * L;
-  const int t0 = kt * kKeyTile, t1 = min(t0 + kKeyTile - 1, L - 1);
-  if (g == 0) {
-    uint32_t w = 0u;
-    for (int k = t0; k <= t1; ++k) w |= (uint32_t)(vb[k] != 0) << (k - t0);
-    words[(size_t)b * nkt + kt] = w;
-  }
-  if (any == nullptr) return;
   const int q0 = 64 * g, q1 = min(q0 + 63, L - 1);
-  bool padded = false;
-  for (int q = q0; q <= q1; ++q) padded |= vb[q] == 0;
-  int k0 = t0, k1 = t1;
+  const bool padded = __ballot(q0 + lane < L && vb[min(q0 + lane, L - 1)] == 0) != 0;
+  int lo = 0, hi = L - 1;  // keys some query of the group may keep
   if (window >= 0 && !padded) {
-    k0 = max(k0, q0 - window);
-    k1 = min(k1, q1 + window);
+    lo = max(0, q0 - window);
+    hi = min(L - 1, q1 + window);
   }
-  bool some = false;
-  for (int k = k0; k <= k1; ++k) some |= vb[k] != 0;
-  any[((size_t)b * ng + g) * laya_map_row(nkt) + kt] = some;
+  uint8_t *row = any + ((size_t)b * ng + g) * laya_map_row(nkt);
+  for (int c0 = 0; c0 < ng; c0 += 8) {
+    uint8_t x[8];  // eight 64-key chunks in flight at once
+#pragma unroll
+    for (int u = 0; u < 8; ++u) x[u] = vb[min(64 * (c0 + u) + lane, L - 1)];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int c = c0 + u, k = 64 * c + lane;
+      const bool v = k < L && x[u] != 0;
+      const uint64_t kept = __ballot(v && k >= lo && k <= hi);
+      const uint64_t vm = __ballot(v);
+      if (lane < 2 && 2 * c + lane < nkt) {  // lane t: tile 2c + t (bits 32t .. 32t + 31)
+        row[2 * c + lane] = (uint32_t)(kept >> (32 * lane)) != 0u;
+        if (g == 0) words[(size_t)b * nkt + 2 * c + lane] = (uint32_t)(vm >> (32 * lane));
+      }
+    }
+  }
 }
 
 // ------------------------------------------------------------------ helpers
@@ -918,9 +924,8 @@ hipError_t launch_laya_keep_bits(const uint8_t *keep, uint32_t *bits, uint8_t *a
 
 hipError_t launch_laya_valid_prep(const uint8_t *valid, uint32_t *words, uint8_t *any, int L,
                                   int B, int nkt, int window, hipStream_t stream) {
-  const long n = (long)B * (any != nullptr ? (L + 63) / 64 : 1) * nkt;
-  hipLaunchKernelGGL(laya_valid_prep_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
-                     stream, valid, words, any, L, B, nkt, window);
+  hipLaunchKernelGGL(laya_valid_prep_kernel, dim3((unsigned)((L + 63) / 64), (unsigned)B),
+                     dim3(64), 0, stream, valid, words, any, L, nkt, window);
   return hipGetLastError();
 }
 
