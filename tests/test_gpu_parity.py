@@ -294,6 +294,53 @@ def test_laya_planned_grids(gpu_ctx, batch, heads, hd, window):
         assert_close(got.cpu().numpy(), want, F32_TOL)
 
 
+def _laya_planned(L, heads, batch, hd_pad, cus=256):
+    """Mirror of laya_planned (tfd_internal.hpp) for MI355X's 256 CUs."""
+    nqb = (L + 63) // 64
+    gpc = 4 if hd_pad <= 64 else 2
+    xcd = (nqb * heads * batch <= gpc * cus and (heads * nqb) % 8 == 0 and 32 % batch == 0
+           and ((heads * nqb) // 8) % (32 // batch) == 0)
+    return xcd and nqb * batch <= 1024
+
+
+# (L, batch, heads, hd, window): one-round grids (so both entries get the
+# placement plan) whose length leaves a partial last 64-query group and a
+# partial last key tile.
+RAGGED_PLANNED = [(200, 32, 2, 64, -1), (200, 32, 2, 64, 16), (72, 32, 4, 32, 8)]
+
+
+@pytest.mark.parametrize("L,batch,heads,hd,window", RAGGED_PLANNED)
+def test_laya_planned_ragged_lengths(gpu_ctx, L, batch, heads, hd, window):
+    """The structured entry's prep pass (valid-key words and the tile map of
+    valid + window) at lengths that are not multiples of 32 or 64: ragged rows
+    with an empty row, a row of one token, an interior hole and padded queries
+    inside windows; against the oracle, and the keep entry bitwise."""
+    import torch
+
+    assert _laya_planned(L, heads, batch, hd)
+    d = heads * hd
+    rng = Lcg(1200 + L + window)
+    valid = np.zeros(L * batch, np.uint8)
+    for b in range(batch):
+        n = {0: L, 1: 0, 2: 1}.get(b, int(rng.uniform(1)[0] * L))
+        valid[b * L:b * L + n] = 1
+    valid[L // 2] = 0  # a hole in row 0
+    qkv = (rng.uniform(3 * d * L * batch) * 2.0 - 1.0).astype(np.float32)
+    keep = oracle.laya_build_mask(valid, L, batch, window)
+    base = 10000.0
+    dev = torch.device("cuda:0")
+    tq = torch.from_numpy(qkv).to(dev)
+    st = te.laya_attention_structured(tq, torch.from_numpy(valid).to(dev), d, heads, L, batch,
+                                      window, base, ctx=gpu_ctx)
+    got = te.laya_attention_block(tq, torch.from_numpy(keep).to(dev), d, heads, base,
+                                  qkv_shape=(3 * d, L, batch), ctx=gpu_ctx)
+    assert torch.equal(torch.isnan(got), torch.isnan(st))
+    assert torch.equal(got.view(torch.int32), st.view(torch.int32))
+    want = oracle.laya_attention_block(qkv, keep, d, heads, L, batch, base)
+    err = assert_close(st.cpu().numpy(), want, F32_TOL)
+    print(f"L {L} B {batch} H {heads} hd {hd} window {window}: max abs error {err:.3e}")
+
+
 # ------------------------------------------------------------------ Jeff
 
 def jeff_case(seed, length, heads, hd, kv_heads, holes):
