@@ -55,11 +55,27 @@ __device__ __forceinline__ f32x16 mfma_32x32x16_bf16(bf16x8 a, bf16x8 b, f32x16 
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-// 16 bytes from global memory into LDS: lane i of the wavefront writes
-// lds_base + 16*i (lds_base must be the same for the whole wavefront).
-__device__ __forceinline__ void load_lds16(const void *src, unsigned char *lds_base) {
-  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds_base, 16,
-                                   0, 0);
+// 16 bytes at byte voff + soff of buffer r into LDS: lane i of the wavefront
+// writes lds_base + 16*i (lds_base and soff the same for the whole
+// wavefront). The buffer form keeps the per-lane address in one 32-bit
+// register (the global form needs a 64-bit address per load, which the
+// compiler ends up spilling, and every reload's wait would then also wait
+// for the loads to LDS issued before it).
+__device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
+                                           unsigned char *lds_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds_base,
+                                           16, (int)voff, (int)soff, 0, 0);
+}
+
+// This lane's index, recomputed where it is used (two vector instructions,
+// opaque to the compiler): the walk needs it only for the mask and the last
+// tile's clamped addresses, and a lane index kept live across the walk is
+// what the compiler spills first (its reload then waits on every load to
+// LDS issued before it).
+__device__ __forceinline__ int lane_now() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
 }
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
@@ -77,8 +93,10 @@ int wide_heads_per_group(const JeffArgs &a) {
 bool jeff_bf16_wide_fits(const JeffArgs &a) {
   const int G = a.kv_heads > 0 ? a.heads / a.kv_heads : 0;
   const bool rope_ok = a.cos_t == nullptr || a.rot_half == 16 || a.rot_half == 32;
+  // Buffer loads address one (row, kv head)'s K and V with 32-bit offsets.
+  const bool offsets_ok = (size_t)a.L * kWideHd * 2 < ((size_t)1 << 31);
   return a.hd == kWideHd && G >= 1 && a.heads == G * a.kv_heads && rope_ok && a.L >= 8 &&
-         a.L % 8 == 0 && (reinterpret_cast<uintptr_t>(a.v) & 15) == 0 &&
+         offsets_ok && a.L % 8 == 0 && (reinterpret_cast<uintptr_t>(a.v) & 15) == 0 &&
          (reinterpret_cast<uintptr_t>(a.q_norm) & 15) == 0;
 }
 
@@ -240,6 +258,10 @@ __global__ __launch_bounds__(256, kWideBlocks == 1 ? 2 : 1) void jeff_bf16_wide_
   const int si = lane & 15, sc = lane >> 4;  // row, chunk within an instruction
   const uint32_t klane = (uint32_t)(si * kWideHd * 2 + sc * 16);
   const uint32_t vlane = (uint32_t)(si * L * 2 + sc * 16);
+  // One (row, kv head)'s prepared K (L x 256) and V (256 x L), bf16 (each
+  // under 2 GiB: jeff_bf16_wide_fits).
+  const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(Kh, (uint32_t)((size_t)L * kWideHd * 2));
+  const __amdgpu_buffer_rsrc_t rv = buffer_rsrc(Vh, (uint32_t)((size_t)L * kWideHd * 2));
   auto stage = [&](int kt, int buf) {
     unsigned char *Kb = lds + buf * kStage;
     unsigned char *Vb = Kb + kKBuf;
@@ -248,27 +270,28 @@ __global__ __launch_bounds__(256, kWideBlocks == 1 ? 2 : 1) void jeff_bf16_wide_
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
         const int B = n >> 1, c0 = 8 * wave + 4 * (n & 1);
-        const char *base =
-            reinterpret_cast<const char *>(Kh) + ((size_t)(k0 + 16 * B) * kWideHd + 8 * c0) * 2;
-        load_lds16(base + klane, Kb + B * kKBlock + c0 * 256);
+        load_lds16(rk, klane, (uint32_t)(((k0 + 16 * B) * kWideHd + 8 * c0) * 2),
+                   Kb + B * kKBlock + c0 * 256);
       }
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
         const int B = 4 * wave + n;
-        const char *base = reinterpret_cast<const char *>(Vh) + ((size_t)16 * B * L + k0) * 2;
-        load_lds16(base + vlane, Vb + B * kVBlock);
+        load_lds16(rv, vlane, (uint32_t)((16 * B * L + k0) * 2), Vb + B * kVBlock);
       }
     } else {
+      const int ln = lane_now(), si = ln & 15, sc = ln >> 4;
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
         const int B = n >> 1, c0 = 8 * wave + 4 * (n & 1);
         const int key = min(k0 + 16 * B + si, L - 1);
-        load_lds16(Kh + (size_t)key * kWideHd + 8 * (c0 + sc), Kb + B * kKBlock + c0 * 256);
+        load_lds16(rk, (uint32_t)((key * kWideHd + 8 * (c0 + sc)) * 2), 0u,
+                   Kb + B * kKBlock + c0 * 256);
       }
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
         const int B = 4 * wave + n;
-        load_lds16(Vh + (size_t)(16 * B + si) * L + min(k0 + 8 * sc, L - 8), Vb + B * kVBlock);
+        load_lds16(rv, (uint32_t)(((16 * B + si) * L + min(k0 + 8 * sc, L - 8)) * 2), 0u,
+                   Vb + B * kVBlock);
       }
     }
   };
@@ -279,8 +302,9 @@ __global__ __launch_bounds__(256, kWideBlocks == 1 ? 2 : 1) void jeff_bf16_wide_
   const int vbase = (col >> 4) * kVBlock + half * 256 + (col & 15) * 16;
 
   auto active_word = [&](float mv, int kt) -> uint32_t {
-    const int k = kt * kWideKeys + lane;
-    return (uint32_t)__ballot(lane < 32 && k < L && mv != 0.0f);
+    const int ln = lane_now();
+    const int k = kt * kWideKeys + ln;
+    return (uint32_t)__ballot(ln < 32 && k < L && mv != 0.0f);
   };
 
   f32x16 O[NB][8];
@@ -324,7 +348,7 @@ __global__ __launch_bounds__(256, kWideBlocks == 1 ? 2 : 1) void jeff_bf16_wide_
     const bool more = kt + 1 < kt_end;
     if (more) {
       stage(kt + 1, cur ^ 1);
-      mnext = maskr[min((kt + 1) * kWideKeys + (lane & 31), L - 1)];
+      mnext = maskr[min((kt + 1) * kWideKeys + (lane_now() & 31), L - 1)];
     }
     const int k0 = kt * kWideKeys;
     // Both blocks run whenever one has work: a block past its diagonal or
