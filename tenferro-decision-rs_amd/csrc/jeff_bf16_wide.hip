@@ -78,6 +78,22 @@ __device__ __forceinline__ int lane_now() {
   return l;
 }
 
+// Orders the scheduling region it ends (a straight run of n LDS operand
+// reads, each feeding one MFMA, n > kReadAhead): kReadAhead reads, then
+// alternately one MFMA and one read, then the last kReadAhead MFMAs.
+constexpr int kReadAhead = 4;
+template <int n>
+__device__ __forceinline__ void pipeline_reads() {
+  static_assert(n > kReadAhead, "more reads than the read-ahead");
+  __builtin_amdgcn_sched_group_barrier(0x100, kReadAhead, 0);  // DS reads
+#pragma unroll
+  for (int i = 0; i < n - kReadAhead; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, kReadAhead, 0);
+}
+
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
 }
@@ -368,6 +384,10 @@ __global__ __launch_bounds__(256, kWideBlocks == 1 ? 2 : 1) void jeff_bf16_wide_
 #pragma unroll
         for (int b = 0; b < NB; ++b) st[b] = mfma_32x32x16_bf16(ka, qb[b][s], st[b]);
       }
+      // Schedule: kReadAhead operand reads in flight ahead of the MFMA chain
+      // (left alone, the scheduler issues two at a time and each MFMA waits
+      // on the LDS latency of its operand).
+      pipeline_reads<16 * NB>();
       // Lane (col, half) holds S^T rows 8*(r/4) + 4*half + (r%4): keys of
       // its query q0w + 32b + col.
       bf16x8 pb[NB][2];
@@ -453,6 +473,7 @@ __global__ __launch_bounds__(256, kWideBlocks == 1 ? 2 : 1) void jeff_bf16_wide_
 #pragma unroll
             for (int b = 0; b < NB; ++b) O[b][j] = mfma_32x32x16_bf16(va, pb[b][hh], O[b][j]);
           }
+        pipeline_reads<16 * NB>();
       }
     }
     __builtin_amdgcn_s_waitcnt(0);  // this wave's part of tile kt + 1 is in LDS
