@@ -94,8 +94,12 @@ __device__ __forceinline__ void pipeline_reads() {
   __builtin_amdgcn_sched_group_barrier(0x008, kReadAhead, 0);
 }
 
+// Two f32 rounded to bf16 (nearest even, as f32_to_bf16) in one register,
+// lo in the low half: one v_cvt_pk_bf16_f32.
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
 }
 
 // Heads per workgroup: 4, 2 or 1, whichever divides the GQA group size.
@@ -399,6 +403,9 @@ __global__ __launch_bounds__(256, kWideBlocks == 1 ? 2 : 1) void jeff_bf16_wide_
         const uint32_t kh = keep >> (4 * half);  // bit 8g + r: key 8g + 4*half + r
         const bool full =
             blk_full[b] && wact == 0xffffffffu && k0 + kWideKeys - 1 <= q0w + 32 * b;
+        // Score r is kept: the whole tile is (full), or its keep bit. The
+        // scores themselves are never rewritten (no second copy of them).
+        auto bit = [](uint32_t w, int r) { return ((w >> (8 * (r >> 2) + (r & 3))) & 1u) != 0u; };
         if (full) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
@@ -408,26 +415,30 @@ __global__ __launch_bounds__(256, kWideBlocks == 1 ? 2 : 1) void jeff_bf16_wide_
         } else {
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const bool kept = (kh >> (8 * (r >> 2) + (r & 3))) & 1u;
-            st[b][r] = kept ? st[b][r] : -INFINITY;
-            e[r] = kept ? fast_exp2(__builtin_fmaf(st[b][r], c1, -m[b])) : 0.0f;
+            e[r] = bit(kh, r) ? fast_exp2(__builtin_fmaf(st[b][r], c1, -m[b])) : 0.0f;
             rs += e[r];
           }
         }
         if (__ballot(q_live[b] && !(rs <= kLazyLimit16)) != 0) {
-          // Rare: some term came out large or non-finite; take the tile max
-          // and move the reference.
-          float mx = st[b][0];
+          // Rare: some term came out large or non-finite; take the max of
+          // the kept scores and move the reference. The keep bits are formed
+          // again here (from an opaque copy of the word), so that the common
+          // path never computes them for a full tile.
+          uint32_t kr;
+          asm volatile("v_mov_b32 %0, %1" : "=v"(kr) : "v"(full ? 0xffffffffu : kh));
+          auto kept = [&](int r) { return bit(kr, r); };
+          float mx = -INFINITY;
 #pragma unroll
-          for (int r = 1; r < 16; ++r) mx = fmaxf(mx, st[b][r]);
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, kept(r) ? st[b][r] : -INFINITY);
           const float mxs = pair_max(mx) * c1;
           const float mn = mxs > m[b] + kRescaleSlack ? mxs : m[b];
           rs = 0.0f;
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            e[r] = (__builtin_isinf(st[b][r]) && st[b][r] < 0.0f)
+            const float x = st[b][r];
+            e[r] = (!kept(r) || (__builtin_isinf(x) && x < 0.0f))
                        ? 0.0f
-                       : fast_exp2(__builtin_fmaf(st[b][r], c1, -mn));
+                       : fast_exp2(__builtin_fmaf(x, c1, -mn));
             rs += e[r];
           }
           if (__ballot(q_live[b] && !__builtin_isfinite(rs)) != 0) {
