@@ -3,27 +3,30 @@
 // v and gate held in bf16), on the 32x32x16 bf16 matrix cores of gfx950.
 //
 // One workgroup = 4 wavefronts on one kv head: hw of the group's query heads
-// (4 when the GQA group size allows it) x 4/hw sub-tiles of 64 queries, so a
-// 32-key tile of K and V staged in LDS serves 256 (query, head) rows. Each
-// wavefront owns two blocks of 32 queries of one head (one wavefront per
-// SIMD: O^T of 64 queries x 256 features fills the accumulation registers)
-// and walks the key tiles; per block:
+// (4 when the GQA group size allows it) x 4/hw sub-tiles of 32 queries, so a
+// 32-key tile of K and V staged in LDS serves 128 (query, head) rows; two
+// workgroups per CU (two wavefronts per SIMD, 256 registers each). Each
+// wavefront owns one block of 32 queries of one head and walks the key
+// tiles:
 //   S^T (32 keys x 32 queries) = K_tile . Q^T  (16 MFMAs, K from LDS, Q^T in
 //                                               registers as bf16 B operands)
 //   online softmax in the log2 domain against a lazily moved reference
 //   O^T (256 x 32) += V_tile^T . P^T           (16 MFMAs, V from LDS)
-// Each K and V operand read from LDS feeds both blocks. The probabilities
-// leave the S^T accumulators in the B operand layout of the P.V product
-// except for one lane-half exchange per 8 keys (v_permlane32_swap). K and V
-// move from global memory straight into LDS (global_load_lds_dwordx4, no
-// staging registers), double-buffered, chunk-major in blocks of 16 rows, so
-// that every 128-bit operand read is free of bank conflicts and addressed
-// from one register per lane.
+// with four operand reads from LDS kept in flight ahead of each MFMA chain.
+// The probabilities leave the S^T accumulators in the B operand layout of
+// the P.V product except for one lane-half exchange per 8 keys
+// (v_permlane32_swap). K and V move from global memory straight into LDS
+// (buffer_load_dwordx4 ... lds, no staging registers), double-buffered,
+// chunk-major in blocks of 16 rows, so that every 128-bit operand read is
+// free of bank conflicts and addressed from one register per lane. (Two
+// query blocks per wavefront, so that each operand read feeds two MFMAs,
+// would need 64 queries x 256 features of O^T plus their Q operands: more
+// than the 512 registers of one wavefront per SIMD.)
 //
 // Non-finite values take another route: a workgroup whose kept scores sum to
 // NaN/inf, or whose output came out non-finite (a NaN/inf value, also one
 // multiplied by a zero probability), writes no output and raises its flags;
-// jeff_attention_bf16_kernel then recomputes the flagged tiles with the
+// jeff_bf16_exact_kernel then recomputes the flagged tiles with the
 // reference's exact semantics (masked or zero-probability values never
 // leak, NaN scores weigh 0, a +inf score empties its row).
 #include "jeff_common.hpp"
