@@ -369,20 +369,17 @@ __global__ __launch_bounds__(256, kWideBlocks == 1 ? 2 : 1) void jeff_bf16_wide_
   int cur = 0;
   for (int kt = kt_begin; kt < kt_end; ++kt) {
     const bool more = kt + 1 < kt_end;
-    if (more) {
-      stage(kt + 1, cur ^ 1);
-      mnext = maskr[min((kt + 1) * kWideKeys + (lane_now() & 31), L - 1)];
-    }
     const int k0 = kt * kWideKeys;
     // Both blocks run whenever one has work: a block past its diagonal or
     // without a live query has an all-zero keep word (probabilities 0).
     bool on = false;
 #pragma unroll
     for (int b = 0; b < NB; ++b) on = on || (blk_live[b] && kt < kt_blk_end[b]);
-    if (!tainted && on) {
-      const unsigned char *Kb = lds + cur * kStage;
-      const unsigned char *Vb = Kb + kKBuf;
-      f32x16 st[NB];
+    const bool compute = !tainted && on;
+    const unsigned char *Kb = lds + cur * kStage;
+    const unsigned char *Vb = Kb + kKBuf;
+    f32x16 st[NB];
+    if (compute) {
 #pragma unroll
       for (int b = 0; b < NB; ++b) st[b] = f32x16{};
 #pragma unroll
@@ -395,6 +392,16 @@ __global__ __launch_bounds__(256, kWideBlocks == 1 ? 2 : 1) void jeff_bf16_wide_
       // (left alone, the scheduler issues two at a time and each MFMA waits
       // on the LDS latency of its operand).
       pipeline_reads<16 * NB>();
+    }
+    // The next tile's loads are issued behind the S^T MFMAs, which the
+    // matrix cores work through meanwhile: issuing the eight loads stalls
+    // while the CU's load path is busy with the other wavefronts' tiles, and
+    // at the top of the step that stall held up the MFMAs.
+    if (more) {
+      stage(kt + 1, cur ^ 1);
+      mnext = maskr[min((kt + 1) * kWideKeys + (lane_now() & 31), L - 1)];
+    }
+    if (compute) {
       // Lane (col, half) holds S^T rows 8*(r/4) + 4*half + (r%4): keys of
       // its query q0w + 32b + col.
       bf16x8 pb[NB][2];
