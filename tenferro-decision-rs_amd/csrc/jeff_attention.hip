@@ -125,15 +125,49 @@ __device__ __forceinline__ size_t split_kp_offset(int key, int d) {
   return ((size_t)(kt * 4 + w) * 4 + c) * 256 + (g * 16 + col) * 4 + e;
 }
 
+// One wavefront: the row's active keys (mask != 0) as one bit per key (zero
+// past L, 32 keys per word) and its (first, last) span, (0, -1) for a row
+// with none, for the attention kernels' scalar loads.
+__device__ void write_row_bits_span(const float *__restrict__ maskr, int L, int lane, int row,
+                                    int *__restrict__ spans, uint32_t *__restrict__ kbits) {
+  uint32_t *bits = kbits + (size_t)row * ((L + 31) / 32);
+  int lo = 0x7fffffff, hi = -1;
+  for (int b0 = 0; b0 < L; b0 += 64 * 8) {
+    float mv[8];
+#pragma unroll
+    for (int v = 0; v < 8; ++v) mv[v] = maskr[min(b0 + 64 * v + lane, L - 1)];
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      const int kb = b0 + 64 * v;
+      const uint64_t bm = __ballot(kb + lane < L && mv[v] != 0.0f);
+      if (lane == 0 && kb < L) {
+        bits[kb / 32] = (uint32_t)bm;
+        if (kb + 32 < L) bits[kb / 32 + 1] = (uint32_t)(bm >> 32);
+      }
+      if (bm != 0) {
+        lo = min(lo, kb + (int)__builtin_ctzll(bm));
+        hi = max(hi, kb + 63 - (int)__builtin_clzll(bm));
+      }
+    }
+  }
+  if (lane == 0) {
+    spans[2 * row] = hi >= 0 ? lo : 0;
+    spans[2 * row + 1] = hi;
+  }
+}
+
 // RMSNorm (lib.rs:676-691) and partial RoPE (692-709) of every key of one
 // (row, kv head) once per call, so attention workgroups stage finished keys.
 // One workgroup = 32 keys; output kp[row][kvh][key][HDP] (zero-padded past
 // hd), written in whole 16-byte chunks. Out: f32, or bf16 (RNE) for the
 // bf16 attention kernel. Every global load (keys, norm weights, RoPE table)
-// is issued before the first is used.
+// is issued before the first is used. With spans set, wavefront 0 of each
+// row's first workgroup also writes the row's active key span and bits.
 
 template <int HDP, typename OutT>
-__global__ __launch_bounds__(256) void jeff_k_prep_kernel(const JeffArgs a, OutT *__restrict__ kp) {
+__global__ __launch_bounds__(256) void jeff_k_prep_kernel(const JeffArgs a, OutT *__restrict__ kp,
+                                                          int *__restrict__ spans,
+                                                          uint32_t *__restrict__ kbits) {
   constexpr int DP = HDP / 8;  // dims per thread: 8 threads per key
   constexpr int KS = HDP + 1;
   constexpr int RT = (HDP / 2 + 7) / 8;  // RoPE pairs per thread, at most
@@ -150,6 +184,8 @@ __global__ __launch_bounds__(256) void jeff_k_prep_kernel(const JeffArgs a, OutT
   const bool kin = key < L;
   const bool rope = a.cos_t != nullptr && rh > 0;
   const int start = a.trim ? wave_first_active(a.mask + (size_t)row * L, L, lane) : 0;
+  if (spans != nullptr && blockIdx.x == 0 && kvh == 0 && (tid >> 6) == 0)
+    write_row_bits_span(a.mask + (size_t)row * L, L, lane, row, spans, kbits);
   float xs[DP], wn[DP], c[RT], sn[RT];
 #pragma unroll
   for (int i = 0; i < DP; ++i) {
@@ -288,34 +324,7 @@ __global__ __launch_bounds__(256) void jeff_k_prep_split_kernel(const JeffArgs a
     }
   }
 
-  if (blockIdx.x == 0 && kvh == 0 && wave == 0) {
-    // The row's active keys: one bit per key (zero past L) and the (first,
-    // last) span, (0, -1) for a row with none.
-    uint32_t *bits = kbits + (size_t)row * ((L + 31) / 32);
-    int lo = 0x7fffffff, hi = -1;
-    for (int b0 = 0; b0 < L; b0 += 64 * 8) {
-      float mv[8];
-#pragma unroll
-      for (int v = 0; v < 8; ++v) mv[v] = maskr[min(b0 + 64 * v + lane, L - 1)];
-#pragma unroll
-      for (int v = 0; v < 8; ++v) {
-        const int kb = b0 + 64 * v;
-        const uint64_t bm = __ballot(kb + lane < L && mv[v] != 0.0f);
-        if (lane == 0 && kb < L) {
-          bits[kb / 32] = (uint32_t)bm;
-          if (kb + 32 < L) bits[kb / 32 + 1] = (uint32_t)(bm >> 32);
-        }
-        if (bm != 0) {
-          lo = min(lo, kb + (int)__builtin_ctzll(bm));
-          hi = max(hi, kb + 63 - (int)__builtin_clzll(bm));
-        }
-      }
-    }
-    if (lane == 0) {
-      spans[2 * row] = hi >= 0 ? lo : 0;
-      spans[2 * row + 1] = hi;
-    }
-  }
+  if (blockIdx.x == 0 && kvh == 0 && wave == 0) write_row_bits_span(maskr, L, lane, row, spans, kbits);
 
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
@@ -1854,7 +1863,7 @@ static hipError_t launch_jeff_f32_hd(const JeffArgs &a, int rows, float *kp, hip
     }
   }
   hipExtLaunchKernelGGL((jeff_k_prep_kernel<HDP, float>), pgrid, dim3(256), 0, stream, ev.start,
-                        nullptr, 0, a, kp);
+                        nullptr, 0, a, kp, nullptr, nullptr);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const dim3 block(kJeffF32Waves * 64);
@@ -1897,8 +1906,14 @@ template <int HDP>
 static hipError_t launch_jeff_bf16_hd(const JeffArgs &a, int rows, uint16_t *kp,
                                       hipStream_t stream, const KernelEvents &ev) {
   dim3 pgrid((a.L + kKeyTile - 1) / kKeyTile, a.kv_heads, rows);
+  // The wide bf16 kernel takes the rows' active spans and bits from the prep.
+  const bool wide = HDP == 256 && jeff_bf16_wide_fits(a);
+  int *spans = wide ? reinterpret_cast<int *>(reinterpret_cast<char *>(kp) +
+                                              jeff_kp_main_bytes(a, rows, HDP, true))
+                    : nullptr;
+  uint32_t *kbits = wide ? reinterpret_cast<uint32_t *>(spans + 2 * rows) : nullptr;
   hipExtLaunchKernelGGL((jeff_k_prep_kernel<HDP, uint16_t>), pgrid, dim3(256), 0, stream, ev.start,
-                        nullptr, 0, a, kp);
+                        nullptr, 0, a, kp, spans, kbits);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int qsubs = kWavesPerGroup / a.heads_per_group;
@@ -1911,7 +1926,7 @@ static hipError_t launch_jeff_bf16_hd(const JeffArgs &a, int rows, uint16_t *kp,
     // flagged (non-finite values) on a resident grid (two workgroups per CU).
     if (jeff_bf16_wide_fits(a)) {
       int *flags = reinterpret_cast<int *>(reinterpret_cast<char *>(kp) + jeff_bf16_flags_offset(a, rows));
-      e = launch_jeff_bf16_wide(a, rows, kp, flags, stream);
+      e = launch_jeff_bf16_wide(a, rows, kp, spans, kbits, flags, stream);
       if (e != hipSuccess) return e;
       const int redo_qt = jeff_bf16_wide_query_tile(a);
       const long units = (long)grid.x * grid.y * grid.z;

@@ -2,28 +2,40 @@
 // jeff_full_attention_into, crates/cpu-kernels/src/lib.rs:609-763, with q, k,
 // v and gate held in bf16), on the 32x32x16 bf16 matrix cores of gfx950.
 //
-// One workgroup = 4 wavefronts on one kv head: hw of the group's query heads
-// (4 when the GQA group size allows it) x 4/hw sub-tiles of 32 queries, so a
-// 32-key tile of K and V staged in LDS serves 128 (query, head) rows; two
-// workgroups per CU (two wavefronts per SIMD, 256 registers each). Each
-// wavefront owns one block of 32 queries of one head and walks the key
-// tiles:
+// One workgroup = 8 wavefronts on one kv head, one workgroup per CU (two
+// wavefronts per SIMD, 256 registers each), in two groups of four. A group
+// owns one query tile: hw of the GQA group's query heads (4 when the group
+// size allows it) x 4/hw sub-tiles of 32 queries; the workgroup's two tiles
+// form a causal pair (2p, 2p + 1), so both walk about the same keys and
+// share every 32-key tile of K and V staged in LDS. Each wavefront owns one
+// block of 32 queries of one head and walks the key tiles:
 //   S^T (32 keys x 32 queries) = K_tile . Q^T  (16 MFMAs, K from LDS, Q^T in
 //                                               registers as bf16 B operands)
 //   online softmax in the log2 domain against a lazily moved reference
 //   O^T (256 x 32) += V_tile^T . P^T           (16 MFMAs, V from LDS)
-// with four operand reads from LDS kept in flight ahead of each MFMA chain.
-// The probabilities leave the S^T accumulators in the B operand layout of
-// the P.V product except for one lane-half exchange per 8 keys
-// (v_permlane32_swap). K and V move from global memory straight into LDS
-// (buffer_load_dwordx4 ... lds, no staging registers), double-buffered,
-// chunk-major in blocks of 16 rows, so that every 128-bit operand read is
-// free of bank conflicts and addressed from one register per lane. (Two
-// query blocks per wavefront, so that each operand read feeds two MFMAs,
-// would need 64 queries x 256 features of O^T plus their Q operands: more
-// than the 512 registers of one wavefront per SIMD.)
+// The walk runs in phases separated by workgroup barriers. A wavefront's
+// step k is an MFMA half (P.V of tile k - 1 interleaved with S^T of tile k:
+// every MFMA of the single S^T accumulator chain is followed by an
+// independent P.V MFMA, which covers the chain's result latency) and a
+// vector half (the softmax of tile k). Group 1 runs one phase behind group
+// 0, so on every SIMD one wavefront keeps the matrix core busy while the
+// other one does its softmax (exponentials, sums, bf16 packing), and the two
+// trade roles at every barrier. Left to chance, as with two independent
+// workgroups per CU, the two wavefronts of a SIMD reach their MFMA chains
+// together as often as not.
 //
-// Non-finite values take another route: a workgroup whose kept scores sum to
+// K and V move from global memory straight into LDS (buffer_load_dwordx4
+// ... lds, no staging registers), four tiles deep, chunk-major in blocks of
+// 16 rows, so that every 128-bit operand read is free of bank conflicts and
+// addressed from one register per lane; each of the 8 wavefronts moves 4 of
+// a tile's 32 one-KB pieces. The probabilities leave the S^T accumulators in
+// the B operand layout of the P.V product except for one lane-half exchange
+// per 8 keys (v_permlane32_swap). (Two query blocks per wavefront, so that
+// each operand read feeds two MFMAs, would need 64 queries x 256 features of
+// O^T plus their Q operands: more than the 512 registers of one wavefront per
+// SIMD.)
+//
+// Non-finite values take another route: a group whose kept scores sum to
 // NaN/inf, or whose output came out non-finite (a NaN/inf value, also one
 // multiplied by a zero probability), writes no output and raises its flags;
 // jeff_bf16_exact_kernel then recomputes the flagged tiles with the
@@ -37,11 +49,11 @@ namespace tfd {
 
 namespace {
 
-constexpr int kWideHd = 256;     // head dim (fixed)
-constexpr int kWideKeys = 32;    // keys per tile
-constexpr int kWideWaves = 4;    // wavefronts per workgroup
-constexpr int kWideBlocks = 1;   // 32-query blocks per wavefront
-constexpr int kWideQueries = 32 * kWideBlocks;  // queries per wavefront
+constexpr int kWideHd = 256;      // head dim (fixed)
+constexpr int kWideKeys = 32;     // keys per tile
+constexpr int kWideWaves = 4;     // wavefronts per group (two groups)
+constexpr int kWideQueries = 32;  // queries per wavefront
+constexpr int kWideStages = 4;    // K/V tiles resident in LDS
 // Staged tiles, 16-byte chunks (8 bf16): K as 2 blocks of 16 keys x 32
 // chunks, V as 16 blocks of 16 features x 4 chunks, each block chunk-major
 // (chunk c of row i at c * 256 + 16 * i within its block).
@@ -58,23 +70,32 @@ __device__ __forceinline__ f32x16 mfma_32x32x16_bf16(bf16x8 a, bf16x8 b, f32x16 
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-// 16 bytes at byte voff + soff of buffer r into LDS: lane i of the wavefront
-// writes lds_base + 16*i (lds_base and soff the same for the whole
-// wavefront). The buffer form keeps the per-lane address in one 32-bit
-// register (the global form needs a 64-bit address per load, which the
-// compiler ends up spilling, and every reload's wait would then also wait
-// for the loads to LDS issued before it).
-__device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
+// A buffer resource as four scalar words (raw buffer, no swizzle).
+typedef unsigned u32x4r __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x4r rsrc_words(const void *base, uint32_t bytes) {
+  const uint64_t ad = reinterpret_cast<uint64_t>(base);
+  return u32x4r{(uint32_t)ad, (uint32_t)(ad >> 32) & 0xffffu, bytes, (uint32_t)kBufferWord3};
+}
+
+// 16 bytes at byte voff + soff of the buffer r into LDS at lds_base + 16*lane
+// (M0 = lds_base; lds_base and soff the same for the whole wavefront): one
+// 32-bit offset register per lane. Written out rather than through the
+// builtin, which the compiler treats as a write to any LDS address: it would
+// make the next LDS operand read wait for every such load issued before it.
+// The walk orders these loads itself (each wavefront waits for its own
+// loads before the barrier that precedes a tile's first read).
+__device__ __forceinline__ void load_lds16(u32x4r r, uint32_t voff, uint32_t soff,
                                            unsigned char *lds_base) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds_base,
-                                           16, (int)voff, (int)soff, 0, 0);
+  const uint32_t m = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)lds_base;
+  asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff),
+               "s"(r), "s"(soff), "s"(m)
+               : "m0");
 }
 
 // This lane's index, recomputed where it is used (two vector instructions,
-// opaque to the compiler): the walk needs it only for the mask and the last
-// tile's clamped addresses, and a lane index kept live across the walk is
-// what the compiler spills first (its reload then waits on every load to
-// LDS issued before it).
+// opaque to the compiler): the walk needs it only for the last tile's
+// clamped addresses, and a lane index kept live across the walk is what the
+// compiler spills first.
 __device__ __forceinline__ int lane_now() {
   int l;
   asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
@@ -83,7 +104,9 @@ __device__ __forceinline__ int lane_now() {
 
 // Orders the scheduling region it ends (a straight run of n LDS operand
 // reads, each feeding one MFMA, n > kReadAhead): kReadAhead reads, then
-// alternately one MFMA and one read, then the last kReadAhead MFMAs.
+// alternately one MFMA and one read, then the last kReadAhead MFMAs. Left
+// alone, the scheduler issues two reads at a time and every MFMA waits out
+// the LDS latency of its operand.
 constexpr int kReadAhead = 4;
 template <int n>
 __device__ __forceinline__ void pipeline_reads() {
@@ -105,7 +128,7 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
 }
 
-// Heads per workgroup: 4, 2 or 1, whichever divides the GQA group size.
+// Heads per group: 4, 2 or 1, whichever divides the GQA group size.
 int wide_heads_per_group(const JeffArgs &a) {
   const int G = a.heads / a.kv_heads;
   return G % 4 == 0 ? 4 : (G % 2 == 0 ? 2 : 1);
@@ -132,38 +155,38 @@ size_t jeff_bf16_wide_flag_count(const JeffArgs &a, int rows) {
   return (size_t)rows * a.heads * ((a.L + qt - 1) / qt);
 }
 
-// Work item p: query tile qt (longest first), then unit u = (row, kv head,
-// head group); the units of one tile are consecutive, so their K/V streams
-// land on few XCDs and meet in L2.
-__global__ __launch_bounds__(256, kWideBlocks == 1 ? 2 : 1) void jeff_bf16_wide_kernel(const JeffArgs a,
+// Work item p: query tile pair qt2 (longest first), then unit u = (row, kv
+// head, head group); the units of one pair are consecutive, so their K/V
+// streams land on few XCDs and meet in L2. spans / kbits: each row's active
+// key span and one bit per key (jeff_k_prep_kernel).
+__global__ __launch_bounds__(512, 1) void jeff_bf16_wide_kernel(const JeffArgs a,
                                                                 const uint16_t *__restrict__ kp,
-                                                                int *__restrict__ flags,
-                                                                int rows, int hw) {
-  constexpr int NB = kWideBlocks;
-  __shared__ __attribute__((aligned(16))) unsigned char lds[2 * kStage];
-  __shared__ int s_span[2];
-  __shared__ int s_flag;
+                                                                const int *__restrict__ spans,
+                                                                const uint32_t *__restrict__ kbits,
+                                                                int *__restrict__ flags, int rows,
+                                                                int hw) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kWideStages * kStage];
+  __shared__ int s_flag[2];
 
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // 0..7
+  const int grp = wave >> 2, w4 = wave & 3;
   const int col = lane & 31, half = lane >> 5;
   const int L = a.L, G = a.heads / a.kv_heads;
-  const int ngrp = G / hw;  // head groups per kv head
+  const int ngrp = G / hw;
   const int QT = kWideQueries * (kWideWaves / hw);
-  const int nqt = (L + QT - 1) / QT;
+  const int nqt = (L + QT - 1) / QT, nqt2 = (nqt + 1) / 2;
   const int units = rows * a.kv_heads * ngrp;
   const int p = blockIdx.x;
-  const int qt = nqt - 1 - p / units;
+  const int qt2 = nqt2 - 1 - p / units;
   const int u = p % units;
   const int row = u / (a.kv_heads * ngrp);
   const int kvh = (u / ngrp) % a.kv_heads;
-  const int head = kvh * G + (u % ngrp) * hw + wave % hw;
-  const int q0w = qt * QT + (wave / hw) * kWideQueries;  // block b: q0w + 32b
-  int qv[NB];
-#pragma unroll
-  for (int b = 0; b < NB; ++b) qv[b] = q0w + 32 * b + col;
+  const int head = kvh * G + (u % ngrp) * hw + w4 % hw;
+  const int qt = 2 * qt2 + grp;
+  const int q0w = qt * QT + (w4 / hw) * kWideQueries;
+  const int qv = q0w + col;
 
-  const float *maskr = a.mask + (size_t)row * L;
   const uint16_t *Qh =
       static_cast<const uint16_t *>(a.q) + row * a.q_row + (size_t)head * kWideHd * L;
   const uint16_t *Gh =
@@ -172,58 +195,33 @@ __global__ __launch_bounds__(256, kWideBlocks == 1 ? 2 : 1) void jeff_bf16_wide_
       static_cast<const uint16_t *>(a.v) + row * a.kv_row + (size_t)kvh * a.kv_head;
   const uint16_t *Kh = kp + ((size_t)row * a.kv_heads + kvh) * (size_t)L * kWideHd;
   float *Oh = a.out + row * a.q_row + (size_t)head * kWideHd * L;
+  const uint32_t *rbits = kbits + (size_t)row * ((L + 31) / 32);
 
-  // -------- the row's active span (mask != 0), one pass of the workgroup.
-  if (tid == 0) {
-    s_span[0] = 0x7fffffff;
-    s_span[1] = -1;
-    s_flag = 0;
-  }
-  __syncthreads();
-  {
-    int lo = 0x7fffffff, hi = -1;
-    for (int k0 = 0; k0 < L; k0 += 256 * 8) {
-      float v[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = maskr[min(k0 + tid + 256 * i, L - 1)];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int k = k0 + tid + 256 * i;
-        if (k < L && v[i] != 0.0f) {
-          lo = min(lo, k);
-          hi = max(hi, k);
-        }
-      }
-    }
-    lo = wave_min(lo);
-    hi = wave_max(hi);
-    if (lane == 0) {
-      atomicMin(&s_span[0], lo);
-      atomicMax(&s_span[1], hi);
-    }
-  }
-  __syncthreads();
-  const int first = s_span[0], last = s_span[1];
+  // -------- the row's active span: the walk covers its tiles up to the
+  // workgroup's last query (causal).
+  const int first = spans[2 * row], last = spans[2 * row + 1];
   const int start = (a.trim && last >= 0) ? first : 0;
-  bool q_live[NB];
-#pragma unroll
-  for (int b = 0; b < NB; ++b) q_live[b] = qv[b] < L && qv[b] >= start;
-  const int q_last_wg = min(qt * QT + QT - 1, L - 1);
+  const bool q_live = qv < L && qv >= start;
+  const int q_last_wg = min((2 * qt2 + 2) * QT - 1, L - 1);
   int kt_begin = 0, kt_end = 0;
   if (last >= 0 && first <= min(last, q_last_wg)) {
     kt_begin = first / kWideKeys;
     kt_end = min(last, q_last_wg) / kWideKeys + 1;
   }
+  // This wavefront's 32 queries: the last tile with a key at or before one
+  // of them, and whether some / all of them are live.
+  const int kt_w_end = q0w < L ? min(kt_end, min(last, q0w + 31) / kWideKeys + 1) : kt_begin;
+  const bool w_live = q0w < L && q0w + 31 >= start;
+  const bool w_full = q0w >= start && q0w + 32 <= L;
 
   // -------- Q: RMSNorm (lib.rs:676-691) and partial RoPE (692-709) in f32,
   // rounded to bf16 B operands: lane (col, half) holds features
-  // 16s + 8*half + e of query q0w + 32b + col in qb[b][s]. RoPE partners
-  // (i, i + rot/2) sit in the same lane, rot/32 steps apart.
-  bf16x8 qb[NB][16];
+  // 16s + 8*half + e of query qv in qb[s]. RoPE partners (i, i + rot/2) sit
+  // in the same lane, rot/32 steps apart.
+  bf16x8 qb[16];
   const int rh = a.cos_t != nullptr ? a.rot_half : 0;
-#pragma unroll
-  for (int b = 0; b < NB; ++b) {
-    const int qc = min(qv[b], L - 1);
+  {
+    const int qc = min(qv, L - 1);
     float y[16][8];
     float ss = 0.0f;
 #pragma unroll
@@ -242,9 +240,7 @@ __global__ __launch_bounds__(256, kWideBlocks == 1 ? 2 : 1) void jeff_bf16_wide_
 #pragma unroll
       for (int e = 0; e < 8; ++e) y[s][e] = rms_apply(y[s][e], scale, e < 4 ? w0[e] : w1[e - 4]);
     }
-    const size_t pos = (size_t)min(max(qv[b] - start, 0), L - 1) * (size_t)(rh > 0 ? rh : 1);
-    // Steps s < rot/32 hold pairs i = 16s + 8*half + e, step s + rot/32
-    // their partners i + rot/2.
+    const size_t pos = (size_t)min(max(qv - start, 0), L - 1) * (size_t)(rh > 0 ? rh : 1);
     auto rotate = [&](float (&lo)[8], float (&hi)[8], int s) {
       const int i0 = 16 * s + 8 * half;
       const f32x4 c0 = *reinterpret_cast<const f32x4 *>(a.cos_t + pos + i0);
@@ -259,297 +255,304 @@ __global__ __launch_bounds__(256, kWideBlocks == 1 ? 2 : 1) void jeff_bf16_wide_
         hi[e] = rope_hi(xl, xh, c, sn);
       }
     };
-    if (q_live[b] && rh == 32) {
+    if (q_live && rh == 32) {
       rotate(y[0], y[2], 0);
       rotate(y[1], y[3], 1);
-    } else if (q_live[b] && rh == 16) {
+    } else if (q_live && rh == 16) {
       rotate(y[0], y[1], 0);
     }
 #pragma unroll
     for (int s = 0; s < 16; ++s)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) qb[b][s][e] = (__bf16)(q_live[b] ? y[s][e] : 0.0f);
+      for (int e = 0; e < 8; ++e) qb[s][e] = (__bf16)(q_live ? y[s][e] : 0.0f);
   }
 
-  // -------- staging (tile of keys k0 .. k0+31): chunk c of key k0 + 16B + i
-  // to K block B, chunk c of V feature 16B + i to V block B. One 1 KB
-  // instruction fills 4 chunks x 16 rows of a block; wavefront w moves K
-  // chunks 8w .. 8w+7 of both blocks and V blocks 4w .. 4w+3. A whole tile
-  // addresses every row from one uniform base and a fixed lane offset; in
-  // the row's last, partial tile keys past L repeat the last key (its keep
-  // bit is 0).
-  const int si = lane & 15, sc = lane >> 4;  // row, chunk within an instruction
+  // -------- staging of local tile j (keys 32 (kt_begin + j) ..) into buffer
+  // j mod 4: a tile is 32 one-KB loads (K: 2 blocks x 8 instructions of 4
+  // chunks; V: 16 blocks), wavefront w issues K instructions 2w, 2w + 1
+  // (block i >> 3, chunks 4 (i & 7) ..) and V blocks 2w, 2w + 1. A lane
+  // moves 16 bytes: row lane & 15, chunk lane >> 4 of its instruction.
+  const int si = lane & 15, sc = lane >> 4;
   const uint32_t klane = (uint32_t)(si * kWideHd * 2 + sc * 16);
   const uint32_t vlane = (uint32_t)(si * L * 2 + sc * 16);
-  // One (row, kv head)'s prepared K (L x 256) and V (256 x L), bf16 (each
-  // under 2 GiB: jeff_bf16_wide_fits).
-  const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(Kh, (uint32_t)((size_t)L * kWideHd * 2));
-  const __amdgpu_buffer_rsrc_t rv = buffer_rsrc(Vh, (uint32_t)((size_t)L * kWideHd * 2));
-  auto stage = [&](int kt, int buf) {
-    unsigned char *Kb = lds + buf * kStage;
+  const u32x4r rk = rsrc_words(Kh, (uint32_t)((size_t)L * kWideHd * 2));
+  const u32x4r rv = rsrc_words(Vh, (uint32_t)((size_t)L * kWideHd * 2));
+  auto buf = [&](int j) { return lds + (j & (kWideStages - 1)) * kStage; };
+  auto stage = [&](int j) {
+    unsigned char *Kb = buf(j);
     unsigned char *Vb = Kb + kKBuf;
-    const int k0 = kt * kWideKeys;
+    const int k0 = (kt_begin + j) * kWideKeys;
     if (k0 + kWideKeys <= L) {
 #pragma unroll
-      for (int n = 0; n < 4; ++n) {
-        const int B = n >> 1, c0 = 8 * wave + 4 * (n & 1);
+      for (int n = 0; n < 2; ++n) {
+        const int i = 2 * wave + n, B = i >> 3, c0 = 4 * (i & 7);
         load_lds16(rk, klane, (uint32_t)(((k0 + 16 * B) * kWideHd + 8 * c0) * 2),
                    Kb + B * kKBlock + c0 * 256);
       }
 #pragma unroll
-      for (int n = 0; n < 4; ++n) {
-        const int B = 4 * wave + n;
+      for (int n = 0; n < 2; ++n) {
+        const int B = 2 * wave + n;
         load_lds16(rv, vlane, (uint32_t)((16 * B * L + k0) * 2), Vb + B * kVBlock);
       }
     } else {
-      const int ln = lane_now(), si = ln & 15, sc = ln >> 4;
+      // The last, partial tile: keys clamped to L - 1 (their scores are
+      // masked), V chunks clamped to the last 8 keys.
+      const int ln = lane_now(), li = ln & 15, lc = ln >> 4;
 #pragma unroll
-      for (int n = 0; n < 4; ++n) {
-        const int B = n >> 1, c0 = 8 * wave + 4 * (n & 1);
-        const int key = min(k0 + 16 * B + si, L - 1);
-        load_lds16(rk, (uint32_t)((key * kWideHd + 8 * (c0 + sc)) * 2), 0u,
+      for (int n = 0; n < 2; ++n) {
+        const int i = 2 * wave + n, B = i >> 3, c0 = 4 * (i & 7);
+        const int key = min(k0 + 16 * B + li, L - 1);
+        load_lds16(rk, (uint32_t)((key * kWideHd + 8 * (c0 + lc)) * 2), 0u,
                    Kb + B * kKBlock + c0 * 256);
       }
 #pragma unroll
-      for (int n = 0; n < 4; ++n) {
-        const int B = 4 * wave + n;
-        load_lds16(rv, (uint32_t)(((16 * B + si) * L + min(k0 + 8 * sc, L - 8)) * 2), 0u,
+      for (int n = 0; n < 2; ++n) {
+        const int B = 2 * wave + n;
+        load_lds16(rv, (uint32_t)(((16 * B + li) * L + min(k0 + 8 * lc, L - 8)) * 2), 0u,
                    Vb + B * kVBlock);
       }
     }
   };
-  // Operand reads: K step s (features 16s .. 16s+15) of key col, chunk
-  // 2s + half; V block j, keys 16hh .. 16hh+15 of feature 32j + col, chunk
-  // 2hh + half. Both are one base register plus a constant.
+  // Operand addresses: lane (col, half) reads K row col (block col >> 4),
+  // chunks 2s + half, and V feature row col of each 32-feature block.
   const int kbase = (col >> 4) * kKBlock + half * 256 + (col & 15) * 16;
   const int vbase = (col >> 4) * kVBlock + half * 256 + (col & 15) * 16;
 
-  auto active_word = [&](float mv, int kt) -> uint32_t {
-    const int ln = lane_now();
-    const int k = kt * kWideKeys + ln;
-    return (uint32_t)__ballot(ln < 32 && k < L && mv != 0.0f);
-  };
-
-  f32x16 O[NB][8];
+  f32x16 O[8];
 #pragma unroll
-  for (int b = 0; b < NB; ++b)
+  for (int j = 0; j < 8; ++j)
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) O[b][j][r] = 0.0f;
-  float m[NB], l[NB];
-#pragma unroll
-  for (int b = 0; b < NB; ++b) {
-    m[b] = kNoMax;
-    l[b] = 0.0f;
-  }
+    for (int r = 0; r < 16; ++r) O[j][r] = 0.0f;
+  float m = kNoMax, l = 0.0f;
   const float c1 = a.c1;
   bool tainted = false;  // wave-uniform
+  f32x16 st = {};
+  bf16x8 pb[2] = {};
 
-  float mnext = 0.0f;
-  if (kt_begin < kt_end) {
-    stage(kt_begin, 0);
-    mnext = maskr[min(kt_begin * kWideKeys + (lane & 31), L - 1)];
-  }
-  __builtin_amdgcn_s_waitcnt(0);
+  const int T = kt_end - kt_begin;
+  if (T > 0) stage(0);
+  if (T > 1) stage(1);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if (tid < 2) s_flag[tid] = 0;
   __syncthreads();
-  uint32_t wact = kt_begin < kt_end ? active_word(mnext, kt_begin) : 0u;
-  // Per block: the last tile with a key at or before one of its queries,
-  // and whether some / all of its queries are live.
-  int kt_blk_end[NB];
-  bool blk_live[NB], blk_full[NB];
-#pragma unroll
-  for (int b = 0; b < NB; ++b) {
-    const int qb0 = q0w + 32 * b;
-    kt_blk_end[b] = min(kt_end, min(last, qb0 + 31) / kWideKeys + 1);
-    blk_live[b] = qb0 < L && qb0 + 31 >= start;
-    blk_full[b] = qb0 >= start && qb0 + 32 <= L;
-  }
 
-  int cur = 0;
-  for (int kt = kt_begin; kt < kt_end; ++kt) {
-    const bool more = kt + 1 < kt_end;
-    const int k0 = kt * kWideKeys;
-    // Both blocks run whenever one has work: a block past its diagonal or
-    // without a live query has an all-zero keep word (probabilities 0).
-    bool on = false;
+  // Steps this wavefront computes: tiles 0 .. kw - 1 of the walk (none
+  // after a tile came out non-finite: the exact pass redoes the wavefront).
+  int kw = w_live ? max(kt_w_end - kt_begin, 0) : 0;
+
+  // -------- the softmax of local tile k (scores in st) into the P^T
+  // operands pb (lib.rs:712-730), against the reference m.
+  auto softmax = [&](int k) {
+    const int kt = kt_begin + k, k0 = kt * kWideKeys;
+    const uint32_t wact = rbits[kt];
+    float e[16];
+    float rs = 0.0f;
+    const uint32_t keep = q_live ? (wact & range_bits(0, qv - k0)) : 0u;
+    const uint32_t kh = keep >> (4 * half);  // bit 8g + r: key 8g + 4*half + r
+    const bool full = w_full && wact == 0xffffffffu && k0 + kWideKeys - 1 <= q0w;
+    auto bit = [](uint32_t w, int r) { return ((w >> (8 * (r >> 2) + (r & 3))) & 1u) != 0u; };
+    // Lane (col, half) holds S^T rows (keys) 8g + 4*half + r' of query col
+    // in st[4g + r'].
+    if (full) {
 #pragma unroll
-    for (int b = 0; b < NB; ++b) on = on || (blk_live[b] && kt < kt_blk_end[b]);
-    const bool compute = !tainted && on;
-    const unsigned char *Kb = lds + cur * kStage;
-    const unsigned char *Vb = Kb + kKBuf;
-    f32x16 st[NB];
-    if (compute) {
+      for (int r = 0; r < 16; ++r) {
+        e[r] = fast_exp2(__builtin_fmaf(st[r], c1, -m));
+        rs += e[r];
+      }
+    } else {
 #pragma unroll
-      for (int b = 0; b < NB; ++b) st[b] = f32x16{};
+      for (int r = 0; r < 16; ++r) {
+        e[r] = bit(kh, r) ? fast_exp2(__builtin_fmaf(st[r], c1, -m)) : 0.0f;
+        rs += e[r];
+      }
+    }
+    if (__ballot(q_live && !(rs <= kLazyLimit16)) != 0) {
+      // Rare: a score far above the reference (or non-finite). Move the
+      // reference to the tile's maximum and redo the terms; -inf scores and
+      // masked keys weigh 0. The keep bits go through an opaque copy so that
+      // the common path above does not hold them.
+      uint32_t kr;
+      asm volatile("v_mov_b32 %0, %1" : "=v"(kr) : "v"(full ? 0xffffffffu : kh));
+      auto kept = [&](int r) { return bit(kr, r); };
+      float mx = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, kept(r) ? st[r] : -INFINITY);
+      const float mxs = pair_max(mx) * c1;
+      const float mn = mxs > m + kRescaleSlack ? mxs : m;
+      rs = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float x = st[r];
+        e[r] = (!kept(r) || (__builtin_isinf(x) && x < 0.0f))
+                   ? 0.0f
+                   : fast_exp2(__builtin_fmaf(x, c1, -mn));
+        rs += e[r];
+      }
+      if (__ballot(q_live && !__builtin_isfinite(rs)) != 0) {
+        tainted = true;
+        kw = 0;
+      } else if (__ballot(mn != m) != 0) {
+        const float alpha = fast_exp2(m - mn);  // exactly 1 where m stays
+        if (__ballot(l != 0.0f) != 0) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) O[j] *= alpha;
+        }
+        l *= alpha;
+        m = mn;
+      }
+    }
+    l += rs;
+    // P^T as the B operand of O^T += V^T . P^T: lane (col, half) needs keys
+    // 8*half .. 8*half + 7 of each 16-key half hh; it holds keys 4*half + r'
+    // of each 8-key group. One permlane32 swap per pair of 8-key groups.
+    uint32_t g[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) g[i] = pack_bf16x2(e[2 * i], e[2 * i + 1]);
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      uint32_t w[4];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const auto r = __builtin_amdgcn_permlane32_swap(g[4 * hh + i], g[4 * hh + 2 + i],
+                                                        false, false);
+        w[i] = r[0];
+        w[2 + i] = r[1];
+      }
+      pb[hh] = __builtin_bit_cast(
+          bf16x8, (__attribute__((ext_vector_type(4))) uint32_t){w[0], w[1], w[2], w[3]});
+    }
+  };
+  // The V operands of the first two P.V MFMAs of tile k (blocks O[0] and
+  // O[1], first key half), read at the end of the vector half so that the
+  // next MFMA half starts without waiting on LDS; tile k is complete then.
+  bf16x8 vpre0, vpre1;
+  auto pre_read = [&](int k) {
+    const unsigned char *Vb = buf(k) + kKBuf;
+    vpre0 = *reinterpret_cast<const bf16x8 *>(Vb + vbase);
+    vpre1 = *reinterpret_cast<const bf16x8 *>(Vb + vbase + 2 * kVBlock);
+  };
+  // End of an MFMA half: this wavefront's loads of the next tile are in LDS
+  // and its operand reads are done.
+  auto mfma_end = [&]() {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  };
+
+  // -------- the walk. Group 1 runs one phase behind group 0: one barrier
+  // more before the walk, one fewer after it. Step k: the MFMA half (P.V of
+  // tile k - 1 and S^T of tile k), then the vector half (staging tile k + 2
+  // into the buffer tile k - 2 left, whose last reader, group 1's P.V, ran
+  // in the phase before; the softmax of tile k). Each wavefront waits for
+  // its share of tile k + 1 at the end of its MFMA half of step k, before
+  // the barrier that precedes the tile's first read (group 0's S^T in step
+  // k + 1). Every barrier is reached by all eight wavefronts: the number of
+  // steps T is the workgroup's.
+  if (grp == 1) asm volatile("s_barrier" ::: "memory");
+  {
+    const bool sk = 0 < kw;
+    if (sk) {
+      const unsigned char *Kb = buf(0);
+      st = f32x16{};
 #pragma unroll
       for (int s = 0; s < 16; ++s) {
         const bf16x8 ka = *reinterpret_cast<const bf16x8 *>(Kb + kbase + s * 512);
-#pragma unroll
-        for (int b = 0; b < NB; ++b) st[b] = mfma_32x32x16_bf16(ka, qb[b][s], st[b]);
+        st = mfma_32x32x16_bf16(ka, qb[s], st);
       }
-      // Schedule: kReadAhead operand reads in flight ahead of the MFMA chain
-      // (left alone, the scheduler issues two at a time and each MFMA waits
-      // on the LDS latency of its operand).
-      pipeline_reads<16 * NB>();
+      pipeline_reads<16>();
     }
-    // The next tile's loads are issued behind the S^T MFMAs, which the
-    // matrix cores work through meanwhile: issuing the eight loads stalls
-    // while the CU's load path is busy with the other wavefronts' tiles, and
-    // at the top of the step that stall held up the MFMAs.
-    if (more) {
-      stage(kt + 1, cur ^ 1);
-      mnext = maskr[min((kt + 1) * kWideKeys + (lane_now() & 31), L - 1)];
-    }
-    if (compute) {
-      // Lane (col, half) holds S^T rows 8*(r/4) + 4*half + (r%4): keys of
-      // its query q0w + 32b + col.
-      bf16x8 pb[NB][2];
-#pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        float e[16];
-        float rs = 0.0f;
-        const uint32_t keep = q_live[b] ? (wact & range_bits(0, qv[b] - k0)) : 0u;
-        const uint32_t kh = keep >> (4 * half);  // bit 8g + r: key 8g + 4*half + r
-        const bool full =
-            blk_full[b] && wact == 0xffffffffu && k0 + kWideKeys - 1 <= q0w + 32 * b;
-        // Score r is kept: the whole tile is (full), or its keep bit. The
-        // scores themselves are never rewritten (no second copy of them).
-        auto bit = [](uint32_t w, int r) { return ((w >> (8 * (r >> 2) + (r & 3))) & 1u) != 0u; };
-        if (full) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            e[r] = fast_exp2(__builtin_fmaf(st[b][r], c1, -m[b]));
-            rs += e[r];
-          }
-        } else {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            e[r] = bit(kh, r) ? fast_exp2(__builtin_fmaf(st[b][r], c1, -m[b])) : 0.0f;
-            rs += e[r];
-          }
-        }
-        if (__ballot(q_live[b] && !(rs <= kLazyLimit16)) != 0) {
-          // Rare: some term came out large or non-finite; take the max of
-          // the kept scores and move the reference. The keep bits are formed
-          // again here (from an opaque copy of the word), so that the common
-          // path never computes them for a full tile.
-          uint32_t kr;
-          asm volatile("v_mov_b32 %0, %1" : "=v"(kr) : "v"(full ? 0xffffffffu : kh));
-          auto kept = [&](int r) { return bit(kr, r); };
-          float mx = -INFINITY;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, kept(r) ? st[b][r] : -INFINITY);
-          const float mxs = pair_max(mx) * c1;
-          const float mn = mxs > m[b] + kRescaleSlack ? mxs : m[b];
-          rs = 0.0f;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float x = st[b][r];
-            e[r] = (!kept(r) || (__builtin_isinf(x) && x < 0.0f))
-                       ? 0.0f
-                       : fast_exp2(__builtin_fmaf(x, c1, -mn));
-            rs += e[r];
-          }
-          if (__ballot(q_live[b] && !__builtin_isfinite(rs)) != 0) {
-            tainted = true;
-          } else if (__ballot(mn != m[b]) != 0) {
-            const float alpha = fast_exp2(m[b] - mn);  // exactly 1 where m stays
-            if (__ballot(l[b] != 0.0f) != 0) {  // nothing accumulated yet: O is 0
-#pragma unroll
-              for (int j = 0; j < 8; ++j) O[b][j] *= alpha;
-            }
-            l[b] *= alpha;
-            m[b] = mn;
-          }
-        }
-        l[b] += rs;
-        // P^T B operands: keys 16hh + 8*half + e for query col. Lanes hold
-        // keys 8g + 4*half + (0..3) in group g; one v_permlane32_swap per
-        // register trades the missing four with lane ^ 32.
-        uint32_t g[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) g[i] = pack_bf16x2(e[2 * i], e[2 * i + 1]);
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          uint32_t w[4];
-#pragma unroll
-          for (int i = 0; i < 2; ++i) {
-            const auto r = __builtin_amdgcn_permlane32_swap(g[4 * hh + i], g[4 * hh + 2 + i],
-                                                            false, false);
-            w[i] = r[0];
-            w[2 + i] = r[1];
-          }
-          pb[b][hh] = __builtin_bit_cast(
-              bf16x8, (__attribute__((ext_vector_type(4))) uint32_t){w[0], w[1], w[2], w[3]});
-        }
-      }
-      if (!tainted) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-#pragma unroll
-          for (int hh = 0; hh < 2; ++hh) {
-            const bf16x8 va =
-                *reinterpret_cast<const bf16x8 *>(Vb + vbase + j * 2 * kVBlock + hh * 512);
-#pragma unroll
-            for (int b = 0; b < NB; ++b) O[b][j] = mfma_32x32x16_bf16(va, pb[b][hh], O[b][j]);
-          }
-        pipeline_reads<16 * NB>();
-      }
-    }
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's part of tile kt + 1 is in LDS
-    __syncthreads();
-    if (more) wact = active_word(mnext, kt + 1);
-    cur ^= 1;
+    mfma_end();
+    if (2 < T) stage(2);
+    if (sk) softmax(0);
+    pre_read(0);
+    asm volatile("s_barrier" ::: "memory");
   }
+  for (int k = 1; k <= T; ++k) {
+    const bool pv = k <= kw, sk = k < kw;
+    if (pv) {
+      // P.V(k - 1) and S^T(k) interleaved. Past this wavefront's last tile
+      // (sk false) the S^T products read a stale buffer and are not used.
+      const unsigned char *Vb = buf(k - 1) + kKBuf;
+      const unsigned char *Kb = buf(k);
+      // P.V order: O blocks (0, 1) of key half 0 from the pre-read, then
+      // (0, 1) of half 1, (2, 3) of half 0, (2, 3) of half 1, ...
+      constexpr int kPj[16] = {0, 1, 0, 1, 2, 3, 2, 3, 4, 5, 4, 5, 6, 7, 6, 7};
+      constexpr int kPh[16] = {0, 0, 1, 1, 0, 0, 1, 1, 0, 0, 1, 1, 0, 0, 1, 1};
+      st = f32x16{};
+      O[0] = mfma_32x32x16_bf16(vpre0, pb[0], O[0]);
+      O[1] = mfma_32x32x16_bf16(vpre1, pb[0], O[1]);
+#pragma unroll
+      for (int s = 0; s < 16; ++s) {
+        const bf16x8 ka = *reinterpret_cast<const bf16x8 *>(Kb + kbase + s * 512);
+        st = mfma_32x32x16_bf16(ka, qb[s], st);
+        if (s < 14) {
+          const int q = s + 2;
+          const bf16x8 va = *reinterpret_cast<const bf16x8 *>(Vb + vbase + kPj[q] * 2 * kVBlock +
+                                                              kPh[q] * 512);
+          O[kPj[q]] = mfma_32x32x16_bf16(va, pb[kPh[q]], O[kPj[q]]);
+        }
+      }
+      // Four operand reads in flight: the two pre-read MFMAs go first.
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // DS reads
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+#pragma unroll
+      for (int i = 0; i < 26; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    }
+    mfma_end();
+    if (k + 2 < T) stage(k + 2);
+    if (sk) softmax(k);
+    pre_read(k);
+    asm volatile("s_barrier" ::: "memory");
+  }
+  if (grp == 0) asm volatile("s_barrier" ::: "memory");
 
   // -------- o / sum (0 when nothing was kept), sigmoid gate, store
   // (lib.rs:731-758). A non-finite output is left to the exact pass.
   bool bad = tainted;
 #pragma unroll
-  for (int b = 0; b < NB; ++b)
+  for (int j = 0; j < 8; ++j)
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) bad |= q_live[b] && !__builtin_isfinite(O[b][j][r]);
-  if (__ballot(bad) != 0 && lane == 0) s_flag = 1;
+    for (int r = 0; r < 16; ++r) bad |= q_live && !__builtin_isfinite(O[j][r]);
+  if (__ballot(bad) != 0 && lane == 0) s_flag[grp] = 1;
   __syncthreads();
-  const bool flagged = s_flag != 0;
-  // one flag per (row, head, query tile): waves 0 .. hw-1 hold the heads
-  if (lane == 0 && wave < hw) flags[((size_t)row * a.heads + head) * nqt + qt] = flagged ? 1 : 0;
-  if (flagged) return;
+  const bool flagged = s_flag[grp] != 0;
+  // One flag per (row, head, query tile): wavefronts 0 .. hw-1 of a group
+  // hold its heads.
+  if (lane == 0 && w4 < hw && qt < nqt)
+    flags[((size_t)row * a.heads + head) * nqt + qt] = flagged ? 1 : 0;
+  if (flagged || qv >= L) return;
+  const float lt = pair_sum(l);
+  const float inv = lt > 0.0f ? fast_rcp(lt) : 0.0f;
+  const bool dropped = a.trim && qv < start;
 #pragma unroll
-  for (int b = 0; b < NB; ++b) {
-    const int q = qv[b];
-    if (q >= L) continue;
-    const float lt = pair_sum(l[b]);
-    const float inv = lt > 0.0f ? fast_rcp(lt) : 0.0f;
-    const bool dropped = a.trim && q < start;
+  for (int j = 0; j < 8; ++j) {
+    float gv[16];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      float gv[16];
+    for (int r = 0; r < 16; ++r) {
+      const int f = 32 * j + 8 * (r >> 2) + 4 * half + (r & 3);
+      gv[r] = bf16_to_f32(Gh[(size_t)f * L + qv]);
+    }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int f = 32 * j + 8 * (r >> 2) + 4 * half + (r & 3);
-        gv[r] = bf16_to_f32(Gh[(size_t)f * L + q]);
-      }
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int f = 32 * j + 8 * (r >> 2) + 4 * half + (r & 3);
-        Oh[(size_t)f * L + q] = dropped ? 0.0f : O[b][j][r] * inv * fast_sigmoid(gv[r]);
-      }
+    for (int r = 0; r < 16; ++r) {
+      const int f = 32 * j + 8 * (r >> 2) + 4 * half + (r & 3);
+      Oh[(size_t)f * L + qv] = dropped ? 0.0f : O[j][r] * inv * fast_sigmoid(gv[r]);
     }
   }
 }
 
-hipError_t launch_jeff_bf16_wide(const JeffArgs &a, int rows, const uint16_t *kp, int *flags,
+hipError_t launch_jeff_bf16_wide(const JeffArgs &a, int rows, const uint16_t *kp,
+                                 const int *spans, const uint32_t *kbits, int *flags,
                                  hipStream_t stream) {
   const int hw = wide_heads_per_group(a);
   const int qt = jeff_bf16_wide_query_tile(a);
   const int units = rows * a.kv_heads * (a.heads / a.kv_heads / hw);
-  const unsigned grid = (unsigned)(units * ((a.L + qt - 1) / qt));
-  hipLaunchKernelGGL(jeff_bf16_wide_kernel, dim3(grid), dim3(256), 0, stream, a, kp, flags, rows,
-                     hw);
+  const int nqt = (a.L + qt - 1) / qt;
+  const unsigned grid = (unsigned)(units * ((nqt + 1) / 2));
+  hipLaunchKernelGGL(jeff_bf16_wide_kernel, dim3(grid), dim3(512), 0, stream, a, kp, spans, kbits,
+                     flags, rows, hw);
   return hipGetLastError();
 }
 
