@@ -161,12 +161,11 @@ __device__ void write_row_bits_span(const float *__restrict__ maskr, int L, int 
 // One workgroup = 32 keys; output kp[row][kvh][key][HDP] (zero-padded past
 // hd), written in whole 16-byte chunks. Out: f32, or bf16 (RNE) for the
 // bf16 attention kernel. Every global load (keys, norm weights, RoPE table)
-// is issued before the first is used. With spans set, wavefront 0 of each
-// row's first workgroup also writes the row's active key span and bits.
+// is issued before the first is used. With kbits set, the workgroups of kv
+// head 0 also write their 32 keys' active bits (mask != 0), one word each.
 
 template <int HDP, typename OutT>
 __global__ __launch_bounds__(256) void jeff_k_prep_kernel(const JeffArgs a, OutT *__restrict__ kp,
-                                                          int *__restrict__ spans,
                                                           uint32_t *__restrict__ kbits) {
   constexpr int DP = HDP / 8;  // dims per thread: 8 threads per key
   constexpr int KS = HDP + 1;
@@ -184,8 +183,11 @@ __global__ __launch_bounds__(256) void jeff_k_prep_kernel(const JeffArgs a, OutT
   const bool kin = key < L;
   const bool rope = a.cos_t != nullptr && rh > 0;
   const int start = a.trim ? wave_first_active(a.mask + (size_t)row * L, L, lane) : 0;
-  if (spans != nullptr && blockIdx.x == 0 && kvh == 0 && (tid >> 6) == 0)
-    write_row_bits_span(a.mask + (size_t)row * L, L, lane, row, spans, kbits);
+  if (kbits != nullptr && kvh == 0 && tid < 64) {
+    const float mv = a.mask[(size_t)row * L + min(k0 + lane, L - 1)];
+    const uint64_t bm = __ballot(lane < kKeyTile && k0 + lane < L && mv != 0.0f);
+    if (lane == 0) kbits[(size_t)row * ((L + 31) / 32) + blockIdx.x] = (uint32_t)bm;
+  }
   float xs[DP], wn[DP], c[RT], sn[RT];
 #pragma unroll
   for (int i = 0; i < DP; ++i) {
@@ -1863,7 +1865,7 @@ static hipError_t launch_jeff_f32_hd(const JeffArgs &a, int rows, float *kp, hip
     }
   }
   hipExtLaunchKernelGGL((jeff_k_prep_kernel<HDP, float>), pgrid, dim3(256), 0, stream, ev.start,
-                        nullptr, 0, a, kp, nullptr, nullptr);
+                        nullptr, 0, a, kp, nullptr);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const dim3 block(kJeffF32Waves * 64);
@@ -1906,14 +1908,15 @@ template <int HDP>
 static hipError_t launch_jeff_bf16_hd(const JeffArgs &a, int rows, uint16_t *kp,
                                       hipStream_t stream, const KernelEvents &ev) {
   dim3 pgrid((a.L + kKeyTile - 1) / kKeyTile, a.kv_heads, rows);
-  // The wide bf16 kernel takes the rows' active spans and bits from the prep.
+  // The wide bf16 kernel takes the rows' active key bits from the prep.
   const bool wide = HDP == 256 && jeff_bf16_wide_fits(a);
-  int *spans = wide ? reinterpret_cast<int *>(reinterpret_cast<char *>(kp) +
-                                              jeff_kp_main_bytes(a, rows, HDP, true))
-                    : nullptr;
-  uint32_t *kbits = wide ? reinterpret_cast<uint32_t *>(spans + 2 * rows) : nullptr;
+  uint32_t *kbits =
+      wide ? reinterpret_cast<uint32_t *>(reinterpret_cast<char *>(kp) +
+                                          jeff_kp_main_bytes(a, rows, HDP, true) +
+                                          (size_t)rows * 2 * sizeof(int))
+           : nullptr;
   hipExtLaunchKernelGGL((jeff_k_prep_kernel<HDP, uint16_t>), pgrid, dim3(256), 0, stream, ev.start,
-                        nullptr, 0, a, kp, spans, kbits);
+                        nullptr, 0, a, kp, kbits);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int qsubs = kWavesPerGroup / a.heads_per_group;
@@ -1926,7 +1929,7 @@ static hipError_t launch_jeff_bf16_hd(const JeffArgs &a, int rows, uint16_t *kp,
     // flagged (non-finite values) on a resident grid (two workgroups per CU).
     if (jeff_bf16_wide_fits(a)) {
       int *flags = reinterpret_cast<int *>(reinterpret_cast<char *>(kp) + jeff_bf16_flags_offset(a, rows));
-      e = launch_jeff_bf16_wide(a, rows, kp, spans, kbits, flags, stream);
+      e = launch_jeff_bf16_wide(a, rows, kp, kbits, flags, stream);
       if (e != hipSuccess) return e;
       const int redo_qt = jeff_bf16_wide_query_tile(a);
       const long units = (long)grid.x * grid.y * grid.z;

@@ -157,16 +157,16 @@ size_t jeff_bf16_wide_flag_count(const JeffArgs &a, int rows) {
 
 // Work item p: query tile pair qt2 (longest first), then unit u = (row, kv
 // head, head group); the units of one pair are consecutive, so their K/V
-// streams land on few XCDs and meet in L2. spans / kbits: each row's active
-// key span and one bit per key (jeff_k_prep_kernel).
+// streams land on few XCDs and meet in L2. kbits: one bit per key, mask != 0
+// (jeff_k_prep_kernel).
 __global__ __launch_bounds__(512, 1) void jeff_bf16_wide_kernel(const JeffArgs a,
                                                                 const uint16_t *__restrict__ kp,
-                                                                const int *__restrict__ spans,
                                                                 const uint32_t *__restrict__ kbits,
                                                                 int *__restrict__ flags, int rows,
                                                                 int hw) {
   __shared__ __attribute__((aligned(16))) unsigned char lds[kWideStages * kStage];
   __shared__ int s_flag[2];
+  __shared__ int s_span[2];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // 0..7
@@ -195,11 +195,35 @@ __global__ __launch_bounds__(512, 1) void jeff_bf16_wide_kernel(const JeffArgs a
       static_cast<const uint16_t *>(a.v) + row * a.kv_row + (size_t)kvh * a.kv_head;
   const uint16_t *Kh = kp + ((size_t)row * a.kv_heads + kvh) * (size_t)L * kWideHd;
   float *Oh = a.out + row * a.q_row + (size_t)head * kWideHd * L;
-  const uint32_t *rbits = kbits + (size_t)row * ((L + 31) / 32);
+  const int nw = (L + 31) / 32;
+  const uint32_t *rbits = kbits + (size_t)row * nw;
 
-  // -------- the row's active span: the walk covers its tiles up to the
-  // workgroup's last query (causal).
-  const int first = spans[2 * row], last = spans[2 * row + 1];
+  // -------- the row's active span (first and last key with mask != 0),
+  // from its key bits; the walk covers its tiles up to the workgroup's last
+  // query (causal).
+  if (tid == 0) {
+    s_span[0] = 0x7fffffff;
+    s_span[1] = -1;
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  {
+    int lo = 0x7fffffff, hi = -1;
+    for (int w = tid; w < nw; w += 2 * kWideWaves * 64) {
+      const uint32_t b = rbits[w];
+      if (b != 0) {
+        lo = min(lo, 32 * w + __builtin_ctz(b));
+        hi = max(hi, 32 * w + 31 - __builtin_clz(b));
+      }
+    }
+    lo = wave_min(lo);
+    hi = wave_max(hi);
+    if (lane == 0) {
+      atomicMin(&s_span[0], lo);
+      atomicMax(&s_span[1], hi);
+    }
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  const int last = s_span[1], first = last >= 0 ? s_span[0] : 0;
   const int start = (a.trim && last >= 0) ? first : 0;
   const bool q_live = qv < L && qv >= start;
   const int q_last_wg = min((2 * qt2 + 2) * QT - 1, L - 1);
@@ -544,15 +568,14 @@ __global__ __launch_bounds__(512, 1) void jeff_bf16_wide_kernel(const JeffArgs a
 }
 
 hipError_t launch_jeff_bf16_wide(const JeffArgs &a, int rows, const uint16_t *kp,
-                                 const int *spans, const uint32_t *kbits, int *flags,
-                                 hipStream_t stream) {
+                                 const uint32_t *kbits, int *flags, hipStream_t stream) {
   const int hw = wide_heads_per_group(a);
   const int qt = jeff_bf16_wide_query_tile(a);
   const int units = rows * a.kv_heads * (a.heads / a.kv_heads / hw);
   const int nqt = (a.L + qt - 1) / qt;
   const unsigned grid = (unsigned)(units * ((nqt + 1) / 2));
-  hipLaunchKernelGGL(jeff_bf16_wide_kernel, dim3(grid), dim3(512), 0, stream, a, kp, spans, kbits,
-                     flags, rows, hw);
+  hipLaunchKernelGGL(jeff_bf16_wide_kernel, dim3(grid), dim3(512), 0, stream, a, kp, kbits, flags,
+                     rows, hw);
   return hipGetLastError();
 }
 

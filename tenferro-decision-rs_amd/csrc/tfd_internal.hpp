@@ -121,14 +121,13 @@ hipError_t launch_jeff_attention_bf16(const JeffArgs &a, int rows, int hd_pad, v
 // The bf16 kernel at head dim 256 on the 32x32x16 matrix cores (used by
 // launch_jeff_attention_bf16 when it fits): one flag per (row, head, query
 // tile of jeff_bf16_wide_query_tile) marks tiles left to the exact pass.
-// spans / kbits: the rows' active key spans and bits, written by the K prep.
+// kbits: the rows' active key bits, written by the K prep.
 bool jeff_bf16_wide_fits(const JeffArgs &a);
 int jeff_bf16_wide_query_tile(const JeffArgs &a);
 size_t jeff_bf16_wide_flag_count(const JeffArgs &a, int rows);
 size_t jeff_bf16_flags_offset(const JeffArgs &a, int rows);
 hipError_t launch_jeff_bf16_wide(const JeffArgs &a, int rows, const uint16_t *kp,
-                                 const int *spans, const uint32_t *kbits, int *flags,
-                                 hipStream_t stream);
+                                 const uint32_t *kbits, int *flags, hipStream_t stream);
 
 // Head dims past the tiled kernels (Laya hd > 128, Jeff hd > 256): one
 // wavefront per query in the reference's scalar order. Laya reads `keep`
