@@ -587,9 +587,9 @@ def test_jeff_bf16_kept_nonfinite_values_propagate(gpu_ctx):
     assert np.abs(got[fin] - want[fin]).max() <= BF16_TOL
 
 
-# Head dim 256 with L % 8 == 0 runs the 32x32x16 kernel (4 wavefronts: hw
-# heads of a GQA group x 4/hw blocks of 32 queries); other RoPE widths fall
-# back to the 16x16x32 kernel.
+# Head dim 256 with L % 8 == 0 runs the 32x32x16 kernel (8 wavefronts in two
+# groups, each hw heads of a GQA group x 4/hw blocks of 32 queries); other
+# RoPE widths fall back to the 16x16x32 kernel.
 @pytest.mark.parametrize("length", [8, 40, 96, 264])
 @pytest.mark.parametrize("heads,kv,rot", [(8, 2, 64), (4, 2, 32), (2, 2, 0), (6, 2, 64),
                                           (8, 1, 64), (4, 2, 48)])
@@ -598,6 +598,24 @@ def test_jeff_bf16_hd256_rows_match_oracle(gpu_ctx, length, heads, kv, rot):
     for trim in (False, True):
         bits, vals, qn, kn, mask = bf16_case(7 * length + heads + rot, rows, length, heads, kv, hd,
                                              True)
+        want = oracle.jeff_rows(*vals, qn, kn, mask, rows, length, heads, kv, hd, rot, 1e7, 1e-6,
+                                trim_leading=trim)
+        got = te.jeff_full_attention_rows(*bits, qn, kn, mask, rows, length, heads, kv, hd, rot,
+                                          1e7, 1e-6, trim_leading=trim, bf16=True, ctx=gpu_ctx)
+        assert_close(got, want, BF16_TOL)
+
+
+@pytest.mark.parametrize("length", [72, 200])
+def test_jeff_bf16_hd256_empty_and_sparse_rows(gpu_ctx, length):
+    """Head dim 256, 32x32x16 kernel: a row with no active key (its walk has
+    no tiles), a row with one active key mid-row, and a row whose active keys
+    start in its last tile, against the oracle with and without trim."""
+    rows, heads, kv, hd, rot = 3, 8, 2, 256, 64
+    bits, vals, qn, kn, _ = bf16_case(4242 + length, rows, length, heads, kv, hd, False)
+    mask = np.zeros(rows * length, np.float32)
+    mask[length + length // 2] = 1.0
+    mask[2 * length + length - 5:] = 1.0
+    for trim in (False, True):
         want = oracle.jeff_rows(*vals, qn, kn, mask, rows, length, heads, kv, hd, rot, 1e7, 1e-6,
                                 trim_leading=trim)
         got = te.jeff_full_attention_rows(*bits, qn, kn, mask, rows, length, heads, kv, hd, rot,
