@@ -83,13 +83,15 @@ __device__ __forceinline__ u32x4r rsrc_words(const void *base, uint32_t bytes) {
 // builtin, which the compiler treats as a write to any LDS address: it would
 // make the next LDS operand read wait for every such load issued before it.
 // The walk orders these loads itself (each wavefront waits for its own
-// loads before the barrier that precedes a tile's first read).
+// loads before the barrier that precedes a tile's first read). M0 is a
+// reserved register that the compiler sets right before each of its own
+// uses and never keeps a value in across other code (this kernel has no such
+// use), so it needs no clobber.
 __device__ __forceinline__ void load_lds16(u32x4r r, uint32_t voff, uint32_t soff,
                                            unsigned char *lds_base) {
   const uint32_t m = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)lds_base;
   asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff),
-               "s"(r), "s"(soff), "s"(m)
-               : "m0");
+               "s"(r), "s"(soff), "s"(m));
 }
 
 // This lane's index, recomputed where it is used (two vector instructions,
