@@ -168,7 +168,12 @@ template <int HDP, typename OutT>
 __global__ __launch_bounds__(256) void jeff_k_prep_kernel(const JeffArgs a, OutT *__restrict__ kp,
                                                           uint32_t *__restrict__ kbits) {
   constexpr int DP = HDP / 8;  // dims per thread: 8 threads per key
-  constexpr int KS = HDP + 1;
+  // LDS rows of the tile: feature d of key k at kx(k, d), one pad word after
+  // every 32 features, so that the output loop's lanes (8 consecutive
+  // features each, 32 lanes along one key) hit 32 different banks (with
+  // rows of HDP + 1 they shared 4 of them).
+  constexpr int KS = HDP + HDP / 32 + 1;
+  auto kx = [](int k, int d) { return k * KS + d + (d >> 5); };
   constexpr int RT = (HDP / 2 + 7) / 8;  // RoPE pairs per thread, at most
   __shared__ float Kt[kKeyTile * KS];
   __shared__ float s_red[8 * kKeyTile];
@@ -196,16 +201,30 @@ __global__ __launch_bounds__(256) void jeff_k_prep_kernel(const JeffArgs a, OutT
     const size_t at = kv_off + (kin ? key : 0) + (size_t)L * dc;
     xs[i] = bf ? __uint_as_float((uint32_t)static_cast<const uint16_t *>(a.k)[at] << 16)
                : static_cast<const float *>(a.k)[at];
-    wn[i] = a.k_norm[dc];
+  }
+  // Norm weights: 16 bytes per load when the thread's run is whole and aligned.
+  if (DP % 4 == 0 && part * DP + DP <= hd && (reinterpret_cast<uintptr_t>(a.k_norm) & 15) == 0) {
+#pragma unroll
+    for (int i = 0; i < DP; i += 4) {
+      const f32x4 w4 = *reinterpret_cast<const f32x4 *>(a.k_norm + part * DP + i);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) wn[i + t] = w4[t];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < DP; ++i) wn[i] = a.k_norm[min(part * DP + i, hd - 1)];
   }
   // Thread (kk, part) rotates pairs i = part, part + 8, ... of key k0 + kk.
   const size_t pos = (size_t)min(max(key - start, 0), L - 1) * rh;
   if (rope) {
 #pragma unroll
     for (int u = 0; u < RT; ++u) {
-      const int i = min(part + 8 * u, rh - 1);
-      c[u] = a.cos_t[pos + i];
-      sn[u] = a.sin_t[pos + i];
+      // Only the pairs below rot/2 are rotated (8u < rh: uniform).
+      if (8 * u < rh) {
+        const int i = min(part + 8 * u, rh - 1);
+        c[u] = a.cos_t[pos + i];
+        sn[u] = a.sin_t[pos + i];
+      }
     }
   }
   float ss = 0.0f;
@@ -225,7 +244,7 @@ __global__ __launch_bounds__(256) void jeff_k_prep_kernel(const JeffArgs a, OutT
 #pragma unroll
     for (int i = 0; i < DP; ++i) {
       const int d = part * DP + i;
-      Kt[kk * KS + d] = (kin && d < hd) ? rms_apply(xs[i], scale, wn[i]) : 0.0f;
+      Kt[kx(kk, d)] = (kin && d < hd) ? rms_apply(xs[i], scale, wn[i]) : 0.0f;
     }
   }
   if (rope) {
@@ -234,9 +253,9 @@ __global__ __launch_bounds__(256) void jeff_k_prep_kernel(const JeffArgs a, OutT
     for (int u = 0; u < RT; ++u) {
       const int i = part + 8 * u;
       if (i < rh && kin) {
-        const float x = Kt[kk * KS + i], y = Kt[kk * KS + i + rh];
-        Kt[kk * KS + i] = rope_lo(x, y, c[u], sn[u]);
-        Kt[kk * KS + i + rh] = rope_hi(x, y, c[u], sn[u]);
+        const float x = Kt[kx(kk, i)], y = Kt[kx(kk, i + rh)];
+        Kt[kx(kk, i)] = rope_lo(x, y, c[u], sn[u]);
+        Kt[kx(kk, i + rh)] = rope_hi(x, y, c[u], sn[u]);
       }
     }
   }
@@ -246,7 +265,7 @@ __global__ __launch_bounds__(256) void jeff_k_prep_kernel(const JeffArgs a, OutT
   constexpr int CH = 16 / (int)sizeof(OutT);  // elements per 16-byte chunk
   for (int e = tid; e < nkeys * (HDP / CH); e += 256) {
     const int k2 = e / (HDP / CH), d0 = (e % (HDP / CH)) * CH;
-    const float *src = &Kt[k2 * KS + d0];
+    const float *src = &Kt[kx(k2, d0)];  // d0 .. d0 + CH - 1 share one 32-feature run
     if constexpr (sizeof(OutT) == 2) {
       u16x8 o;
 #pragma unroll
