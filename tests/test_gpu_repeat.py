@@ -1,0 +1,131 @@
+"""Run-to-run equality of the attention kernels at their workload sizes.
+
+Every kernel of the fused path is deterministic: no floating-point atomics,
+a fixed key-tile order per query block, and placement plans and key spans
+derived from the inputs alone. Repeated calls on the same device inputs must
+therefore give bitwise-equal outputs (NaN payloads included). A race in a
+kernel's LDS staging, barriers or workspace reuse shows up here as a
+difference between repeats; the calls of the other configurations run in
+between, so each repeat starts from different cache and workspace contents.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import tenferro_ext as te
+from tenferro_ext.workloads import jeff_config, laya_config
+
+pytestmark = pytest.mark.gpu
+
+REPEATS = 4
+
+
+@pytest.fixture(autouse=True)
+def _announce(request):
+    print(f"\n[gpu] {request.node.nodeid}", flush=True)
+    sys.stdout.flush()
+    yield
+
+
+def _bits(t):
+    import torch
+
+    return t.detach().contiguous().view(torch.int32).cpu().numpy().copy()
+
+
+def _laya_calls(ctx, cfg):
+    """The keep entry and the structured entry of Laya config cfg on device
+    inputs, as zero-argument callables returning the output tensor."""
+    import torch
+
+    w = laya_config(cfg)
+    dev = torch.device("cuda:0")
+    qkv = torch.from_numpy(w.qkv).to(dev)
+    keep = torch.from_numpy(w.keep).to(dev)
+    valid = torch.from_numpy(w.valid).to(dev)
+    shape = (3 * w.hidden, w.length, w.batch)
+    torch.cuda.synchronize()
+    keep_call = lambda: te.laya_attention_block(qkv, keep, w.hidden, w.heads, w.rope_base,
+                                                qkv_shape=shape, ctx=ctx)
+    struct_call = lambda: te.laya_attention_structured(qkv, valid, w.hidden, w.heads, w.length,
+                                                       w.batch, w.window, w.rope_base, ctx=ctx)
+    return [(f"C{cfg} keep", keep_call), (f"C{cfg} structured", struct_call)]
+
+
+def _jeff_call(ctx, cfg, bf16, trim=False):
+    import torch
+
+    w = jeff_config(cfg)
+    dev = torch.device("cuda:0")
+    if bf16:
+        mats = [torch.from_numpy(te.to_bf16_bits(getattr(w, n)).view(np.int16)).to(dev)
+                for n in ("q", "k", "v", "gate")]
+    else:
+        mats = [torch.from_numpy(getattr(w, n)).to(dev) for n in ("q", "k", "v", "gate")]
+    rest = [torch.from_numpy(getattr(w, n)).to(dev) for n in ("q_norm", "k_norm", "mask")]
+    args = (w.rows, w.length, w.heads, w.kv_heads, w.head_dim, w.rotary_dim, w.theta, w.eps)
+    torch.cuda.synchronize()
+    name = f"C{cfg} {'bf16' if bf16 else 'f32'}{' trim' if trim else ''}"
+    return name, lambda: te.jeff_full_attention_rows(*mats, *rest, *args, trim_leading=trim,
+                                                     bf16=bf16, ctx=ctx)
+
+
+def test_workload_configs_repeat_bitwise(gpu_ctx):
+    """C2 and C3 (keep and structured entries), C4 (f32 rows, with and
+    without trim) and C5 (bf16 rows) at full size, each run REPEATS times with
+    the others interleaved: every repeat bitwise equal to the first."""
+    import torch
+
+    calls = _laya_calls(gpu_ctx, 2) + _laya_calls(gpu_ctx, 3)
+    calls += [_jeff_call(gpu_ctx, 4, False), _jeff_call(gpu_ctx, 4, False, trim=True),
+              _jeff_call(gpu_ctx, 5, True)]
+    first = {}
+    for rep in range(REPEATS):
+        for name, fn in calls:
+            print(f"[repeat] {name} #{rep}", flush=True)
+            got = _bits(fn())
+            if rep == 0:
+                first[name] = got
+            else:
+                diff = np.nonzero(got != first[name])[0]
+                assert diff.size == 0, (f"{name}: repeat {rep} differs from the first at "
+                                        f"{diff.size} outputs, e.g. {diff[:8]}")
+    torch.cuda.synchronize()
+
+
+def test_exact_pass_repeat_bitwise(gpu_ctx):
+    """The bf16 head-dim-256 path with non-finite values (tiles handed to the
+    exact pass through the flags workspace), alternated with a clean call on
+    the same context: both bitwise stable across repeats."""
+    import torch
+
+    rows, length, heads, kv, hd, rot = 2, 264, 8, 2, 256, 64
+    rng = np.random.default_rng(5)
+    W, KW = heads * hd, kv * hd
+    q, g = (rng.standard_normal(rows * length * W).astype(np.float32) for _ in range(2))
+    k, v = (rng.standard_normal(rows * length * KW).astype(np.float32) for _ in range(2))
+    qn = (rng.standard_normal(hd) * 0.1).astype(np.float32)
+    kn = (rng.standard_normal(hd) * 0.1).astype(np.float32)
+    mask = np.ones(rows * length, np.float32)
+    mask[:40] = 0.0
+    clean = [te.to_bf16_bits(x) for x in (q, k, v, g)]
+    dirty = [b.copy() for b in clean]
+    Vb = dirty[2].reshape(rows, KW, length)
+    Vb[0, 7, 100] = 0x7F80   # +inf value
+    Vb[1, hd + 3, 200] = 0x7FC0  # NaN value
+    dev = torch.device("cuda:0")
+    to_dev = lambda bits: [torch.from_numpy(b.view(np.int16)).to(dev) for b in bits]
+    rest = [torch.from_numpy(x).to(dev) for x in (qn, kn, mask)]
+    args = (rows, length, heads, kv, hd, rot, 1e7, 1e-6)
+    cases = {"clean": to_dev(clean), "dirty": to_dev(dirty)}
+    torch.cuda.synchronize()
+    first = {}
+    for rep in range(REPEATS):
+        for name, mats in cases.items():
+            got = _bits(te.jeff_full_attention_rows(*mats, *rest, *args, bf16=True, ctx=gpu_ctx))
+            if rep == 0:
+                first[name] = got
+            else:
+                assert np.array_equal(got, first[name]), f"{name}: repeat {rep} differs"
+    assert not np.array_equal(first["clean"], first["dirty"])
