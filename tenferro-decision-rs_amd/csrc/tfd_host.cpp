@@ -219,12 +219,21 @@ int rope_table(tfd_ctx *c, int kind, size_t length, size_t dim, float base, uint
   ent.dim = dim;
   ent.bits = bits;
   ent.bytes = 2 * sizeof(float) * ct.size();
-  TFD_HIP(c, hipMalloc((void **)&ent.cos_d, sizeof(float) * ct.size()), "hipMalloc");
-  TFD_HIP(c, hipMalloc((void **)&ent.sin_d, sizeof(float) * st.size()), "hipMalloc");
-  TFD_HIP(c, hipMemcpy(ent.cos_d, ct.data(), sizeof(float) * ct.size(), hipMemcpyHostToDevice),
-          "hipMemcpy rope");
-  TFD_HIP(c, hipMemcpy(ent.sin_d, st.data(), sizeof(float) * st.size(), hipMemcpyHostToDevice),
-          "hipMemcpy rope");
+  // Allocate and upload both tables; on any failure free what was allocated.
+  const char *what = "hipMalloc";
+  hipError_t e = hipMalloc((void **)&ent.cos_d, sizeof(float) * ct.size());
+  if (e == hipSuccess) e = hipMalloc((void **)&ent.sin_d, sizeof(float) * st.size());
+  if (e == hipSuccess) {
+    what = "hipMemcpy rope";
+    e = hipMemcpy(ent.cos_d, ct.data(), sizeof(float) * ct.size(), hipMemcpyHostToDevice);
+  }
+  if (e == hipSuccess)
+    e = hipMemcpy(ent.sin_d, st.data(), sizeof(float) * st.size(), hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    if (ent.cos_d) (void)hipFree(ent.cos_d);
+    if (ent.sin_d) (void)hipFree(ent.sin_d);
+    return hip_fail(c, e, what);
+  }
   ent.stamp = ++c->clock;
   c->rope.push_back(ent);
   *cos_d = ent.cos_d;
