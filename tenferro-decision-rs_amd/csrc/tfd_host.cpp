@@ -17,6 +17,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -244,9 +245,13 @@ int rope_table(tfd_ctx *c, int kind, size_t length, size_t dim, float base, uint
 // The no-allocation entry's RoPE tables: computed on the host exactly as
 // rope_table() does, into a static host buffer, and copied into the start of
 // the device scratch; the (length, dim, base) last copied to each device is
-// remembered, and an unchanged table is not copied again.
+// remembered, and an unchanged table is not copied again. One host buffer
+// serves every device, so building and copying a table holds a lock (calls
+// on different GPUs from different threads would otherwise overwrite each
+// other's table before its copy drains).
 constexpr size_t kNoallocRopeMax = (size_t)1 << 19;  // floats per table (L * hd / 2)
 float g_noalloc_rope_host[2 * kNoallocRopeMax];
+std::mutex g_noalloc_rope_lock;
 struct NoallocRopeKey {
   bool valid = false;
   size_t length = 0, dim = 0;
@@ -259,6 +264,7 @@ int noalloc_rope_table(tfd_ctx *c, size_t length, size_t dim, float base, uint32
   const size_t half = dim / 2, n = length * half;
   *cos_d = dev;
   *sin_d = dev + n;
+  std::lock_guard<std::mutex> guard(g_noalloc_rope_lock);
   NoallocRopeKey &key = g_noalloc_rope_key[c->device];
   if (key.valid && key.length == length && key.dim == dim && key.bits == bits) return TFD_OK;
   key.valid = false;
