@@ -129,3 +129,37 @@ def test_exact_pass_repeat_bitwise(gpu_ctx):
             else:
                 assert np.array_equal(got, first[name]), f"{name}: repeat {rep} differs"
     assert not np.array_equal(first["clean"], first["dirty"])
+
+
+def test_two_contexts_interleaved_match_one(gpu_ctx):
+    """Two more library contexts on the same GPU, each with its own stream,
+    workspace and RoPE-table cache, their calls alternated and enqueued
+    without waiting (TFD_ASYNC): every output bitwise equal to the same call
+    run synchronously on the session's context. Nothing the library keeps per
+    context (packed keep words, tile maps, prepared keys, tables) leaks
+    between contexts or calls."""
+    import torch
+
+    ctx_a, ctx_b = te.Context(0), te.Context(0)
+    try:
+        runs = {}
+        for label, ctx in (("session", gpu_ctx), ("a", ctx_a), ("b", ctx_b)):
+            calls = _laya_calls(ctx, 2) + _laya_calls(ctx, 3)
+            calls += [_jeff_call(ctx, 4, False, trim=True), _jeff_call(ctx, 5, True)]
+            runs[label] = calls
+        want = {name: _bits(fn()) for name, fn in runs["session"]}
+        outs = {}
+        with te.asynchronous():
+            # Context b runs the configurations in the opposite order.
+            for (name_a, fa), (name_b, fb) in zip(runs["a"], runs["b"][::-1]):
+                outs[("a", name_a)] = fa()
+                outs[("b", name_b)] = fb()
+        ctx_a.synchronize()
+        ctx_b.synchronize()
+        torch.cuda.synchronize()
+        for (label, name), t in outs.items():
+            print(f"[contexts] {label} {name}", flush=True)
+            assert np.array_equal(_bits(t), want[name]), f"context {label}: {name} differs"
+    finally:
+        ctx_a.close()
+        ctx_b.close()
