@@ -86,7 +86,8 @@ __device__ __forceinline__ u32x4r rsrc_words(const void *base, uint32_t bytes) {
 // loads before the barrier that precedes a tile's first read). M0 is a
 // reserved register that the compiler sets right before each of its own
 // uses and never keeps a value in across other code (this kernel has no such
-// use), so it needs no clobber.
+// use; tests/test_kernel_asm.py checks the compiled kernel for it), so it
+// needs no clobber.
 __device__ __forceinline__ void load_lds16(u32x4r r, uint32_t voff, uint32_t soff,
                                            unsigned char *lds_base) {
   const uint32_t m = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)lds_base;
