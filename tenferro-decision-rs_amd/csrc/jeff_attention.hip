@@ -159,8 +159,10 @@ __device__ void write_row_bits_span(const float *__restrict__ maskr, int L, int 
 // RMSNorm (lib.rs:676-691) and partial RoPE (692-709) of every key of one
 // (row, kv head) once per call, so attention workgroups stage finished keys.
 // One workgroup = 32 keys; output kp[row][kvh][key][HDP] (zero-padded past
-// hd), written in whole 16-byte chunks. Out: f32, or bf16 (RNE) for the
-// bf16 attention kernel. Every global load (keys, norm weights, RoPE table)
+// hd), written in whole 16-byte chunks. Out: f32, or for the bf16 attention
+// kernels fp16 (RNE) of the key times 2^-e, e = norm_weight_exp(k_norm): the
+// Q.K^T product of those kernels takes fp16 operands. Every global load
+// (keys, norm weights, RoPE table)
 // is issued before the first is used. With kbits set, the workgroups of kv
 // head 0 also write their 32 keys' active bits (mask != 0), one word each.
 
@@ -262,6 +264,7 @@ __global__ __launch_bounds__(256) void jeff_k_prep_kernel(const JeffArgs a, OutT
   __syncthreads();
   OutT *dst = kp + (((size_t)row * a.kv_heads + kvh) * L + k0) * HDP;
   const int nkeys = min(kKeyTile, L - k0);
+  const float ksig = bf ? ldexpf(1.0f, -norm_weight_exp(a.k_norm, hd, lane)) : 1.0f;
   constexpr int CH = 16 / (int)sizeof(OutT);  // elements per 16-byte chunk
   for (int e = tid; e < nkeys * (HDP / CH); e += 256) {
     const int k2 = e / (HDP / CH), d0 = (e % (HDP / CH)) * CH;
@@ -269,10 +272,7 @@ __global__ __launch_bounds__(256) void jeff_k_prep_kernel(const JeffArgs a, OutT
     if constexpr (sizeof(OutT) == 2) {
       u16x8 o;
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        const __bf16 h = (__bf16)src[t];
-        o[t] = *reinterpret_cast<const unsigned short *>(&h);
-      }
+      for (int t = 0; t < 8; ++t) o[t] = f32_to_f16_bits(src[t] * ksig);
       *reinterpret_cast<u16x8 *>(dst + (size_t)k2 * HDP + d0) = o;
     } else {
       const f32x4 o = {src[0], src[1], src[2], src[3]};
@@ -1513,8 +1513,10 @@ __host__ __device__ constexpr int jeff_bf16_smem_bytes() {
 }
 
 // Same arithmetic as jeff_attention_f32_kernel with q, k, v and gate in bf16:
-// normalized/rotated q and k and the probabilities are rounded to bf16 for
-// v_mfma_f32_16x16x32_bf16; softmax, accumulation and output stay f32.
+// normalized/rotated q and k, scaled by powers of two (norm_weight_exp), are
+// rounded to fp16 for S^T on v_mfma_f32_16x16x32_f16, and the probabilities
+// to bf16 for P.V on v_mfma_f32_16x16x32_bf16 (V stays bf16); the row sum l
+// adds the rounded probabilities; softmax, accumulation and output stay f32.
 // A 32-key tile is two 16-key S^T blocks (lane group g holds keys 4g + r and
 // 16 + 4g + r of its query), which together are exactly the B operand of one
 // P.V MFMA per 16-row block of O^T.
@@ -1592,8 +1594,12 @@ __device__ __forceinline__ void jeff_bf16_unit(const JeffArgs &a, const uint16_t
   }
 
   // -------- Q: RMSNorm + partial RoPE in f32 (wave-local LDS phases), then
-  // rounded to bf16: lane (col, grp) holds Q[q][32*s + 8*grp + e] in qb[s].
-  bf16x8 qb[QS8];
+  // scaled by 2^-e_q and rounded to fp16 (the prepared keys are fp16 with
+  // 2^-e_k): lane (col, grp) holds Q[q][32*s + 8*grp + e] in qb[s].
+  const int eq = norm_weight_exp(a.q_norm, hd, lane);
+  const float qsig = ldexpf(1.0f, -eq);
+  const float c1 = ldexpf(a.c1, eq + norm_weight_exp(a.k_norm, hd, lane));
+  f16x8 qb[QS8];
   const bool q_live = qin && q >= start;
   {
     float *qw = qscr + wave * (kJeffWaveQueries * QP);
@@ -1653,7 +1659,7 @@ __device__ __forceinline__ void jeff_bf16_unit(const JeffArgs &a, const uint16_t
 #pragma unroll
     for (int s = 0; s < QS8; ++s)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) qb[s][e] = (__bf16)qs[32 * s + 8 * grp + e];
+      for (int e = 0; e < 8; ++e) qb[s][e] = (_Float16)(qs[32 * s + 8 * grp + e] * qsig);
   }
   __syncthreads();  // the Q scratch becomes the K/V buffers
 
@@ -1707,12 +1713,13 @@ __device__ __forceinline__ void jeff_bf16_unit(const JeffArgs &a, const uint16_t
       const uint16_t *k1row = Kc + (16 + col) * KSB + 8 * grp;
 #pragma unroll
       for (int st8 = 0; st8 < QS8; ++st8) {
-        const bf16x8 ka = *reinterpret_cast<const bf16x8 *>(k0row + 32 * st8);
-        const bf16x8 kb = *reinterpret_cast<const bf16x8 *>(k1row + 32 * st8);
-        s0 = mfma_16x16x32_bf16(ka, qb[st8], s0);
-        s1 = mfma_16x16x32_bf16(kb, qb[st8], s1);
+        const f16x8 ka = *reinterpret_cast<const f16x8 *>(k0row + 32 * st8);
+        const f16x8 kb = *reinterpret_cast<const f16x8 *>(k1row + 32 * st8);
+        s0 = mfma_16x16x32_f16(ka, qb[st8], s0);
+        s1 = mfma_16x16x32_f16(kb, qb[st8], s1);
       }
-      const float alpha = softmax_tile16(s0, s1, w, grp, a.c1, m, l);
+      // The probabilities are summed as the bf16 values P.V consumes.
+      const float alpha = softmax_tile16<true>(s0, s1, w, grp, c1, m, l);
       if (alpha != 1.0f) {
 #pragma unroll
         for (int j = 0; j < NB; ++j) O[j] *= alpha;

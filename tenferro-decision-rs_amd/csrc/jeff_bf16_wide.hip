@@ -1,6 +1,11 @@
 // Jeff full attention, bf16 variant at head dim 256 (cpu-kernels
 // jeff_full_attention_into, crates/cpu-kernels/src/lib.rs:609-763, with q, k,
-// v and gate held in bf16), on the 32x32x16 bf16 matrix cores of gfx950.
+// v and gate held in bf16), on the 32x32x16 matrix cores of gfx950: S^T on
+// fp16 operands (normalized, rotated q and k scaled by powers of two,
+// norm_weight_exp), P.V on bf16 operands (V as given). fp16 rounds q and k
+// 8x finer than bf16: with bf16 scores a query that keeps two keys missed
+// 1e-2 by up to 22% (V ~ N(0, 1)); the row sum adds the bf16-rounded
+// probabilities P.V consumes, so the output is a convex combination of V.
 //
 // One workgroup = 8 wavefronts on one kv head, one workgroup per CU (two
 // wavefronts per SIMD, 256 registers each), in two groups of four. A group
@@ -10,7 +15,7 @@
 // share every 32-key tile of K and V staged in LDS. Each wavefront owns one
 // block of 32 queries of one head and walks the key tiles:
 //   S^T (32 keys x 32 queries) = K_tile . Q^T  (16 MFMAs, K from LDS, Q^T in
-//                                               registers as bf16 B operands)
+//                                               registers as fp16 B operands)
 //   online softmax in the log2 domain against a lazily moved reference
 //   O^T (256 x 32) += V_tile^T . P^T           (16 MFMAs, V from LDS)
 // The walk runs in phases separated by workgroup barriers. A wavefront's
@@ -68,6 +73,9 @@ constexpr float kLazyLimit16 = 4096.0f;
 
 __device__ __forceinline__ f32x16 mfma_32x32x16_bf16(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma_32x32x16_f16(f16x8 a, f16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
 // A buffer resource as four scalar words (raw buffer, no swizzle).
@@ -129,6 +137,21 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   typedef float f32x2 __attribute__((ext_vector_type(2)));
   typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
+}
+
+// Sum of the 16 bf16 values packed two per word in g, in f32 (each half
+// moved into the high half of a word is that value as an f32; two chains):
+// the row sum of exactly the probabilities the P.V product consumes. (One
+// v_dot2 per word against 1.0 does the same in fewer instructions but
+// measured 4% slower on C5.)
+__device__ __forceinline__ float sum_bf16x16(const uint32_t (&g)[8]) {
+  float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    s0 += __uint_as_float(g[i] << 16);
+    s1 += __uint_as_float(g[i] & 0xffff0000u);
+  }
+  return s0 + s1;
 }
 
 // Heads per group: 4, 2 or 1, whichever divides the GQA group size.
@@ -242,10 +265,14 @@ __global__ __launch_bounds__(512, 1) void jeff_bf16_wide_kernel(const JeffArgs a
   const bool w_full = q0w >= start && q0w + 32 <= L;
 
   // -------- Q: RMSNorm (lib.rs:676-691) and partial RoPE (692-709) in f32,
-  // rounded to bf16 B operands: lane (col, half) holds features
+  // times 2^-e_q, rounded to fp16 B operands (the prepared keys are fp16
+  // times 2^-e_k; norm_weight_exp): lane (col, half) holds features
   // 16s + 8*half + e of query qv in qb[s]. RoPE partners (i, i + rot/2) sit
   // in the same lane, rot/32 steps apart.
-  bf16x8 qb[16];
+  const int eq = norm_weight_exp(a.q_norm, kWideHd, lane);
+  const float qsig = ldexpf(1.0f, -eq);
+  const float c1 = ldexpf(a.c1, eq + norm_weight_exp(a.k_norm, kWideHd, lane));
+  f16x8 qb[16];
   const int rh = a.cos_t != nullptr ? a.rot_half : 0;
   {
     const int qc = min(qv, L - 1);
@@ -291,7 +318,7 @@ __global__ __launch_bounds__(512, 1) void jeff_bf16_wide_kernel(const JeffArgs a
 #pragma unroll
     for (int s = 0; s < 16; ++s)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) qb[s][e] = (__bf16)(q_live ? y[s][e] : 0.0f);
+      for (int e = 0; e < 8; ++e) qb[s][e] = (_Float16)(q_live ? y[s][e] * qsig : 0.0f);
   }
 
   // -------- staging of local tile j (keys 32 (kt_begin + j) ..) into buffer
@@ -351,7 +378,6 @@ __global__ __launch_bounds__(512, 1) void jeff_bf16_wide_kernel(const JeffArgs a
 #pragma unroll
     for (int r = 0; r < 16; ++r) O[j][r] = 0.0f;
   float m = kNoMax, l = 0.0f;
-  const float c1 = a.c1;
   bool tainted = false;  // wave-uniform
   f32x16 st = {};
   bf16x8 pb[2] = {};
@@ -368,12 +394,14 @@ __global__ __launch_bounds__(512, 1) void jeff_bf16_wide_kernel(const JeffArgs a
   int kw = w_live ? max(kt_w_end - kt_begin, 0) : 0;
 
   // -------- the softmax of local tile k (scores in st) into the P^T
-  // operands pb (lib.rs:712-730), against the reference m.
+  // operands pb (lib.rs:712-730), against the reference m. The row sum l
+  // adds the bf16-rounded terms that P.V consumes, so that O / l is a convex
+  // combination of V, as the reference's p = e / sum is (lib.rs:731-754).
   auto softmax = [&](int k) {
     const int kt = kt_begin + k, k0 = kt * kWideKeys;
     const uint32_t wact = rbits[kt];
     float e[16];
-    float rs = 0.0f;
+    uint32_t g[8];
     const uint32_t keep = q_live ? (wact & range_bits(0, qv - k0)) : 0u;
     const uint32_t kh = keep >> (4 * half);  // bit 8g + r: key 8g + 4*half + r
     const bool full = w_full && wact == 0xffffffffu && k0 + kWideKeys - 1 <= q0w;
@@ -382,17 +410,15 @@ __global__ __launch_bounds__(512, 1) void jeff_bf16_wide_kernel(const JeffArgs a
     // in st[4g + r'].
     if (full) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        e[r] = fast_exp2(__builtin_fmaf(st[r], c1, -m));
-        rs += e[r];
-      }
+      for (int r = 0; r < 16; ++r) e[r] = fast_exp2(__builtin_fmaf(st[r], c1, -m));
     } else {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
+      for (int r = 0; r < 16; ++r)
         e[r] = bit(kh, r) ? fast_exp2(__builtin_fmaf(st[r], c1, -m)) : 0.0f;
-        rs += e[r];
-      }
     }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) g[i] = pack_bf16x2(e[2 * i], e[2 * i + 1]);
+    float rs = sum_bf16x16(g);
     if (__ballot(q_live && !(rs <= kLazyLimit16)) != 0) {
       // Rare: a score far above the reference (or non-finite). Move the
       // reference to the tile's maximum and redo the terms; -inf scores and
@@ -406,15 +432,16 @@ __global__ __launch_bounds__(512, 1) void jeff_bf16_wide_kernel(const JeffArgs a
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, kept(r) ? st[r] : -INFINITY);
       const float mxs = pair_max(mx) * c1;
       const float mn = mxs > m + kRescaleSlack ? mxs : m;
-      rs = 0.0f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const float x = st[r];
         e[r] = (!kept(r) || (__builtin_isinf(x) && x < 0.0f))
                    ? 0.0f
                    : fast_exp2(__builtin_fmaf(x, c1, -mn));
-        rs += e[r];
       }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) g[i] = pack_bf16x2(e[2 * i], e[2 * i + 1]);
+      rs = sum_bf16x16(g);
       if (__ballot(q_live && !__builtin_isfinite(rs)) != 0) {
         tainted = true;
         kw = 0;
@@ -432,9 +459,6 @@ __global__ __launch_bounds__(512, 1) void jeff_bf16_wide_kernel(const JeffArgs a
     // P^T as the B operand of O^T += V^T . P^T: lane (col, half) needs keys
     // 8*half .. 8*half + 7 of each 16-key half hh; it holds keys 4*half + r'
     // of each 8-key group. One permlane32 swap per pair of 8-key groups.
-    uint32_t g[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) g[i] = pack_bf16x2(e[2 * i], e[2 * i + 1]);
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
       uint32_t w[4];
@@ -482,8 +506,8 @@ __global__ __launch_bounds__(512, 1) void jeff_bf16_wide_kernel(const JeffArgs a
       st = f32x16{};
 #pragma unroll
       for (int s = 0; s < 16; ++s) {
-        const bf16x8 ka = *reinterpret_cast<const bf16x8 *>(Kb + kbase + s * 512);
-        st = mfma_32x32x16_bf16(ka, qb[s], st);
+        const f16x8 ka = *reinterpret_cast<const f16x8 *>(Kb + kbase + s * 512);
+        st = mfma_32x32x16_f16(ka, qb[s], st);
       }
       pipeline_reads<16>();
     }
@@ -509,8 +533,8 @@ __global__ __launch_bounds__(512, 1) void jeff_bf16_wide_kernel(const JeffArgs a
       O[1] = mfma_32x32x16_bf16(vpre1, pb[0], O[1]);
 #pragma unroll
       for (int s = 0; s < 16; ++s) {
-        const bf16x8 ka = *reinterpret_cast<const bf16x8 *>(Kb + kbase + s * 512);
-        st = mfma_32x32x16_bf16(ka, qb[s], st);
+        const f16x8 ka = *reinterpret_cast<const f16x8 *>(Kb + kbase + s * 512);
+        st = mfma_32x32x16_f16(ka, qb[s], st);
         if (s < 14) {
           const int q = s + 2;
           const bf16x8 va = *reinterpret_cast<const bf16x8 *>(Vb + vbase + kPj[q] * 2 * kVBlock +

@@ -9,6 +9,7 @@ namespace tfd {
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
 typedef unsigned short u16x4 __attribute__((ext_vector_type(4)));
 
@@ -30,6 +31,11 @@ __device__ __forceinline__ f32x4 mfma_16x16x4(float a, float b, f32x4 c) {
 // accumulator r holds D[4*(l/16) + r][l%16].
 __device__ __forceinline__ f32x4 mfma_16x16x32_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// The same product with fp16 operands (same lane layout).
+__device__ __forceinline__ f32x4 mfma_16x16x32_f16(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
 __device__ __forceinline__ float bf16_to_f32(unsigned short h) {
@@ -129,6 +135,36 @@ __device__ __forceinline__ void buffer_store4(f32x4 v, __amdgpu_buffer_rsrc_t r,
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, v), r, voff, soff, 0);
 }
 
+__device__ __forceinline__ float wave_max_f(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+// Exponent e of a power-of-two factor 2^-e for the fp16 Q.K^T operands of
+// the bf16 Jeff kernels: max_i |1 + w_i| * 2^-e lies in [0.5, 1) (e clamped
+// to [-64, 64]; e = 0 when the max is 0 or not finite). After the centered
+// RMSNorm |x_i * scale| <= sqrt(hd), and RoPE keeps each pair's norm, so a
+// normalized, rotated q or k times 2^-e stays below sqrt(hd) <= 16 for
+// hd <= 256: inside fp16's range, with a relative rounding of 2^-11 instead
+// of bf16's 2^-8. Scaling by a power of two is exact; the scores come back
+// through c1 * 2^(e_q + e_k). Every lane of the wavefront takes part and
+// gets the same e.
+__device__ __forceinline__ int norm_weight_exp(const float *__restrict__ w, int hd, int lane) {
+  float mx = 0.0f;
+  for (int i = lane; i < hd; i += 64) mx = fmaxf(mx, fabsf(1.0f + w[i]));
+  mx = wave_max_f(mx);
+  if (!(mx > 0.0f) || !__builtin_isfinite(mx)) return 0;
+  int e;
+  (void)frexpf(mx, &e);
+  return __builtin_amdgcn_readfirstlane(e < -64 ? -64 : (e > 64 ? 64 : e));
+}
+
+__device__ __forceinline__ unsigned short f32_to_f16_bits(float x) {
+  const _Float16 h = (_Float16)x;
+  return __builtin_bit_cast(unsigned short, h);
+}
+
 __device__ __forceinline__ int wave_min(int v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o));
@@ -189,6 +225,10 @@ __device__ __forceinline__ float tile_prob(const f32x16 &s, int kk, int col) {
 // softmax_tile for the 16x16 layout: a 32-key tile is two S^T blocks,
 // s0 (keys 0..15) and s1 (keys 16..31); lane group g = lane/16 holds keys
 // 16*b + 4*g + r of its query lane%16.
+// With ROUND_BF16 the probabilities are rounded to bf16 (nearest even) before
+// they are summed, so that l is the sum of exactly the values a bf16 P.V
+// product consumes and O / l stays a convex combination of V.
+template <bool ROUND_BF16 = false>
 __device__ __forceinline__ float softmax_tile16(f32x4 &s0, f32x4 &s1, uint32_t keep, int grp,
                                                 float c1, float &m, float &l) {
   float mx = -INFINITY;
@@ -208,8 +248,12 @@ __device__ __forceinline__ float softmax_tile16(f32x4 &s0, f32x4 &s1, uint32_t k
   float rs = 0.0f;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const float e0 = __builtin_isfinite(s0[r]) ? fast_exp2(s0[r] - mn) : 0.0f;
-    const float e1 = __builtin_isfinite(s1[r]) ? fast_exp2(s1[r] - mn) : 0.0f;
+    float e0 = __builtin_isfinite(s0[r]) ? fast_exp2(s0[r] - mn) : 0.0f;
+    float e1 = __builtin_isfinite(s1[r]) ? fast_exp2(s1[r] - mn) : 0.0f;
+    if (ROUND_BF16) {
+      e0 = bf16_to_f32(f32_to_bf16(e0));
+      e1 = bf16_to_f32(f32_to_bf16(e1));
+    }
     s0[r] = e0;
     s1[r] = e1;
     rs += e0 + e1;
