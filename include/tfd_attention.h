@@ -122,19 +122,28 @@ int tfd_laya_attention_block_f32(tfd_ctx *ctx, const float *qkv, const size_t *q
 
 /*
  * The Laya drop-in without any allocation (no counterpart in the reference:
- * an entry for callers that cannot allocate device memory -- code under HIP
- * graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * an entry for callers that cannot allocate device memory -- tight serving
+ * loops, harnesses that forbid hipMalloc, code under HIP graph capture).
  * Same arguments, checks and results as tfd_laya_attention_block_f32, but:
  *   - operands must be device pointers (TFD_DEVICE_PTRS; TFD_ASYNC allowed);
- *   - its workspace (RoPE tables, packed keep words, tile map) lives in one
- *     static 16 MiB device array per GPU, held until the process ends: it
- *     needs 4*L*hd + 4*L*B*ceil(L/32) bytes plus a small tile map (L 2048,
- *     B 8, hd 128: 5 MiB); a call that needs more returns TFD_EUNSUPPORTED
- *     before any device access;
+ *   - its workspace lives in one static 16 MiB device array per GPU, held
+ *     until the process ends: a 4 MiB region for the RoPE tables (L*hd/2 <=
+ *     2^19), then the packed keep words and tile map, 4*L*B*ceil(L/32)
+ *     bytes plus a small map, which must fit the other 12 MiB (L 2048, B 8:
+ *     4 MiB); a call that needs more returns TFD_EUNSUPPORTED before any
+ *     device access;
  *   - no timing events are recorded (tfd_ctx_set_timing is ignored).
  * Every call on a GPU shares that GPU's array: calls that overlap on one GPU
  * (several threads or streams) race. A context made by tfd_ctx_create creates
  * its stream on first use; tfd_ctx_create_on_stream adopts the caller's.
+ * The RoPE table of the last (L, hd, rope_base) used on a GPU stays resident;
+ * a call with another one uploads its table from the host and synchronizes
+ * the stream. Under stream capture: pass TFD_ASYNC (else TFD_EINVAL), and make
+ * one eager call with the same (L, hd, rope_base) first (else
+ * TFD_EUNSUPPORTED: the upload cannot be captured). The captured kernels read
+ * whichever table is resident when the graph is launched, so replays must not
+ * interleave with calls of another (L, hd, rope_base) on that GPU; calls with
+ * rope_base 0 leave the table in place.
  */
 int tfd_laya_attention_block_noalloc_f32(tfd_ctx *ctx, const float *qkv, const size_t *qkv_shape,
                                          size_t qkv_rank, size_t qkv_len, const uint8_t *keep,

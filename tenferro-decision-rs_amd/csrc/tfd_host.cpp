@@ -243,13 +243,21 @@ int rope_table(tfd_ctx *c, int kind, size_t length, size_t dim, float base, uint
 }
 
 // The no-allocation entry's RoPE tables: computed on the host exactly as
-// rope_table() does, into a static host buffer, and copied into the start of
-// the device scratch; the (length, dim, base) last copied to each device is
-// remembered, and an unchanged table is not copied again. One host buffer
-// serves every device, so building and copying a table holds a lock (calls
-// on different GPUs from different threads would otherwise overwrite each
-// other's table before its copy drains).
+// rope_table() does, into a static host buffer, and copied into the first
+// kNoallocRopeBytes of the device scratch, a region nothing else writes (the
+// packed keep words and tile map start after it, also on calls with RoPE
+// off); the (length, dim, base) last copied to each device is remembered,
+// and an unchanged table is not copied again. One host buffer serves every
+// device, so building and copying a table holds a lock (calls on different
+// GPUs from different threads would otherwise overwrite each other's table
+// before its copy drains). A new table needs a host copy and a stream
+// synchronization, which a stream under graph capture cannot take: such a
+// call is refused, and one eager call with the same (length, dim, base)
+// makes the table resident first.
 constexpr size_t kNoallocRopeMax = (size_t)1 << 19;  // floats per table (L * hd / 2)
+constexpr size_t kNoallocRopeBytes = 2 * kNoallocRopeMax * sizeof(float);  // 4 MiB
+static_assert(kNoallocRopeBytes % 256 == 0 && kNoallocRopeBytes < tfd::kNoallocScratchBytes,
+              "the RoPE region leaves room for the keep words");
 float g_noalloc_rope_host[2 * kNoallocRopeMax];
 std::mutex g_noalloc_rope_lock;
 struct NoallocRopeKey {
@@ -267,6 +275,14 @@ int noalloc_rope_table(tfd_ctx *c, size_t length, size_t dim, float base, uint32
   std::lock_guard<std::mutex> guard(g_noalloc_rope_lock);
   NoallocRopeKey &key = g_noalloc_rope_key[c->device];
   if (key.valid && key.length == length && key.dim == dim && key.bits == bits) return TFD_OK;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  TFD_HIP(c, hipStreamIsCapturing(c->stream, &cap), "hipStreamIsCapturing");
+  if (cap != hipStreamCaptureStatusNone)
+    return fail(c, TFD_EUNSUPPORTED,
+                "tfd_laya_attention_block_noalloc_f32: the RoPE table for (length %zu, head_dim "
+                "%zu) and this base is not resident and cannot be uploaded under stream capture; "
+                "make one call with the same length, head_dim and rope_base before capturing",
+                length, dim);
   key.valid = false;
   for (size_t l = 0; l < length; ++l) {
     for (size_t i = 0; i < half; ++i) {
@@ -352,14 +368,12 @@ int laya_run(tfd_ctx *c, const char *op, const float *qkv, const uint8_t *keep,
     return fail(c, TFD_EUNSUPPORTED, "%s: length/hidden too large for the kernels", op);
   if (heads > 65535 || batch > 65535 || (length + tfd::kKeyTile - 1) / tfd::kKeyTile > 65535)
     return fail(c, TFD_EUNSUPPORTED, "%s: heads/batch/length exceed the launch grid", op);
-  // No-allocation layout: the RoPE tables (2 * L * hd/2 floats, rounded up
-  // to 256 bytes), then the packed keep words and the tile map.
+  // No-allocation layout: the RoPE region (kNoallocRopeBytes, whether or not
+  // this call uses RoPE), then the packed keep words and the tile map.
   const size_t nkt = (length + tfd::kKeyTile - 1) / tfd::kKeyTile;
-  const size_t rope_bytes =
-      (bits_to_f32(rope_bits) != 0.0f && !zero_fill) ? ((2 * length * (hd / 2) * 4 + 255) & ~(size_t)255) : 0;
   if (noalloc) {
     const size_t words = nkt * batch * length, groups = (size_t)tfd::laya_map_row((int)nkt) * batch * ((length + 63) / 64);
-    const size_t need = rope_bytes + ((sizeof(uint32_t) * words + 255) & ~(size_t)255) + groups;
+    const size_t need = kNoallocRopeBytes + ((sizeof(uint32_t) * words + 255) & ~(size_t)255) + groups;
     if (length * (hd / 2) > kNoallocRopeMax || need > tfd::kNoallocScratchBytes)
       return fail(c, TFD_EUNSUPPORTED,
                   "%s: needs %zu bytes of workspace; this entry has %zu (use "
@@ -369,6 +383,11 @@ int laya_run(tfd_ctx *c, const char *op, const float *qkv, const uint8_t *keep,
   if (rc) return rc;
   unsigned char *scratch = nullptr;
   if (noalloc) {
+    // A stream under graph capture records work and cannot synchronize.
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    TFD_HIP(c, hipStreamIsCapturing(c->stream, &cap), "hipStreamIsCapturing");
+    if (cap != hipStreamCaptureStatusNone && !(flags & TFD_ASYNC))
+      return invalid(c, op, "flags", "a call under stream capture needs TFD_ASYNC");
     hipError_t e = hipSuccess;
     scratch = static_cast<unsigned char *>(tfd::noalloc_scratch(c->device, &e));
     if (!scratch) return hip_fail(c, e, "hipGetSymbolAddress(scratch)");
@@ -431,7 +450,7 @@ int laya_run(tfd_ctx *c, const char *op, const float *qkv, const uint8_t *keep,
     const size_t map_off = (sizeof(uint32_t) * words + 255) & ~(size_t)255;
     uint8_t *base = nullptr;
     if (noalloc) {
-      base = scratch + rope_bytes;
+      base = scratch + kNoallocRopeBytes;
     } else {
       if ((rc = reserve(c, c->bits, map_off + groups))) return rc;
       base = static_cast<uint8_t *>(c->bits.ptr);
@@ -453,7 +472,7 @@ int laya_run(tfd_ctx *c, const char *op, const float *qkv, const uint8_t *keep,
       const size_t groups = (size_t)tfd::laya_map_row(a.nkt) * batch * ((length + 63) / 64);
       uint8_t *base = nullptr;
       if (noalloc) {
-        base = scratch + rope_bytes;
+        base = scratch + kNoallocRopeBytes;
       } else {
         if ((rc = reserve(c, c->bits, map_off + groups))) return rc;
         base = static_cast<uint8_t *>(c->bits.ptr);
