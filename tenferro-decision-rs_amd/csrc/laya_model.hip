@@ -143,47 +143,66 @@ __global__ __launch_bounds__(256) void copy_columns_kernel(const float *__restri
   }
 }
 
-// pool_host (model.rs:773-837) for batch column blockIdx.x, in the
-// reference's sequential order on one lane (K is a handful of markers), and
-// the pooled action-head input [h[:, 0, b]; top1; top1 - top2; entropy;
-// used / 255] (model.rs:944-952).
+// pool_host (model.rs:773-837) for batch column blockIdx.x on one
+// wavefront, markers spread over the lanes (marker j on lane j % 64), and the
+// pooled action-head input [h[:, 0, b]; top1; top1 - top2; entropy;
+// used / 255] (model.rs:944-952). Masked markers take the logit -1e4
+// (model.rs:779-786); the softmax max, sum and entropy are wave reductions,
+// and each lane keeps the two largest probabilities it has seen, merged
+// across lanes as (max, second largest with repeats), which is the pair the
+// reference's sequential scan (model.rs:805-813) ends with.
+__device__ __forceinline__ float wave_sum_f(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
 __global__ __launch_bounds__(64) void pool_kernel(PoolArgs a) {
-  const int b = blockIdx.x;
+  const int b = blockIdx.x, lane = threadIdx.x;
   const int K = a.k;
   const float *raw = a.raw + (size_t)b * K;
   const uint8_t *mm = a.marker_mask + (size_t)b * K;
   float *lo = a.logits + (size_t)b * K;
   float *pooled = a.pooled + (size_t)b * (a.d + 4);
   const float *h0 = a.h + (size_t)(a.h0_col ? a.h0_col[b] : b * a.L) * a.d;
-  for (int i = threadIdx.x; i < a.d; i += 64) pooled[i] = h0[i];
-  if (threadIdx.x != 0) return;
+  for (int i = lane; i < a.d; i += 64) pooled[i] = h0[i];
+
+  auto masked = [&](int j) { return mm[j] ? raw[j] : -1.0e4f; };
   float mx = -INFINITY;
-  int count = 0;
-  for (int j = 0; j < K; ++j) {
-    const float v = mm[j] ? raw[j] : -1.0e4f;
-    lo[j] = v;
+  int used = 0;
+  for (int j0 = 0; j0 < K; j0 += 64) {
+    const int j = j0 + lane;
+    const bool in = j < K;
+    const float v = in ? masked(j) : -INFINITY;
+    if (in) lo[j] = v;
     mx = fmaxf(mx, v);
-    count += mm[j] ? 1 : 0;
+    used += __popcll(__ballot(in && mm[j] != 0));
   }
+  mx = wave_max_f(mx);
   float sum = 0.0f;
-  for (int j = 0; j < K; ++j) sum += expf(lo[j] - mx);
-  float top1 = -INFINITY, top2 = -INFINITY, ent = 0.0f;
-  for (int j = 0; j < K; ++j) {
-    const float p = expf(lo[j] - mx) / sum;
-    if (p > top1) {
-      top2 = top1;
-      top1 = p;
-    } else if (p > top2) {
-      top2 = p;
-    }
+  for (int j = lane; j < K; j += 64) sum += expf(masked(j) - mx);
+  sum = wave_sum_f(sum);
+  float t1 = -INFINITY, t2 = -INFINITY, ent = 0.0f;
+  for (int j = lane; j < K; j += 64) {
+    const float p = expf(masked(j) - mx) / sum;
+    t2 = fmaxf(t2, fminf(t1, p));
+    t1 = fmaxf(t1, p);
     ent -= p * logf(fmaxf(p, 1.0e-9f));
   }
-  const float used = (float)(count > 2 ? count : 2);
-  ent /= logf(used);
-  pooled[a.d] = top1;
-  pooled[a.d + 1] = top1 - top2;
-  pooled[a.d + 2] = ent;
-  pooled[a.d + 3] = used / 255.0f;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float u1 = __shfl_xor(t1, o), u2 = __shfl_xor(t2, o);
+    t2 = fmaxf(fminf(t1, u1), fmaxf(t2, u2));
+    t1 = fmaxf(t1, u1);
+  }
+  ent = wave_sum_f(ent);
+  if (lane == 0) {
+    const float n = (float)(used < 2 ? 2 : used);
+    pooled[a.d] = t1;
+    pooled[a.d + 1] = t1 - t2;
+    pooled[a.d + 2] = ent / logf(n);
+    pooled[a.d + 3] = n / 255.0f;
+  }
 }
 
 unsigned grid_for(size_t total) {

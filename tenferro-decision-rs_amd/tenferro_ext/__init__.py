@@ -356,10 +356,14 @@ class _StreamOrder:
 
 
 def _call(ctx: "Context", flags: int, fn, *args) -> None:
-    """Runs one C ABI call with stream ordering and error mapping."""
+    """Runs one C ABI call with stream ordering and error mapping. torch's
+    stream waits for the context stream also when the call fails: kernels it
+    enqueued before the failing step may still read the inputs."""
     order = _StreamOrder(ctx, flags)
-    ctx.check(fn(*args))
-    order.done()
+    try:
+        ctx.check(fn(*args))
+    finally:
+        order.done()
 
 
 def _shape_arr(shape):
