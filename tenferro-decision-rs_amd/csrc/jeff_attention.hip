@@ -696,7 +696,9 @@ struct JeffStage {
 };
 
 // TAG gives each calling kernel its own copy, compiled to that kernel's
-// register budget; TAG 1 (the split-head kernel) reads the split K layout.
+// register budget; TAG 1 (the split-head kernel) reads the split K layout,
+// TAG 2 (the fused kernel, no K prep) normalizes and rotates each key tile
+// from K itself into LDS.
 template <int HDP, bool VEC, int TAG = 0>
 __device__ __noinline__ void jeff_redo_wave(const JeffArgs *ap, const float *__restrict__ kp,
                                             int row, int head, int q0, int kt_begin, int kt_end,
@@ -949,8 +951,12 @@ __device__ __noinline__ void jeff_redo_wave(const JeffArgs *ap, const float *__r
   const float *Gt = static_cast<const float *>(a.gate) + row * a.q_row + (size_t)head * hd * L;
   const float *V = static_cast<const float *>(a.v) + row * a.kv_row + (size_t)kvh * a.kv_head;
   constexpr bool SPLIT = TAG == 1;
+  constexpr bool RAW = TAG == 2;  // keys straight from K, normalized per tile into LDS
   const size_t Lu = SPLIT ? (size_t)((L + 15) & ~15) : (size_t)L;
-  const float *KP = kp + ((size_t)row * a.kv_heads + kvh) * Lu * HDP;
+  const float *KP = RAW ? nullptr : kp + ((size_t)row * a.kv_heads + kvh) * Lu * HDP;
+  const float *Kraw = static_cast<const float *>(a.k) + row * a.kv_row + (size_t)kvh * a.kv_head;
+  constexpr int QP = HDP + 4;
+  float *Kw = ws + 512;  // RAW: 16 keys x QP floats, after Pw
   float *OUT = a.out + row * a.q_row + (size_t)head * hd * L;
   float qreg[QS];
   jeff_q_prep<HDP, VEC>(a, Q, q0, start, ws, qreg);
@@ -970,13 +976,49 @@ __device__ __noinline__ void jeff_redo_wave(const JeffArgs *ap, const float *__r
     const uint32_t w = q_live ? (abits & range_bits(0, q - k0)) : 0u;
     if (__ballot(w != 0u) == 0) continue;
     const int kcl = min(kc, L - 1);
-    const float *krow = KP + (size_t)kcl * HDP + grp * QS;
+    if constexpr (RAW) {
+      // The reference's key arithmetic (lib.rs:676-709) for keys k0 .. k0 +
+      // 15: lane (col, grp) normalizes features grp*QS .. + QS - 1 of key
+      // kcl, then rotates pairs i = grp, grp + 4, ... of it.
+      float xk[QS];
+      float ss = 0.0f;
+#pragma unroll
+      for (int x = 0; x < QS; ++x) {
+        const int d = grp * QS + x;
+        xk[x] = d < hd ? Kraw[kcl + (size_t)L * d] : 0.0f;
+        ss += xk[x] * xk[x];
+      }
+      ss += __shfl_xor(ss, 16);
+      ss += __shfl_xor(ss, 32);
+      const float scale = rms_scale(ss, hd, a.eps);
+#pragma unroll
+      for (int x = 0; x < QS; ++x) {
+        const int d = grp * QS + x;
+        Kw[col * QP + d] = d < hd ? rms_apply(xk[x], scale, a.k_norm[d]) : 0.0f;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      if (a.cos_t != nullptr && a.rot_half > 0) {
+        const int rh = a.rot_half;
+        const size_t pos = (size_t)min(max(kcl - start, 0), L - 1) * rh;
+        for (int i = grp; i < rh; i += 4) {
+          const float x = Kw[col * QP + i], y = Kw[col * QP + i + rh];
+          Kw[col * QP + i] = rope_lo(x, y, a.cos_t[pos + i], a.sin_t[pos + i]);
+          Kw[col * QP + i + rh] = rope_hi(x, y, a.cos_t[pos + i], a.sin_t[pos + i]);
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    const float *krow = RAW ? Kw + col * QP + grp * QS : KP + (size_t)kcl * HDP + grp * QS;
     f32x4 s;
 #pragma unroll
     for (int r = 0; r < 4; ++r) s[r] = 0.0f;
 #pragma unroll
     for (int x = 0; x < QS; ++x) {
-      const float kx = SPLIT ? KP[split_kp_offset(kcl, grp * QS + x)] : krow[x];
+      const float kx = SPLIT ? KP[split_kp_offset(kcl, grp * QS + x)] : krow[x];  // RAW: LDS
       s = mfma_16x16x4(kc < L ? kx : 0.0f, qreg[x], s);
     }
     float mx = -INFINITY;
@@ -1428,6 +1470,435 @@ __global__ __launch_bounds__(256, 4) void jeff_split_f32_kernel(const JeffArgs a
   }
 }
 
+// ------------------------------------------- f32 attention, fused, hd 256
+
+constexpr int kJeffFusedWaves = 8;  // waves per fused workgroup (the key range's parts)
+
+// One kernel for the whole op at hd 256 (no K prep): one workgroup = NW
+// wavefronts = one (row, head, 16-query tile). The RMSNorm scales are
+// folded into the scores: with q' = R_q(x_q (1 + w_q)) and, per key,
+// k' = R_k(x_k (1 + w_k)) on the rotated features and x_k elsewhere,
+//   s(q, k) = scale_q scale_k (q'' . k') / sqrt(hd),
+// where q'' is q' times (1 + w_k) on the features past rot_dim (the same
+// product as the reference's q^.k^ of lib.rs:676-716, up to rounding). So
+// wave w prepares Q's features 64 w .. 64 w + 63 elementwise (its RoPE pairs
+// stay inside slice 0) into LDS, where every wave reads its B operands, and
+// scale_q waits in the exponent's factor; a key tile needs only its sum of
+// squares, (1 + w_k) and RoPE on its first rot_dim features, all in the
+// lanes that feed them to the matrix cores.
+//
+// Layout (lane = 16 grp + col): B operand Q^T and A operand K carry feature
+// f = 64 s + 16 c + 4 grp + e at step (s, c, e) of the S^T chain, for query
+// (K: key) col; S^T holds keys 4 grp + r of query col; O^T block J holds
+// features 16 J + 4 grp + r. RoPE partners (i, i + rot/2) sit in one lane,
+// rot/32 blocks of 16 apart (rot/2 = 16 or 32).
+//
+// The tile's key range (first active key .. last query) is cut into NW
+// contiguous parts walked by the NW waves with no barrier; the partial
+// states merge once through LDS. K arrives with 4-byte loads (a lane needs
+// one key's features), V with 16-byte loads along tokens; both stream
+// through a ring of four 16-register pieces, three ahead: K slices 1, 2, 3,
+// then slice 0 (the rotated features, whose table entries load a tile
+// ahead), then V groups 0 .. 3. (Eight slots, each piece a whole tile ahead,
+// measured slower: 21.7 against 19.3 us per C4 row.)
+template <int NW, int RB>  // RB: rotated blocks of 16 in the lower half (rot_dim / 32: 0, 1, 2)
+__global__ __launch_bounds__(NW * 64, 8 / NW) void jeff_fused_f32_kernel(const JeffArgs a,
+                                                                         int rows) {
+  static_assert(RB >= 0 && RB <= 2, "rot_dim 0, 32 or 64");
+  constexpr int HDP = 256, NB = 16, KT = 16;
+  constexpr int BPW = NB / NW;  // O^T blocks each wave finishes
+  static_assert(NW == 4 || NW == 8, "four Q-prep slices; 16 O^T blocks over the waves");
+  constexpr int OMF = NW * NB * 64 * 4;  // partial O^T of every wave (the redo's rows too)
+  // Q operands [slice][run c][lane] as f32x4 (feature 64 s + 16 c + 4 grp + e
+  // of query col), 16 KB at the front of smem until the merge.
+  __shared__ __attribute__((aligned(16))) float smem[OMF];
+  __shared__ __attribute__((aligned(16))) float s_wkr[4 * 4 * 4];  // (1 + w_k), rotated blocks
+  __shared__ float s_ssq[4 * 16];
+  __shared__ float s_m[NW * 16], s_l[NW * 16];
+  __shared__ int s_bad;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15, grp = lane >> 4;
+  const int L = a.L, heads = a.heads, G = a.groups;
+  const int L4 = 4 * L;
+
+  // -------- work item: query tiles from the last one down; the heads of a
+  // (row, kv head) on one XCD.
+  const int nq = (L + 15) / 16;
+  const int units = rows * heads;
+  const int p = blockIdx.x;
+  const int qt = nq - 1 - p / units;
+  int u = p % units, row, head;
+  if (units % 8 == 0 && (rows * a.kv_heads) % 8 == 0) {
+    const int x = u % 8, i = u / 8;
+    const int kvu = x + 8 * (i / G);
+    row = kvu / a.kv_heads;
+    head = (kvu % a.kv_heads) * G + i % G;
+  } else {
+    row = u / heads;
+    head = u % heads;
+  }
+  const int kvh = min(head / G, a.kv_heads - 1);
+  const int q0 = qt * 16, q = q0 + col;
+  const uint32_t bytes = (uint32_t)((size_t)HDP * L * 4);
+  const __amdgpu_buffer_rsrc_t rq = buffer_rsrc(
+      static_cast<const float *>(a.q) + row * a.q_row + (size_t)head * HDP * L, bytes);
+  const __amdgpu_buffer_rsrc_t rg = buffer_rsrc(
+      static_cast<const float *>(a.gate) + row * a.q_row + (size_t)head * HDP * L, bytes);
+  const __amdgpu_buffer_rsrc_t ro =
+      buffer_rsrc(a.out + row * a.q_row + (size_t)head * HDP * L, bytes);
+  const float *Kb = static_cast<const float *>(a.k) + row * a.kv_row + (size_t)kvh * a.kv_head;
+  const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(Kb, bytes);
+  const __amdgpu_buffer_rsrc_t rv = buffer_rsrc(
+      static_cast<const float *>(a.v) + row * a.kv_row + (size_t)kvh * a.kv_head, bytes);
+  const __amdgpu_buffer_rsrc_t rm = buffer_rsrc(a.mask + (size_t)row * L, (uint32_t)L4);
+  // Per-lane byte offsets: feature 4 grp (+ the step's 64s + 16c + e, a
+  // scalar offset) of token col (+ the tile's first token, scalar). A lane
+  // with nothing to load takes an offset past the buffer's end, which the
+  // hardware range check reads as 0 (whether or not it adds the scalar part).
+  const int ofs_t = (4 * grp * L + col) * 4;
+  const int koob = (int)bytes;
+  const int ofs_q = q < L ? ofs_t : koob;
+
+  // -------- loads that need nothing: Q slice `wave` (waves 0 .. 3) in
+  // B-operand order (feature 64 wave + 16 c + 4 grp + e), its norm weights.
+  const bool prep = wave < 4;
+  const int sw = wave & 3;
+  float xq[16];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      xq[4 * c + e] = prep ? buffer_load1(rq, ofs_q, q0 * 4 + (64 * sw + 16 * c + e) * L4) : 0.0f;
+  const __amdgpu_buffer_rsrc_t rwq = buffer_rsrc(a.q_norm, HDP * 4);
+  const __amdgpu_buffer_rsrc_t rwk = buffer_rsrc(a.k_norm, HDP * 4);
+  f32x4 wq[4], wk[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    wq[c] = buffer_load4(rwq, (64 * sw + 16 * c + 4 * grp) * 4, 0);
+    wk[c] = buffer_load4(rwk, (64 * sw + 16 * c + 4 * grp) * 4, 0);
+  }
+
+  // -------- the row's active span (mask != 0), every wave on its own.
+  int first, last;
+  {
+    int lo = 0x7fffffff, hi = -1;
+    for (int k0 = 0; k0 < L; k0 += 256) {
+      const f32x4 mv = buffer_load4(rm, (k0 + 4 * lane) * 4, 0);  // past L: 0
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        if (mv[t] != 0.0f) {
+          lo = min(lo, k0 + 4 * lane + t);
+          hi = max(hi, k0 + 4 * lane + t);
+        }
+    }
+    lo = wave_min(lo);
+    hi = wave_max(hi);
+    first = __builtin_amdgcn_readfirstlane(hi >= 0 ? lo : 0);
+    last = __builtin_amdgcn_readfirstlane(hi);
+  }
+  const int start = (a.trim && last >= 0) ? first : 0;
+  const bool q_live = q < L && q >= start;
+  const int q_last = min(q0 + 15, L - 1);
+  int kt_begin = 0, kt_end = 0;
+  {
+    const int kl = min(last, q_last);
+    if (last >= 0 && first <= kl && q_last >= start) {
+      kt_begin = first / KT;
+      kt_end = kl / KT + 1;
+    }
+  }
+  // o * sigmoid(gate) (lib.rs:755-758) for the wave's features 16 (BPW wave
+  // + j) + 4 grp + r of query col; 0 for a dropped query (q < start).
+  auto finish = [&](const f32x4 (&o)[BPW]) {
+    float g[4 * BPW];
+#pragma unroll
+    for (int j = 0; j < BPW; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        g[4 * j + r] = buffer_load1(rg, ofs_q, q0 * 4 + (16 * (BPW * wave + j) + r) * L4);
+    if (q < L) {
+#pragma unroll
+      for (int j = 0; j < BPW; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float x = q < start ? 0.0f : o[j][r] * fast_sigmoid(g[4 * j + r]);
+          buffer_store1(x, ro, ofs_t, q0 * 4 + (16 * (BPW * wave + j) + r) * L4);
+        }
+    }
+  };
+  if (kt_begin >= kt_end) {  // no key at or before these queries: o = 0 (lib.rs:739-743)
+    const f32x4 z[BPW] = {};
+    finish(z);
+    return;
+  }
+
+  // -------- Q: x (1 + w_q), RoPE, (1 + w_k) past rot_dim, into LDS; the sum
+  // of squares over the four slices gives scale_q.
+  constexpr int rb = RB, rh = 16 * RB;
+  float ssq = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) ssq += xq[i] * xq[i];
+  ssq += __shfl_xor(ssq, 16);
+  ssq += __shfl_xor(ssq, 32);
+  if (prep && grp == 0) s_ssq[sw * 16 + col] = ssq;
+  float qs[16];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) qs[4 * c + e] = xq[4 * c + e] * (1.0f + wq[c][e]);
+  if (rb > 0 && wave == 0) {  // slice 0 holds the rotated features
+    const int pos = min(max(q - start, 0), L - 1);
+#pragma unroll
+    for (int b = 0; b < rb; ++b) {
+      const f32x4 cs = *reinterpret_cast<const f32x4 *>(a.cos_t + (size_t)pos * rh + 16 * b + 4 * grp);
+      const f32x4 sn = *reinterpret_cast<const f32x4 *>(a.sin_t + (size_t)pos * rh + 16 * b + 4 * grp);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float x = qs[4 * b + e], y = qs[4 * (b + rb) + e];
+        qs[4 * b + e] = rope_lo(x, y, cs[e], sn[e]);
+        qs[4 * (b + rb) + e] = rope_hi(x, y, cs[e], sn[e]);
+      }
+    }
+  }
+  f32x4 *QL = reinterpret_cast<f32x4 *>(smem);
+  if (prep) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const bool rotated = wave == 0 && c < 2 * rb;
+      f32x4 y;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y[e] = q_live ? qs[4 * c + e] * (rotated ? 1.0f : 1.0f + wk[c][e]) : 0.0f;
+      QL[(sw * 4 + c) * 64 + lane] = y;
+    }
+  }
+  if (wave == 0 && col == 0) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) *reinterpret_cast<f32x4 *>(s_wkr + (c * 4 + grp) * 4) = wk[c] + 1.0f;
+  }
+  __syncthreads();
+  const float c1q =
+      a.c1 * rms_scale(s_ssq[col] + s_ssq[16 + col] + s_ssq[32 + col] + s_ssq[48 + col], HDP, a.eps);
+
+  // -------- this wave's part of the key range.
+  const int T = kt_end - kt_begin;
+  const int w_begin = kt_begin + (T * wave) / NW, w_end = kt_begin + (T * (wave + 1)) / NW;
+  // Ring slot i % 4: piece i of a tile, i = 0, 1, 2: K slice i + 1; 3: K
+  // slice 0; 4 .. 7: V group i - 4 (O^T blocks 4 (i - 4) .. + 3). Loads are
+  // unconditional (at the last tile the "next" K pieces re-read the current
+  // tile), so no ring slot ever holds one of two values.
+  f32x4 ring[4][4];
+  f32x4 tcs[2], tsn[2];  // the tile's table entries (rotated pairs of key col)
+  auto k_off = [&](int kt) -> int { return kt * KT + col < L ? ofs_t : koob; };
+  auto load_k = [&](int slot, int sl, int kt) {
+    const int vo = k_off(kt);
+    kt = __builtin_amdgcn_readfirstlane(kt);
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        ring[slot][c][e] = buffer_load1(rk, vo, kt * KT * 4 + (64 * sl + 16 * c + e) * L4);
+  };
+  auto load_tab = [&](int kt) {
+    if (rb > 0) {
+      const int pos = min(max(kt * KT + col - start, 0), L - 1);
+#pragma unroll
+      for (int b = 0; b < rb; ++b) {
+        tcs[b] = *reinterpret_cast<const f32x4 *>(a.cos_t + (size_t)pos * rh + 16 * b + 4 * grp);
+        tsn[b] = *reinterpret_cast<const f32x4 *>(a.sin_t + (size_t)pos * rh + 16 * b + 4 * grp);
+      }
+    }
+  };
+  // V: features 16 J + col, keys k0 + 4 grp .. + 3 (L % 4 == 0: all in or out).
+  const int ofs_v = (col * L + 4 * grp) * 4;
+  auto load_v = [&](int slot, int g, int kt) {
+    const int k = kt * KT + 4 * grp;
+    const int vo = k < L ? ofs_v + kt * KT * 4 : koob;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ring[slot][j] = buffer_load4(rv, vo, (4 * g + j) * 16 * L4);
+  };
+
+  f32x4 O[NB];
+#pragma unroll
+  for (int j = 0; j < NB; ++j) O[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float m = kNoMax, l = 0.0f;  // l: this lane's share of the row sum
+  bool tainted = false;        // wave-uniform
+
+  if (w_begin < w_end) {
+    load_tab(w_begin);
+    load_k(0, 1, w_begin);
+    load_k(1, 2, w_begin);
+    load_k(2, 3, w_begin);
+  }
+  for (int kt = w_begin; kt < w_end; ++kt) {
+    const int kn = kt + 1 < w_end ? kt + 1 : kt;
+    const int k0 = kt * KT;
+    const float mv = buffer_load1(rm, (k0 + col) * 4, 0);  // past L: 0
+    f32x4 s0 = {0.0f, 0.0f, 0.0f, 0.0f}, s1 = {0.0f, 0.0f, 0.0f, 0.0f};
+    float ssk = 0.0f;
+    // S^T over K slices 1, 2, 3 (features past the rotated ones)
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      if (i == 0)
+        load_k(3, 0, kt);
+      else
+        load_v(i - 1, i - 1, kt);  // V groups 0, 1
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float x = ring[i][c][e];
+          ssk += x * x;
+          const float y = QL[((i + 1) * 4 + c) * 64 + lane][e];
+          if (c & 1)
+            s1 = mfma_16x16x4(x, y, s1);
+          else
+            s0 = mfma_16x16x4(x, y, s0);
+        }
+    }
+    // slice 0: sum of squares of the raw key, then x (1 + w_k) and RoPE on
+    // the rotated blocks (0 .. 2 rb - 1)
+    load_v(2, 2, kt);  // V group 2
+    {
+      f32x4(&k)[4] = ring[3];
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ssk += k[c][e] * k[c][e];
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (c < 2 * rb) k[c] *= *reinterpret_cast<const f32x4 *>(s_wkr + (c * 4 + grp) * 4);
+#pragma unroll
+      for (int b = 0; b < rb; ++b) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float x = k[b][e], y = k[b + rb][e];
+          k[b][e] = rope_lo(x, y, tcs[b][e], tsn[b][e]);
+          k[b + rb][e] = rope_hi(x, y, tcs[b][e], tsn[b][e]);
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float y = QL[c * 64 + lane][e];
+          if (c & 1)
+            s1 = mfma_16x16x4(k[c][e], y, s1);
+          else
+            s0 = mfma_16x16x4(k[c][e], y, s0);
+        }
+    }
+    // the key's scale (lanes col hold key col), to the S^T rows 4 grp + r
+    ssk += __shfl_xor(ssk, 16);
+    ssk += __shfl_xor(ssk, 32);
+    const float sck = rms_scale(ssk, HDP, a.eps);
+    const uint32_t abits = (uint32_t)__ballot(mv != 0.0f && k0 + col >= start) & 0xffffu;
+    const uint32_t w = q_live ? (abits & range_bits(0, q - k0)) : 0u;
+    f32x4 s = s0 + s1;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s[r] *= c1q * __shfl(sck, 4 * grp + r);
+    if (__ballot(q_live && w != 0xffffu) != 0) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s[r] = ((w >> (4 * grp + r)) & 1u) ? s[r] : -INFINITY;
+    }
+    load_tab(kn);  // the next tile's table entries
+    f32x4 ex;
+    float rs = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      ex[r] = fast_exp2(s[r] - m);
+      rs += ex[r];
+    }
+    if (__builtin_expect(__ballot(q_live && !(rs <= kLazyLimit)) != 0, 0)) {
+      const float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+      const float mxs = pair_max(pair16_max(mx));
+      const float mn = mxs > m + kRescaleSlack ? mxs : m;
+      rs = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        ex[r] = fast_exp2(s[r] - mn);
+        rs += ex[r];
+      }
+      if (__ballot(q_live && !__builtin_isfinite(rs)) != 0) {
+        tainted = true;
+      } else {
+        const float alpha = fast_exp2(m - mn);  // exactly 1 where the reference stays
+#pragma unroll
+        for (int j = 0; j < NB; ++j) O[j] *= alpha;
+        l *= alpha;
+        m = mn;
+      }
+    }
+    l += rs;
+    // P.V: V groups 0 .. 3 in slots 0, 1, 2 and (loaded now) 3; the next
+    // tile's K slices 1 .. 3 into slots 0 .. 2 as they free up.
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      if (g == 0)
+        load_v(3, 3, kt);
+      else
+        load_k(g - 1, g, kn);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          O[4 * g + j] = mfma_16x16x4(ring[g][j][r], ex[r], O[4 * g + j]);
+    }
+    if (tainted) break;  // wave-uniform; the whole tile is redone below
+  }
+
+  // -------- careful redo (rare): some wave's scores or O went non-finite;
+  // one wave redoes the whole tile with the reference's exact semantics.
+  if (tid == 0) s_bad = 0;
+  __syncthreads();
+  bool bad = tainted;
+#pragma unroll
+  for (int j = 0; j < NB; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) bad |= q_live && !__builtin_isfinite(O[j][r]);
+  if (__ballot(bad) != 0 && lane == 0) s_bad = 1;
+  __syncthreads();
+  if (s_bad != 0) {
+    if (wave == 0)
+      jeff_redo_wave<HDP, true, 2>(kernel_jeff_args(), nullptr, row, head, q0, kt_begin, kt_end,
+                                   start, smem);
+    return;
+  }
+
+  // -------- merge: O = sum_w 2^(m_w - M) O_w / sum_w 2^(m_w - M) l_w; wave w
+  // finishes O^T blocks BPW w .. BPW w + BPW - 1. Every
+  // wave is past its walk (the barrier above), so OM may cover the Q rows.
+  f32x4 *OM = reinterpret_cast<f32x4 *>(smem);
+#pragma unroll
+  for (int j = 0; j < NB; ++j) OM[(wave * NB + j) * 64 + lane] = O[j];
+  const float lt = pair_sum(pair16_sum(l));
+  if (grp == 0) {
+    s_m[wave * 16 + col] = m;
+    s_l[wave * 16 + col] = lt;
+  }
+  __syncthreads();
+  float M = s_m[col];
+#pragma unroll
+  for (int v = 1; v < NW; ++v) M = fmaxf(M, s_m[v * 16 + col]);
+  float fac[NW], lsum = 0.0f;
+#pragma unroll
+  for (int v = 0; v < NW; ++v) {
+    fac[v] = fast_exp2(s_m[v * 16 + col] - M);  // 0 for a wave without keys (m = kNoMax)
+    lsum += fac[v] * s_l[v * 16 + col];
+  }
+  const float inv = lsum > 0.0f ? fast_rcp(lsum) : 0.0f;
+  f32x4 Of[BPW];
+#pragma unroll
+  for (int j = 0; j < BPW; ++j) {
+    Of[j] = OM[(BPW * wave + j) * 64 + lane] * fac[0];
+#pragma unroll
+    for (int v = 1; v < NW; ++v) Of[j] += OM[(v * NB + BPW * wave + j) * 64 + lane] * fac[v];
+    Of[j] *= inv;
+  }
+  finish(Of);
+}
+
 // ---------------------------------------------------------- bf16 attention
 
 // Tile data for one 32-key bf16 tile: finished K rows from the prep workspace
@@ -1873,6 +2344,28 @@ static hipError_t launch_jeff_f32_hd(const JeffArgs &a, int rows, float *kp, hip
   const bool vec = a.L % 4 == 0 && (bases & 15) == 0 &&
                    ((size_t)a.L + 15) * (size_t)HDP * 4 < ((size_t)1 << 31);
   if constexpr (HDP == 256) {
+    // Grids of at most two workgroups per CU (one row of C4 is 128) take
+    // the fused kernel: one launch, no K prep, every query tile's key range
+    // on eight wavefronts. Larger grids keep the K prep and the split-head
+    // kernel, which holds four workgroups per CU (the fused kernel's 256
+    // registers per wave allow two) and reads each prepared key tile with
+    // 1 KB loads instead of normalizing it again for every query tile.
+    const int rb = a.cos_t == nullptr ? 0 : (a.rot_half % 16 == 0 ? a.rot_half / 16 : -1);
+    const long items = (long)nq * rows * a.heads;
+    if (vec && a.hd == 256 && rb >= 0 && rb <= 2 && items <= 2L * (a.cus > 0 ? a.cus : 1)) {
+      constexpr int NW = kJeffFusedWaves;
+      const dim3 fgrid((unsigned)items);
+      if (rb == 0)
+        hipExtLaunchKernelGGL((jeff_fused_f32_kernel<NW, 0>), fgrid, dim3(NW * 64), 0, stream,
+                              ev.start, ev.stop, 0, a, rows);
+      else if (rb == 1)
+        hipExtLaunchKernelGGL((jeff_fused_f32_kernel<NW, 1>), fgrid, dim3(NW * 64), 0, stream,
+                              ev.start, ev.stop, 0, a, rows);
+      else
+        hipExtLaunchKernelGGL((jeff_fused_f32_kernel<NW, 2>), fgrid, dim3(NW * 64), 0, stream,
+                              ev.start, ev.stop, 0, a, rows);
+      return hipGetLastError();
+    }
     // Buffer offsets of the split kernel: one head's (hd, L) block and one
     // kv head's padded K blocks within 2 GiB (checked above, L + 15 < 2^21).
     if (vec) {
