@@ -276,6 +276,14 @@ def run(args):
                      "traffic": _traffic("laya_attention_kernel"),
                      "algorithmic_bytes": laya_bytes(w)},
         "gpu": gpu_name,
+        "provenance": provenance(),
+        "timing_note": ("ms_per_step: torch events around `steps` back-to-back calls with the "
+                        "library's timing off; kernel_ms (and roofline.achieved): a second pass "
+                        "of `steps` calls with timing on, the mean span from the start of the "
+                        "op's first kernel to the end of its last, recorded by the dispatches "
+                        "themselves (hipExtLaunchKernel events). For the Jeff rows that span "
+                        "covers the K prep and the attention kernel and the gap between them; "
+                        "the per-kernel durations are in profiles/ (rocprofv3)."),
     }
 
     # ------------------------------------------------------------ other configs
@@ -356,18 +364,20 @@ def run(args):
                                                              tkn, tm, kj)
             if cfg == 4 and not args.no_cpu:
                 cores = host_threads()[0]
-                t = cpu_jeff_rows(wj, 2, cores)
-                also["C4"]["cpu_port_tokens_per_s"] = round(
-                    float((wj.mask[: 2 * wj.length] != 0).sum()) / t, 1)
-                also["C4"]["cpu_port_sample"] = f"2 of 16 rows, median of 3, {cores} threads"
+                t = cpu_jeff_rows(wj, wj.rows, cores)
+                also["C4"]["cpu_port_tokens_per_s"] = round(wj.valid_tokens() / t, 1)
+                also["C4"]["cpu_port_tflops"] = round(fj / t / 1e12, 5)
+                also["C4"]["cpu_port_sample"] = (f"full C4 workload (16 rows), median of 3, "
+                                                 f"{cores} threads (one task per head, as the "
+                                                 f"reference), {t * 1e3:.1f} ms")
             if cfg == 5 and not args.no_cpu:
                 cores = host_threads()[0]
-                ws = jeff_config(5, rows=1, length=2048)
-                t = cpu_jeff_rows(ws, 1, cores, reps=1)
-                fs = 4 * ws.head_dim * ws.kept_pairs() * ws.heads
-                also["C5"]["cpu_port_tflops"] = round(fs / t / 1e12, 5)
-                also["C5"]["cpu_port_sample"] = (f"1 row x L 2048 of the C5 generator (f32 path), "
-                                                 f"{cores} threads, {t:.2f} s")
+                log("[bench] C5 CPU leg: the full workload once (about 20-40 s)")
+                t = cpu_jeff_rows(wj, wj.rows, cores, reps=1)
+                also["C5"]["cpu_port_tflops"] = round(fj / t / 1e12, 5)
+                also["C5"]["cpu_port_tokens_per_s"] = round(wj.valid_tokens() / t, 1)
+                also["C5"]["cpu_port_sample"] = (f"full C5 workload (2 x 8192, the bf16 inputs' "
+                                                 f"f32 values), once, {cores} threads, {t:.2f} s")
             del tq, tk, tv, tg, tqn, tkn, tm, oj
         log("[bench] reference micro-benchmark shapes")
         also["micro_reference_shapes"] = micro_lines(args, ctx, dev)
@@ -647,6 +657,47 @@ def _traffic(kernel):
         return data["kernels"][kernel]["hbm_bytes_per_launch"]
     except (OSError, KeyError, ValueError):
         return None
+
+
+def provenance():
+    """Where and from what the line was measured (the reference's bench-suite
+    BenchMetadata, crates/bench-suite/src/lib.rs:14-73: git revision,
+    timestamp, OS and architecture): the git revision when the tree is a git
+    checkout (GPU boxes receive a snapshot without .git), a hash of the
+    sources the measured library and this script are built from, UTC time,
+    OS/arch, Python, torch and HIP versions."""
+    import hashlib
+    import platform
+    import subprocess
+    import datetime
+
+    rev = None
+    try:
+        rev = subprocess.run(["git", "-C", ROOT, "rev-parse", "HEAD"], capture_output=True,
+                             text=True, timeout=10).stdout.strip() or None
+    except (OSError, subprocess.SubprocessError):
+        rev = None
+    h = hashlib.sha256()
+    for sub in ("tenferro-decision-rs_amd/csrc", "include"):
+        d = os.path.join(ROOT, sub)
+        for name in sorted(os.listdir(d)):
+            fp = os.path.join(d, name)
+            if os.path.isfile(fp):
+                h.update(name.encode())
+                h.update(open(fp, "rb").read())
+    h.update(open(os.path.abspath(__file__), "rb").read())
+    out = {"git_rev": rev, "sources_sha16": h.hexdigest()[:16],
+           "timestamp_utc": datetime.datetime.now(datetime.timezone.utc).isoformat(timespec="seconds"),
+           "os": platform.platform(), "arch": platform.machine(),
+           "python": platform.python_version()}
+    try:
+        import torch
+
+        out["torch"] = torch.__version__
+        out["hip"] = getattr(torch.version, "hip", None)
+    except ImportError:
+        pass
+    return out
 
 
 def _cpu_model():
