@@ -155,13 +155,17 @@ void oracle_rope_table(size_t length, size_t hd, float base, float *cos_out, flo
  * Every output is accumulated over k in order, acc = fma(a, b, acc) from 0,
  * so the blocked kernel below and the plain loop give the same bits.
  *
- * The FMA path is a packed, register-tiled kernel in the manner of
- * matrixmultiply 0.3.11 (the reference's sgemm): B is packed into panels
- * of 16 columns (k x 16, contiguous), and a 6 x 16 block of C lives in
- * twelve 8-wide registers for the whole k loop (two B loads and six A
- * broadcasts per twelve FMAs). k is never split (at most the span length
- * or the head dim), which keeps the summation order above. Edge rows and
- * columns run the same in-order FMA chain one element at a time. */
+ * This is an in-order FMA restatement of the two products, not a copy of
+ * matrixmultiply 0.3.11's summation order: that crate blocks k by its kc
+ * and its source is not vendored with the reference, so the two agree to
+ * f32 rounding, not bit for bit (the reference itself pins this path only
+ * by tolerance). For speed it is a packed, register-tiled kernel: B is
+ * packed into panels of 16 columns (k x 16, contiguous), and a 6 x 16
+ * block of C lives in twelve 8-wide registers for the whole k loop (two B
+ * loads and six A broadcasts per twelve FMAs). k is never split (at most
+ * the span length or the head dim), which keeps the in-order summation
+ * above. Edge rows and columns run the same FMA chain one element at a
+ * time. */
 #if defined(__x86_64__)
 #include <immintrin.h>
 
