@@ -22,6 +22,8 @@
 // Each wavefront owns 16 queries and walks 32-key tiles on the 16x16x4 f32
 // MFMA: S^T = K Q^T as two 16-key blocks, then O^T += V^T P^T. At hd = 256
 // this keeps Q (hd/4 registers) and O^T (hd/4) within one wave's registers.
+#include <type_traits>
+
 #include "jeff_common.hpp"
 #include "tfd_device.hpp"
 #include "tfd_internal.hpp"
@@ -1115,15 +1117,22 @@ __global__ __launch_bounds__(256, 4) void jeff_split_f32_kernel(const JeffArgs a
   constexpr int NB = DS / 16;    // 16-feature blocks of O^T per wave
   constexpr int KT = kJeffKeyTile;
   constexpr int QW = DS + 4;     // wave rows [query][feature] for Q
-  constexpr int OW = 16 + 4;     // wave rows [feature][query] for the output
+  constexpr int OW = 16;         // wave rows [feature][query] for the output (the K slice)
   constexpr int WROWS = DS * OW > 16 * QW ? DS * OW : 16 * QW;
   constexpr int QP = HDP + 4;    // whole-tile Q rows (RoPE widths other than 16, 32)
   constexpr int WAREA = 4 * WROWS > 16 * QP ? 4 * WROWS : 16 * QP;
   constexpr int SX = 2 * 4 * 64 * 4;  // score exchange: 2 buffers x 4 waves x 64 lanes x f32x4
-  __shared__ __attribute__((aligned(16))) float smem[WAREA + SX];
-  __shared__ float s_ssq[4 * 16];
-  __shared__ __attribute__((aligned(16))) float s_inv[4 * 16];
-  __shared__ int s_bad;
+  // Each wave's K and V tile slices (4 KB each), where the next tile lands
+  // while the current one is computed; the wave rows and the whole-tile Q
+  // rows use the same bytes before the walk and after it. 40 KB in all, so
+  // four workgroups share a CU's 160 KB.
+  constexpr int KVW = 2 * QS * 64;  // floats per wave: K and V, 16 floats per lane each
+  constexpr int KVAREA = 4 * KVW;
+  static_assert(WAREA <= KVAREA && WROWS <= KVW && DS * OW <= QS * 64,
+                "the wave rows alias the wave's tile slices; the output rows its K slice");
+  __shared__ __attribute__((aligned(16))) float smem[KVAREA + SX];
+  // RMSNorm partial sums in exchange buffer 1, read before its first use.
+  float *const s_ssq = smem + KVAREA + SX / 2;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1154,7 +1163,7 @@ __global__ __launch_bounds__(256, 4) void jeff_split_f32_kernel(const JeffArgs a
   const float *KP = kp + ((size_t)row * a.kv_heads + kvh) * (size_t)Lp * HDP;
   const uint32_t *rbits = kbits + (size_t)row * ((L + 31) / 32);
   float *OUT = a.out + row * a.q_row + (size_t)head * hd * L;
-  float *ww = smem + wave * WROWS;  // this wave's rows
+  float *ww = smem + wave * (2 * QS * 64);  // this wave's rows: its K and V slices
 
   // This lane's features in both products: step (c, e) of the 16x16x4 MFMA
   // chain uses feature d0 + 16c + e (the prep workspace's run order).
@@ -1267,7 +1276,6 @@ __global__ __launch_bounds__(256, 4) void jeff_split_f32_kernel(const JeffArgs a
 
   // -------- RMSNorm (lib.rs:676-691): the sum of squares over the four
   // waves' slices through LDS, then partial RoPE (692-709).
-  if (tid == 0) s_bad = 0;
   float ss = 0.0f;
 #pragma unroll
   for (int c = 0; c < QS / 4; ++c)
@@ -1288,17 +1296,23 @@ __global__ __launch_bounds__(256, 4) void jeff_split_f32_kernel(const JeffArgs a
     }
   if (rope && lane_rope) {
     if (wave == 0 && q_live) {
-      const int pc = rh / 16;  // register-block offset of the partner
+      // pc: register-block offset of the partner, a constant in each branch
+      // (a run-time one indexes the register array indirectly).
+      auto rotate = [&](auto pcv) {
+        constexpr int pc = decltype(pcv)::value;
 #pragma unroll
-      for (int c = 0; c < 2; ++c)
-        if (c < pc) {
+        for (int c = 0; c < pc; ++c)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const float x = qreg[4 * c + e], y = qreg[4 * (c + pc) + e];
             qreg[4 * c + e] = rope_lo(x, y, tc[c][e], ts[c][e]);
             qreg[4 * (c + pc) + e] = rope_hi(x, y, tc[c][e], ts[c][e]);
           }
-        }
+      };
+      if (rh == 16)
+        rotate(std::integral_constant<int, 1>{});
+      else
+        rotate(std::integral_constant<int, 2>{});
     }
   } else if (rope) {
     // Any other rotary width: rotate the normalized rows of the whole tile
@@ -1328,7 +1342,45 @@ __global__ __launch_bounds__(256, 4) void jeff_split_f32_kernel(const JeffArgs a
       for (int e = 0; e < 4; ++e) qreg[4 * c + e] = Qs[col * QP + d0 + 16 * c + e];
     __syncthreads();  // the tile rows become wave rows again
   }
-  f32x4 *sx = reinterpret_cast<f32x4 *>(smem + WAREA);
+  f32x4 *sx = reinterpret_cast<f32x4 *>(smem + KVAREA);
+
+  // The next key tile's K and V go into this wave's LDS slices with LDS-DMA
+  // loads (no registers held; the wave reads back exactly the bytes it
+  // loaded, so it only waits for its own loads). Issued once the previous
+  // contents are in registers, one tile ahead of their use.
+  unsigned char *const kv_lds = reinterpret_cast<unsigned char *>(smem) + wave * KVW * 4;
+  const u32x4r rkw = rsrc_words(KP, (uint32_t)((size_t)Lp * HDP * 4));
+  const u32x4r rvw = rsrc_words(V, (uint32_t)((size_t)hd * L * 4));
+  auto prefetch = [&](int k0) {
+    k0 = __builtin_amdgcn_readfirstlane(k0);
+    // One offset register per lane (okk, ovv); the per-load steps go in the
+    // scalar offset.
+#pragma unroll
+    for (int c = 0; c < QS / 4; ++c)
+      load_lds16(rkw, (uint32_t)okk, (uint32_t)(k0 * HDP * 4 + 1024 * c), kv_lds + 1024 * c);
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+      load_lds16(rvw, (uint32_t)ovv, (uint32_t)(k0 * 4 + j * 16 * L * 4),
+                 kv_lds + QS * 256 + 1024 * j);
+  };
+  auto take = [&]() {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int c = 0; c < QS / 4; ++c)
+      kc[c] = *reinterpret_cast<const f32x4 *>(kv_lds + 1024 * c + 16 * lane);
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+      vc[j] = *reinterpret_cast<const f32x4 *>(kv_lds + QS * 256 + 1024 * j + 16 * lane);
+  };
+  // The gate tasks of the wave's slice go into its V slice during the last
+  // step (read back after the walk).
+  const u32x4r rgw = rsrc_words(Gt, (uint32_t)((size_t)hd * L * 4));
+  auto gate_to_lds = [&]() {
+#pragma unroll
+    for (int t = 0; t < NB; ++t)
+      load_lds16(rgw, (uint32_t)otask, (uint32_t)(q0 * 4 + t * 16 * L * 4),
+                 kv_lds + QS * 256 + 1024 * t);
+  };
 
   // Keep word of a 16-key tile for query col: active key (the prep's bits:
   // mask != 0, zero past L), key <= query (lib.rs:716). Keys before `start`
@@ -1351,20 +1403,32 @@ __global__ __launch_bounds__(256, 4) void jeff_split_f32_kernel(const JeffArgs a
   // only moves rounding). A workgroup whose kept scores sum to NaN or inf
   // stops computing; it, or one whose O took a NaN or inf, redoes the tile
   // with the reference's exact semantics afterwards. The gate loads go out
-  // with the last tile.
+  // with the last tile. The first tile is in registers (loaded with the
+  // item); every later one comes through LDS, prefetched a step ahead (the
+  // prologue's last use of the wave rows was before its barrier).
   const int kt_hi = kt_end - 1;
   if (kt_hi != qt) fetch(kt_hi * KT, kc, vc);  // the span ends before the diagonal
+  if (kt_hi > kt_begin) prefetch((kt_hi - 1) * KT);
   uint32_t w = keep_word(kt_hi, bits_of(kt_hi));
   bool tainted = false;  // workgroup-uniform
   int xb = 0;            // exchange buffer
-  for (int kt = kt_hi; kt >= kt_begin; --kt) {
+  // One step per key tile. The first is peeled off (FIRST): its K and V come
+  // from registers, every later one from the slices. So no vector-memory
+  // load that the compiler tracks is in flight inside the loop, and the
+  // waits it inserts there never hold up the next tile's LDS-DMA loads.
+  auto step = [&](int kt, auto first) {
+    constexpr bool FIRST = decltype(first)::value;
     const bool more = kt > kt_begin;
     uint32_t bnext = 0u;
-    if (kt != kt_hi) fetch(kt * KT, kc, vc);
+    if constexpr (!FIRST) {
+      take();
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slices are in registers
+    }
     if (more) {
+      if constexpr (!FIRST) prefetch((kt - 1) * KT);
       bnext = bits_of(kt - 1);
     } else {
-      load_gate();
+      gate_to_lds();
     }
     if (kt * KT + KT > L) {  // the row's last, partial tile: V past L is another feature's
 #pragma unroll
@@ -1434,7 +1498,10 @@ __global__ __launch_bounds__(256, 4) void jeff_split_f32_kernel(const JeffArgs a
       }
     }
     if (more) w = keep_word(kt - 1, bnext);
-  }
+  };
+  step(kt_hi, std::true_type{});
+  for (int kt = kt_hi - 1; kt >= kt_begin; --kt) step(kt, std::false_type{});
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the gate slice, and no LDS-DMA left in flight
 
   // -------- careful redo (rare): the scores (shared) or this wave's O went
   // non-finite; one wave redoes the whole tile from global memory.
@@ -1443,9 +1510,15 @@ __global__ __launch_bounds__(256, 4) void jeff_split_f32_kernel(const JeffArgs a
   for (int j = 0; j < NB; ++j)
 #pragma unroll
     for (int r = 0; r < 4; ++r) bad |= !__builtin_isfinite(O[j][r]);
-  if (__ballot(q_live && bad) != 0 && lane == 0) s_bad = 1;
+  // Flags and the row sums' inverses go into the exchange buffer that the
+  // last exchange did not use: every wave finished reading it before that
+  // exchange's barrier.
+  float *const xs = smem + KVAREA + xb * (SX / 2);
+  int *const s_flag = reinterpret_cast<int *>(xs);
+  const bool wbad = __ballot(q_live && bad) != 0;
+  if (lane == 0) s_flag[wave] = wbad ? 1 : 0;
   __syncthreads();
-  if (tainted || s_bad != 0) {
+  if (tainted || (s_flag[0] | s_flag[1] | s_flag[2] | s_flag[3]) != 0) {
     if (wave == 0) jeff_redo_wave<HDP, true, 1>(kernel_jeff_args(), kp, row, head, q0, kt_begin, kt_end, start, smem);
     return;
   }
@@ -1453,6 +1526,7 @@ __global__ __launch_bounds__(256, 4) void jeff_split_f32_kernel(const JeffArgs a
   // -------- o / sum (0 when nothing was kept), sigmoid gate, store: O^T
   // through the wave's rows [feature][query] so that each task stores 4
   // tokens of one feature.
+  float *const s_inv = xs + 64;
   const float lt = pair_sum(pair16_sum(l));
   if (grp == 0) s_inv[wave * 16 + col] = lt > 0.0f ? fast_rcp(lt) : 0.0f;
 #pragma unroll
@@ -1463,6 +1537,9 @@ __global__ __launch_bounds__(256, 4) void jeff_split_f32_kernel(const JeffArgs a
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   const f32x4 inv4 = *reinterpret_cast<const f32x4 *>(s_inv + wave * 16 + 4 * tg4);
+#pragma unroll
+  for (int t = 0; t < NB; ++t)
+    gv[t] = *reinterpret_cast<const f32x4 *>(kv_lds + QS * 256 + 1024 * t + 16 * lane);
 #pragma unroll
   for (int t = 0; t < NB; ++t) {
     const f32x4 o = *reinterpret_cast<const f32x4 *>(ww + (tdl + 16 * t) * OW + 4 * tg4);

@@ -78,31 +78,6 @@ __device__ __forceinline__ f32x16 mfma_32x32x16_f16(f16x8 a, f16x8 b, f32x16 c) 
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-// A buffer resource as four scalar words (raw buffer, no swizzle).
-typedef unsigned u32x4r __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ u32x4r rsrc_words(const void *base, uint32_t bytes) {
-  const uint64_t ad = reinterpret_cast<uint64_t>(base);
-  return u32x4r{(uint32_t)ad, (uint32_t)(ad >> 32) & 0xffffu, bytes, (uint32_t)kBufferWord3};
-}
-
-// 16 bytes at byte voff + soff of the buffer r into LDS at lds_base + 16*lane
-// (M0 = lds_base; lds_base and soff the same for the whole wavefront): one
-// 32-bit offset register per lane. Written out rather than through the
-// builtin, which the compiler treats as a write to any LDS address: it would
-// make the next LDS operand read wait for every such load issued before it.
-// The walk orders these loads itself (each wavefront waits for its own
-// loads before the barrier that precedes a tile's first read). M0 is a
-// reserved register that the compiler sets right before each of its own
-// uses and never keeps a value in across other code (this kernel has no such
-// use; tests/test_kernel_asm.py checks the compiled kernel for it), so it
-// needs no clobber.
-__device__ __forceinline__ void load_lds16(u32x4r r, uint32_t voff, uint32_t soff,
-                                           unsigned char *lds_base) {
-  const uint32_t m = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)lds_base;
-  asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff),
-               "s"(r), "s"(soff), "s"(m));
-}
-
 // This lane's index, recomputed where it is used (two vector instructions,
 // opaque to the compiler): the walk needs it only for the last tile's
 // clamped addresses, and a lane index kept live across the walk is what the

@@ -121,6 +121,32 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, 
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
                                            kBufferWord3);
 }
+// A buffer resource as four scalar words (raw buffer, no swizzle).
+typedef unsigned u32x4r __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x4r rsrc_words(const void *base, uint32_t bytes) {
+  const uint64_t ad = reinterpret_cast<uint64_t>(base);
+  return u32x4r{(uint32_t)ad, (uint32_t)(ad >> 32) & 0xffffu, bytes, (uint32_t)kBufferWord3};
+}
+
+// 16 bytes at byte voff + soff of the buffer r into LDS at lds_base + 16*lane
+// (M0 = lds_base; lds_base and soff the same for the whole wavefront): one
+// 32-bit offset register per lane. Written out rather than through the
+// builtin, which the compiler treats as a write to any LDS address: it would
+// make the next LDS operand read wait for every such load issued before it.
+// Callers order these loads themselves: a wavefront waits for its own loads
+// (s_waitcnt vmcnt) before it, or a barrier after it, reads the data, and
+// issues them only after its reads of the old contents have completed. M0 is a
+// reserved register that the compiler sets right before each of its own
+// uses and never keeps a value in across other code (the kernels that use
+// this load have no such use; tests/test_kernel_asm.py checks the compiled
+// kernels for it), so it needs no clobber.
+__device__ __forceinline__ void load_lds16(u32x4r r, uint32_t voff, uint32_t soff,
+                                           unsigned char *lds_base) {
+  const uint32_t m = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)lds_base;
+  asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff),
+               "s"(r), "s"(soff), "s"(m));
+}
+
 __device__ __forceinline__ f32x4 buffer_load4(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
   return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
