@@ -436,8 +436,9 @@ def dropin_rows_line(args, ctx, w, tq, tk, tv, tg, tqn, tkn, tm, rows_kernel_ms)
     out["rows_entry_kernel_us_per_row"] = round(rows_kernel_ms * 1e3 / R, 3)
     out["flag_over_rows_entry"] = round(out["kv_heads_flag"]["kernel_us_per_row"]
                                         / out["rows_entry_kernel_us_per_row"], 2)
-    out["note"] = ("one launch pair (K prep, attention) per 256-token row: a row fills 128 "
-                   "workgroups of 256 CUs, so per-call latency, not the GQA reads, bounds it")
+    out["note"] = ("one launch of the fused kernel per 256-token row: a row is 128 work items "
+                   "for 256 CUs, and its longest query tile walks 16 key tiles on one CU, so "
+                   "per-call latency, not the GQA reads, bounds it")
     return out
 
 
@@ -612,6 +613,29 @@ def run_only(args):
         ctx.close()
         return {"only": name, "ms_per_step": round(ms, 5), "attention_kernel_ms": round(kern, 5),
                 "tflops": round((att + gemm) / (ms * 1e-3) / 1e12, 3)}
+    if args.only == "c4row":
+        # The drop-in op once per C4 row with TFD_KV_HEADS (dropin_rows_line's
+        # flag case), for a kernel trace of the per-row path.
+        w = jeff_config(4)
+        R, L, H, KV, hd = w.rows, w.length, w.heads, w.kv_heads, w.head_dim
+        W, G = H * hd, H // KV
+        t = {n: torch.from_numpy(getattr(w, n)).to(dev)
+             for n in ("q", "k", "v", "gate", "q_norm", "k_norm", "mask")}
+        expand = lambda x: x.view(R, KV, hd * L).repeat_interleave(G, dim=1).reshape(-1).contiguous()
+        ke, ve = expand(t["k"]), expand(t["v"])
+        oj = torch.empty(R * L * W, dtype=torch.float32, device=dev)
+
+        def fn():
+            for r in range(R):
+                sl = slice(r * L * W, (r + 1) * L * W)
+                te.jeff_full_attention(t["q"][sl], ke[sl], ve[sl], t["gate"][sl], t["q_norm"],
+                                       t["k_norm"], t["mask"][r * L:(r + 1) * L], H, hd,
+                                       w.rotary_dim, w.theta, w.eps, q_shape=(L, W), ctx=ctx,
+                                       out=oj[sl], kv_heads=KV)
+        ms, kern = time_gpu(fn, args.steps, args.warmup, ctx)
+        ctx.close()
+        return {"only": "C4_dropin_per_row", "ms_per_16_rows": round(ms, 5),
+                "kernel_us_per_row": round(kern * 1e3, 3)}
     cfg = int(args.only[1])
     structured = args.only.endswith("s")
     if cfg in (2, 3):
@@ -717,7 +741,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="only the C2 headline")
-    ap.add_argument("--only", choices=["c2", "c3", "c4", "c5", "c2s", "c3s", "c2l", "c4l", "model", "copy"], default=None,
+    ap.add_argument("--only", choices=["c2", "c3", "c4", "c5", "c2s", "c3s", "c2l", "c4l", "c4row", "model", "copy"], default=None,
                     help="profiling aid: run one configuration's op (steps + warmup calls), "
                          "print its timing line and skip everything else")
     args = ap.parse_args()
