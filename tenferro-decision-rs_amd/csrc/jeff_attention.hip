@@ -1230,10 +1230,18 @@ __global__ __launch_bounds__(256, 4) void jeff_split_f32_kernel(const JeffArgs a
     if (qa < L && d < hd) buffer_store4(r, ro, otask + t * 16 * L * 4, q0 * 4);
   };
   if (kt_begin >= kt_end) {
-    // No key at or before these queries: o = 0 (lib.rs:739-743).
+    // No key at or before these queries: o = 0 (lib.rs:739-743), and
+    // 0 * sigmoid(gate) is 0 for every gate but NaN (sigmoid is in [0, 1],
+    // also at +-inf), which it propagates: no exponential needed.
     load_gate();
 #pragma unroll
-    for (int t = 0; t < NB; ++t) store_task(t, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+    for (int t = 0; t < NB; ++t) {
+      const int qa = q0 + 4 * tg4, d = wave * DS + tdl + 16 * t;
+      f32x4 r;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) r[i] = (qa + i >= start && gv[t][i] != gv[t][i]) ? gv[t][i] : 0.0f;
+      if (qa < L && d < hd) buffer_store4(r, ro, otask + t * 16 * L * 4, q0 * 4);
+    }
     return;
   }
 

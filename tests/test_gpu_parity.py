@@ -442,6 +442,40 @@ def test_jeff_masked_nonfinite_values_and_empty_rows(gpu_ctx):
     assert np.all(out[:, :3] == 0.0)  # no active key at or before these queries
 
 
+@pytest.mark.parametrize("rows,length,hd", [(5, 256, 256), (1, 64, 256), (2, 48, 64)])
+def test_jeff_nonfinite_gates(gpu_ctx, rows, length, hd):
+    """NaN, +inf and -inf gates, on queries that keep keys and on left-padded
+    query tiles that keep none: out = o * sigmoid(gate), so a padded query
+    gives 0 for every gate but NaN (sigmoid(+-inf) is 1 or 0), and a live one
+    gives o, 0 or NaN. Shapes: 5 x 256 rows at hd 256 (640 query tiles: the K
+    prep and split-head kernels), one short row at hd 256 (the fused kernel),
+    hd 64 (the general kernel)."""
+    heads, kv = 8, 2
+    rng = np.random.default_rng(9100 + length)
+    W, KW = heads * hd, kv * hd
+    q = rng.standard_normal(rows * length * W).astype(np.float32)
+    k = rng.standard_normal(rows * length * KW).astype(np.float32)
+    v = rng.standard_normal(rows * length * KW).astype(np.float32)
+    g = rng.standard_normal(rows * length * W).astype(np.float32)
+    qn = (rng.standard_normal(hd) * 0.1).astype(np.float32)
+    kn = (rng.standard_normal(hd) * 0.1).astype(np.float32)
+    mask = np.ones(rows * length, np.float32)
+    G = g.reshape(rows, W, length)
+    for r in range(rows):
+        first = min(length - 8, 16 + 7 * r)
+        mask[r * length:r * length + first] = 0.0          # whole padded query tiles
+        for j, val in enumerate((np.nan, np.inf, -np.inf)):
+            G[r, (37 * j + 5 * r) % W, (3 * j + r) % first] = val      # padded queries
+            G[r, (53 * j + 11 * r) % W, first + (5 * j + r) % (length - first)] = val  # live
+    for trim in (False, True):
+        want = oracle.jeff_rows(q, k, v, g, qn, kn, mask, rows, length, heads, kv, hd, 64,
+                                1e7, 1e-6, trim_leading=trim)
+        got = te.jeff_full_attention_rows(q, k, v, g, qn, kn, mask, rows, length, heads, kv, hd,
+                                          64, 1e7, 1e-6, trim_leading=trim, ctx=gpu_ctx)
+        assert np.isnan(want).sum() >= rows, "the case has NaN outputs"
+        assert_close(got, want, F32_TOL)
+
+
 @pytest.mark.parametrize("hd,length", [(16, 50), (256, 50), (256, 52)])
 def test_jeff_kept_nonfinite_values_propagate(gpu_ctx, hd, length):
     """Kept inf / NaN values reach exactly the outputs whose p is non-zero."""
