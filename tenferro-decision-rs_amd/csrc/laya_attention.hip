@@ -224,15 +224,15 @@ __device__ __forceinline__ f32x4 rot_hi(f32x4 x, f32x4 y, f32x4 c, f32x4 s) {
 // key rows) that land as one 16-byte [d][key .. key + 3] LDS row piece.
 // Keys at or past L read as 0. Otherwise (any hd) the commit loads and
 // rotates element by element and the prefetch is empty.
-template <int HDP, bool VEC, bool ROPE>
+template <int HDP, bool VEC, bool ROPE, int NT = 256>  // NT: threads that stage a tile
 struct LayaStage {
   static constexpr int KS = HDP + 4;        // conflict-free 16-byte row reads
   static constexpr int VS = kKeyTile + 4;   // 16 lanes of 16-byte row pieces: conflict-free
   static constexpr int KBUF = kKeyTile * KS, VBUF = HDP * VS;
   static constexpr int KTASKS = kKeyTile * HDP / 8;
   static constexpr int VTASKS = (kKeyTile / 4) * HDP;
-  static constexpr int KN = VEC ? (KTASKS + 255) / 256 : 1;
-  static constexpr int VN = VEC ? (VTASKS + 255) / 256 : 1;
+  static constexpr int KN = VEC ? (KTASKS + NT - 1) / NT : 1;
+  static constexpr int VN = VEC ? (VTASKS + NT - 1) / NT : 1;
   static constexpr int CN = ROPE ? KN : 1;
   f32x4 ka[KN], kb[KN], c[CN], s[CN];
   f32x4 v[VN];
@@ -253,14 +253,14 @@ struct LayaStage {
       }
 #pragma unroll
       for (int i = 0; i < KN; ++i) {
-        const int task = min(tid + 256 * i, KTASKS - 1);
+        const int task = min(tid + NT * i, KTASKS - 1);
         const int kk = task / (HDP / 8), cp = task % (HDP / 8);
         ok[i] = (int)(((size_t)kk * tok + 4 * cp) * 4);
         oc[i] = (kk * hh + 4 * cp) * 4;
       }
 #pragma unroll
       for (int i = 0; i < VN; ++i) {
-        const int task = min(tid + 256 * i, VTASKS - 1);
+        const int task = min(tid + NT * i, VTASKS - 1);
         const int dd = task % HDP, kq = task / HDP;
         ov[i] = (int)(((size_t)(4 * kq) * tok + dd) * 4);
       }
@@ -295,8 +295,8 @@ struct LayaStage {
       const int hh = a.half;
 #pragma unroll
       for (int i = 0; i < KN; ++i) {
-        const int task = tid + 256 * i;
-        if (KTASKS % 256 == 0 || task < KTASKS) {  // blockDim is 256
+        const int task = tid + NT * i;
+        if (KTASKS % NT == 0 || task < KTASKS) {
           const int kk = task / (HDP / 8), cp = task % (HDP / 8);
           f32x4 lo = ka[i], hi = kb[i];
           if constexpr (ROPE) {
@@ -309,15 +309,15 @@ struct LayaStage {
       }
 #pragma unroll
       for (int i = 0; i < VN; ++i) {
-        const int task = tid + 256 * i;
-        if (VTASKS % 256 == 0 || task < VTASKS) {
+        const int task = tid + NT * i;
+        if (VTASKS % NT == 0 || task < VTASKS) {
           const int dd = task % HDP, kq = task / HDP;
           *reinterpret_cast<f32x4 *>(&Vs[dd * VS + 4 * kq]) = v[i];
         }
       }
     } else {
       const int L = a.L, hd = a.hd, hh = a.half;
-      for (int e = tid; e < kKeyTile * HDP; e += 256) {
+      for (int e = tid; e < kKeyTile * HDP; e += NT) {
         const int kk = e / HDP, dd = e % HDP;
         const int key = k0 + kk;
         float kv = 0.0f, vv = 0.0f;
@@ -455,19 +455,28 @@ __device__ __noinline__ void laya_redo_wave(const LayaArgs *ap, int b, int head,
 // ALU share the SIMD (they never run at the same time), so the walk keeps its
 // vector work per tile small and relies on other waves to cover memory and
 // barrier waits.
-template <int HDP, int MODE, bool VEC, bool ROPE, bool VW>
-__global__ __launch_bounds__(256, laya_groups_per_cu(HDP)) void laya_attention_kernel(
+template <int HDP, int MODE, bool VEC, bool ROPE, bool VW, int TEAMS, int QW>
+__global__ __launch_bounds__(64 * QW * TEAMS, TEAMS == 1 ? laya_groups_per_cu(HDP) : 1) void laya_attention_kernel(
     const LayaArgs a) {
-  using Stage = LayaStage<HDP, VEC, ROPE>;
+  static_assert(QW == 4 || (QW == 2 && TEAMS > 1), "16 queries per wave, 4 or 2 waves per team");
+  constexpr int NT = 64 * QW;  // threads per team
+  using Stage = LayaStage<HDP, VEC, ROPE, NT>;
   constexpr int KS = Stage::KS, VS = Stage::VS;
   constexpr int QS = HDP / 4;   // Q registers per lane (4 lane groups split hd)
   constexpr int NB = HDP / 16;  // 16-row blocks of O^T
-  constexpr int GQ = kLayaGroupQueries;
-  __shared__ __attribute__((aligned(16))) float smem[2 * (Stage::KBUF + Stage::VBUF)];
-  auto Ks = [&](int i) { return smem + i * Stage::KBUF; };
-  auto Vs = [&](int i) { return smem + 2 * Stage::KBUF + i * Stage::VBUF; };
+  constexpr int GQ = kLayaWaveQueries * QW;  // queries per workgroup
+  // TEAMS > 1 (grids of at most one workgroup per CU): TEAMS teams of four
+  // waves, each with its own K/V buffers, walk every TEAMS-th key tile of
+  // the workgroup's span and merge their (m, l, O) once at the end.
+  constexpr int TB = 2 * (Stage::KBUF + Stage::VBUF);  // floats per team
+  static_assert(TEAMS == 1 || (TEAMS - 1) * 4 * (4 * (HDP / 16) + 2) * 64 + 4 * kKeyTile * 17 <= TEAMS * TB,
+                "merge data and the redo rows fit in the teams' K/V buffers");
+  __shared__ __attribute__((aligned(16))) float smem[TEAMS * TB];
+  const int team = TEAMS == 1 ? 0 : __builtin_amdgcn_readfirstlane((int)threadIdx.x / NT);
+  auto Ks = [&](int i) { return smem + team * TB + i * Stage::KBUF; };
+  auto Vs = [&](int i) { return smem + team * TB + 2 * Stage::KBUF + i * Stage::VBUF; };
 
-  const int tid = threadIdx.x, lane = tid & 63;
+  const int tid = TEAMS == 1 ? (int)threadIdx.x : (int)(threadIdx.x & (NT - 1)), lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform, in a scalar register
   const int col = lane & 15, grp = lane >> 4;
   const int L = a.L, hd = a.hd, hh = a.half, nkt = a.nkt;
@@ -485,7 +494,7 @@ __global__ __launch_bounds__(256, laya_groups_per_cu(HDP)) void laya_attention_k
   int b = blockIdx.z, head = blockIdx.y, qb = blockIdx.x;
   int kt_begin = 0, kt_end = 0;
   const int nqb = gridDim.x, H = gridDim.y, B = gridDim.z;
-  const bool xcd = laya_xcd_layout(nqb, H, B, laya_groups_per_cu(HDP), a.cus);
+  const bool xcd = TEAMS == 1 && QW == 4 && laya_xcd_layout(nqb, H, B, laya_groups_per_cu(HDP), a.cus);
   const bool planned = a.any != nullptr && xcd && nqb * B <= kLayaPlanMax;
   {
     const int p = blockIdx.x + nqb * (blockIdx.y + H * blockIdx.z);
@@ -534,13 +543,14 @@ __global__ __launch_bounds__(256, laya_groups_per_cu(HDP)) void laya_attention_k
   bool padded = false;
   if (MODE != kMaskBits) {
     const int qx = qg0 + lane;
+    const bool mine = lane < GQ;  // lane = one of the workgroup's queries
     const uint8_t xv = vb[min(qx, L - 1)];
-    padded = __ballot(qx < L && xv == 0) != 0;
+    padded = __ballot(mine && qx < L && xv == 0) != 0;
     // A caller that reads only some queries' outputs (the model forward)
     // skips groups without one. Every wave takes the same branch before any
     // barrier, so the workgroup leaves as a whole.
     if (a.qneed != nullptr &&
-        __ballot(qx < L && a.qneed[(size_t)b * L + min(qx, L - 1)] != 0) == 0)
+        __ballot(mine && qx < L && a.qneed[(size_t)b * L + min(qx, L - 1)] != 0) == 0)
       return;
   }
 
@@ -640,6 +650,15 @@ __global__ __launch_bounds__(256, laya_groups_per_cu(HDP)) void laya_attention_k
   // counters and offsets.
   kt_begin = __builtin_amdgcn_readfirstlane(kt_begin);
   kt_end = __builtin_amdgcn_readfirstlane(kt_end);
+  // This team's tiles: those of [kt_begin, kt_end) with kt % TEAMS == team,
+  // from tb in steps of TEAMS (a choice that depends on the tile index only,
+  // not on the span, so that two spans of the same keep pattern give the
+  // same sums); every team runs the same number of steps (one barrier each).
+  int tb = kt_begin, te = kt_end, kt_stop = kt_end;
+  if constexpr (TEAMS > 1) {
+    tb = kt_begin + ((team - kt_begin) % TEAMS + TEAMS) % TEAMS;
+    kt_stop = kt_begin + (kt_end - kt_begin + TEAMS - 1) / TEAMS * TEAMS + (tb - kt_begin);
+  }
 
   // This lane's keep word for key tile kt (bit j: key 32*kt + j). The raw
   // word or validity byte is fetched one tile ahead (mask_of) and turned
@@ -659,9 +678,9 @@ __global__ __launch_bounds__(256, laya_groups_per_cu(HDP)) void laya_attention_k
   Stage st;
   st.init(a, xb, tok, tid);
   uint32_t m0 = 0u;
-  if (kt_begin < kt_end) {
-    m0 = mask_of(kt_begin);
-    st.fetch(kt_begin * kKeyTile);
+  if (tb < te) {
+    m0 = mask_of(tb);
+    st.fetch(tb * kKeyTile);
   }
 
   if constexpr (VEC) {
@@ -738,9 +757,9 @@ __global__ __launch_bounds__(256, laya_groups_per_cu(HDP)) void laya_attention_k
   // inf value reaches O and stays there, and either way the wave redoes its
   // queries with the reference's exact semantics after the walk.
   uint32_t w = 0u, m_next = 0u;
-  if (kt_begin < kt_end) {
-    st.commit(a, xb, tok, kt_begin * kKeyTile, tid, Ks(0), Vs(0));
-    w = keep_word(kt_begin, m0);
+  if (tb < te) {
+    st.commit(a, xb, tok, tb * kKeyTile, tid, Ks(0), Vs(0));
+    w = keep_word(tb, m0);
   }
   __syncthreads();
   // Nothing may still be in flight when the walk starts: otherwise the
@@ -750,13 +769,14 @@ __global__ __launch_bounds__(256, laya_groups_per_cu(HDP)) void laya_attention_k
   __builtin_amdgcn_s_waitcnt(0);
   bool tainted = false;  // wave-uniform
   int cur = 0;
-  for (int kt = kt_begin; kt < kt_end; ++kt) {
-    const bool more = kt + 1 < kt_end;
+  for (int kt = tb; kt < kt_stop; kt += TEAMS) {
+    const bool act = TEAMS == 1 || kt < te;  // a team with fewer tiles idles at its last step
+    const bool more = kt + TEAMS < te;
     if (more) {
-      m_next = mask_of(kt + 1);
-      st.fetch((kt + 1) * kKeyTile);
+      m_next = mask_of(kt + TEAMS);
+      st.fetch((kt + TEAMS) * kKeyTile);
     }
-    if (!tainted && __ballot(w != 0u) != 0) {  // wave-uniform
+    if (act && !tainted && __ballot(w != 0u) != 0) {  // wave-uniform
       // S^T: K rows from LDS against the Q registers, two independent chains.
       f32x4 s0 = {0.0f, 0.0f, 0.0f, 0.0f}, s1 = {0.0f, 0.0f, 0.0f, 0.0f};
       {
@@ -832,9 +852,9 @@ __global__ __launch_bounds__(256, laya_groups_per_cu(HDP)) void laya_attention_k
         }
       }
     }
-    if (more) st.commit(a, xb, tok, (kt + 1) * kKeyTile, tid, Ks(cur ^ 1), Vs(cur ^ 1));
+    if (more) st.commit(a, xb, tok, (kt + TEAMS) * kKeyTile, tid, Ks(cur ^ 1), Vs(cur ^ 1));
     __syncthreads();
-    if (more) w = keep_word(kt + 1, m_next);
+    if (more) w = keep_word(kt + TEAMS, m_next);
     cur ^= 1;
   }
 
@@ -846,13 +866,56 @@ __global__ __launch_bounds__(256, laya_groups_per_cu(HDP)) void laya_attention_k
   for (int j = 0; j < NB; ++j)
 #pragma unroll
     for (int r = 0; r < 4; ++r) bad |= !__builtin_isfinite(O[j][r]);
-  if (tainted || __ballot(qin && bad) != 0) {
+  bool redo = tainted || __ballot(qin && bad) != 0;
+  if constexpr (TEAMS > 1) {
+    // Teams 1 .. TEAMS-1 hand their (m, l, O) for the same queries to team
+    // 0 through LDS (the K/V buffers: every wave is past the walk's last
+    // barrier), with their redo flags; team 0 merges them, or redoes the
+    // whole span when any part met a non-finite value.
+    constexpr int MF = 4 * NB + 2;  // floats per lane: O, m, l
+    __shared__ int s_redo[TEAMS * 4];
+    float *mg = smem + ((team - 1) * 4 + wave) * MF * 64;
+    if (team > 0) {
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) mg[(4 * j + r) * 64 + lane] = O[j][r];
+      mg[4 * NB * 64 + lane] = m;
+      mg[(4 * NB + 1) * 64 + lane] = l;
+    }
+    if (lane == 0) s_redo[team * 4 + wave] = redo ? 1 : 0;
+    __syncthreads();
+    if (team > 0) return;
+#pragma unroll
+    for (int t = 1; t < TEAMS; ++t) redo |= s_redo[t * 4 + wave] != 0;
+    if (!redo) {
+      float M = m;
+#pragma unroll
+      for (int t = 1; t < TEAMS; ++t) M = fmaxf(M, smem[((t - 1) * 4 + wave) * MF * 64 + 4 * NB * 64 + lane]);
+      const float f0 = fast_exp2(m - M);  // 1 for the part that holds the max
+      l *= f0;
+#pragma unroll
+      for (int j = 0; j < NB; ++j) O[j] *= f0;
+#pragma unroll
+      for (int t = 1; t < TEAMS; ++t) {
+        const float *src = smem + ((t - 1) * 4 + wave) * MF * 64;
+        const float ft = fast_exp2(src[4 * NB * 64 + lane] - M);
+        l += ft * src[(4 * NB + 1) * 64 + lane];
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) O[j][r] += ft * src[(4 * j + r) * 64 + lane];
+      }
+    }
+  }
+  if (redo) {
     // The kernel's LayaArgs (its first parameter, at offset 0 of the kernel
     // argument segment): passing the struct by value would copy it to
     // scratch.
     laya_redo_wave<HDP, MODE, ROPE>((const LayaArgs *)__builtin_amdgcn_kernarg_segment_ptr(), b,
                                     head, q0w, kt_begin, kt_end,
-                                    smem + wave * kKeyTile * 17);
+                                    smem + (TEAMS > 1 ? (TEAMS - 1) * 4 * (4 * NB + 2) * 64 : 0) +
+                                        wave * kKeyTile * 17);
     return;
   }
 
@@ -929,20 +992,41 @@ hipError_t launch_laya_valid_prep(const uint8_t *valid, uint32_t *words, uint8_t
   return hipGetLastError();
 }
 
+template <int HDP, bool VEC, bool ROPE, int TEAMS, int QW>
+static hipError_t launch_laya_teams(const LayaArgs &a, dim3 grid, int mode, hipStream_t stream,
+                                    const KernelEvents &ev) {
+  const dim3 block(64 * QW * TEAMS);
+  if (mode == kMaskBits)
+    hipExtLaunchKernelGGL((laya_attention_kernel<HDP, kMaskBits, VEC, ROPE, false, TEAMS, QW>),
+                          grid, block, 0, stream, ev.start, ev.stop, 0, a);
+  else if (a.bits != nullptr)
+    hipExtLaunchKernelGGL((laya_attention_kernel<HDP, kMaskStruct, VEC, ROPE, true, TEAMS, QW>),
+                          grid, block, 0, stream, ev.start, ev.stop, 0, a);
+  else
+    hipExtLaunchKernelGGL((laya_attention_kernel<HDP, kMaskStruct, VEC, ROPE, false, TEAMS, QW>),
+                          grid, block, 0, stream, ev.start, ev.stop, 0, a);
+  return hipGetLastError();
+}
+
 template <int HDP, bool VEC, bool ROPE>
 static hipError_t launch_laya_hd(const LayaArgs &a, int heads, int batch, int mode,
                                  hipStream_t stream, const KernelEvents &ev) {
-  dim3 grid((a.L + kLayaGroupQueries - 1) / kLayaGroupQueries, heads, batch);
-  if (mode == kMaskBits)
-    hipExtLaunchKernelGGL((laya_attention_kernel<HDP, kMaskBits, VEC, ROPE, false>), grid,
-                          dim3(256), 0, stream, ev.start, ev.stop, 0, a);
-  else if (a.bits != nullptr)
-    hipExtLaunchKernelGGL((laya_attention_kernel<HDP, kMaskStruct, VEC, ROPE, true>), grid,
-                          dim3(256), 0, stream, ev.start, ev.stop, 0, a);
-  else
-    hipExtLaunchKernelGGL((laya_attention_kernel<HDP, kMaskStruct, VEC, ROPE, false>), grid,
-                          dim3(256), 0, stream, ev.start, ev.stop, 0, a);
-  return hipGetLastError();
+  const unsigned ng = (a.L + kLayaGroupQueries - 1) / kLayaGroupQueries;
+  // A grid of at most one 64-query workgroup per CU would leave each CU one
+  // wave per SIMD walking every key tile of its span, latency-bound: split
+  // the span over teams of waves instead (four teams at hd <= 64, two at
+  // 128, as the teams' K/V buffers fit in LDS), and where even half the CUs
+  // would suffice, give each workgroup 32 queries (two waves per team), so
+  // that every CU gets one.
+  const long groups = (long)ng * heads * batch;
+  if (a.cus > 0 && a.nkt > 1 && groups * 2 <= a.cus) {
+    const dim3 grid((a.L + 2 * kLayaWaveQueries - 1) / (2 * kLayaWaveQueries), heads, batch);
+    return launch_laya_teams<HDP, VEC, ROPE, laya_teams(HDP), 2>(a, grid, mode, stream, ev);
+  }
+  const dim3 grid(ng, heads, batch);
+  if (a.cus > 0 && a.nkt > 1 && groups <= a.cus)
+    return launch_laya_teams<HDP, VEC, ROPE, laya_teams(HDP), 4>(a, grid, mode, stream, ev);
+  return launch_laya_teams<HDP, VEC, ROPE, 1, 4>(a, grid, mode, stream, ev);
 }
 
 template <int HDP>

@@ -26,6 +26,11 @@ __host__ __device__ constexpr int laya_map_row(int nkt) { return (nkt + 63) & ~6
 // two at 128.
 __host__ __device__ constexpr int laya_groups_per_cu(int hd_pad) { return hd_pad <= 64 ? 4 : 2; }
 
+// Teams of four waves per Laya workgroup when the grid has at most one
+// workgroup per CU: as many as the teams' double-buffered K/V tiles fit in a
+// CU's LDS (four at padded head dims up to 64, two at 128).
+__host__ __device__ constexpr int laya_teams(int hd_pad) { return hd_pad <= 64 ? 4 : 2; }
+
 // Whether a Laya grid of nqb x H x B workgroups gets the XCD-aware layout:
 // the whole grid fits in one dispatch round (workgroup p then runs on XCD
 // p % 8 and CU slot p % cus) and each of the 8 XCDs can take an equal share
