@@ -18,6 +18,8 @@
 // 16 queries keep nothing in a tile skips its MFMAs. Small workgroups (four
 // per CU) keep the per-tile critical path short and the work per CU even
 // when rows differ in length.
+#include <type_traits>
+
 #include "tfd_device.hpp"
 #include "tfd_internal.hpp"
 
@@ -379,6 +381,11 @@ __device__ __noinline__ void laya_redo_wave(const LayaArgs *ap, int b, int head,
     if (MODE == kMaskBits) {
       const uint32_t x = a.bits[((size_t)b * nkt + kt) * L + qq];
       wk = qin ? x : 0u;
+    } else if (MODE == kMaskRaw) {
+      uint32_t x = 0u;
+      for (int j = 0; j < kKeyTile && k0 + j < L; ++j)
+        x |= (uint32_t)(a.keep[(size_t)b * L * L + (size_t)(k0 + j) * L + qq] != 0) << j;
+      wk = qin ? x : 0u;
     } else {
       const int key = k0 + (lane & 31);
       const bool kv = key < L && a.valid[(size_t)b * L + min(key, L - 1)] != 0;
@@ -540,8 +547,11 @@ __global__ __launch_bounds__(64 * QW * TEAMS, TEAMS == 1 ? laya_groups_per_cu(HD
   // kMaskBits: the workgroup's 64 queries are exactly tile-map group qg0 / 64.
   const uint8_t *anyb = a.any + ((size_t)b * ng + qg0 / 64) * laya_map_row(nkt);
   const uint8_t *vb = a.valid + (size_t)b * L;  // kMaskStruct
+  const __amdgpu_buffer_rsrc_t rkeep =  // kMaskRaw: this batch row's keep bytes
+      buffer_rsrc(MODE == kMaskRaw ? a.keep + (size_t)b * L * L : nullptr,
+                  MODE == kMaskRaw ? (uint32_t)((size_t)L * L) : 0u);
   bool padded = false;
-  if (MODE != kMaskBits) {
+  if (MODE == kMaskStruct) {
     const int qx = qg0 + lane;
     const bool mine = lane < GQ;  // lane = one of the workgroup's queries
     const uint8_t xv = vb[min(qx, L - 1)];
@@ -598,6 +608,11 @@ __global__ __launch_bounds__(64 * QW * TEAMS, TEAMS == 1 ? laya_groups_per_cu(HD
   };
   if (planned) {
     // the span came with the plan entry
+  } else if (MODE == kMaskRaw) {
+    // Every tile for now: the first tiles are fetched on that guess while
+    // the workgroup scans its queries' keep bytes for the real span (below).
+    kt_begin = 0;
+    kt_end = nkt;
   } else if (MODE == kMaskBits) {
     // The group's row of the tile map, 64 flags (16 words) per scalar load.
     const uint32_t *anyw = reinterpret_cast<const uint32_t *>(anyb);
@@ -655,10 +670,12 @@ __global__ __launch_bounds__(64 * QW * TEAMS, TEAMS == 1 ? laya_groups_per_cu(HD
   // not on the span, so that two spans of the same keep pattern give the
   // same sums); every team runs the same number of steps (one barrier each).
   int tb = kt_begin, te = kt_end, kt_stop = kt_end;
-  if constexpr (TEAMS > 1) {
+  auto team_span = [&]() {
     tb = kt_begin + ((team - kt_begin) % TEAMS + TEAMS) % TEAMS;
+    te = kt_end;
     kt_stop = kt_begin + (kt_end - kt_begin + TEAMS - 1) / TEAMS * TEAMS + (tb - kt_begin);
-  }
+  };
+  if constexpr (TEAMS > 1) team_span();
 
   // This lane's keep word for key tile kt (bit j: key 32*kt + j). The raw
   // word or validity byte is fetched one tile ahead (mask_of) and turned
@@ -667,20 +684,56 @@ __global__ __launch_bounds__(64 * QW * TEAMS, TEAMS == 1 ? laya_groups_per_cu(HD
   // kMaskStruct reads the rows' valid-key words (VW: the prep gave them,
   // planned grids), else the validity bytes of the tile's keys.
   constexpr bool vwords = MODE == kMaskStruct && VW;
-  auto mask_of = [&](int kt) -> uint32_t {
-    if (MODE == kMaskBits)
-      return a.bits[((size_t)b * nkt + min(kt, nkt - 1)) * L + min(q, L - 1)];
-    if (vwords) return a.bits[(size_t)b * nkt + min(kt, nkt - 1)];  // uniform
-    return a.valid[(size_t)b * L + min(kt * kKeyTile + (lane & 31), L - 1)];
+  // kMaskRaw: lanes 0..31 fetch the keep bytes of key 32*kt + lane for the
+  // wave's 16 queries (one 16-byte piece of that key's row; a key past L
+  // reads 0), turned into the 16 queries' words by ballots.
+  using MaskT = typename std::conditional<MODE == kMaskRaw, uint4, uint32_t>::type;
+  auto raw_of = [&](int kt) -> uint4 {
+    const int key = kt * kKeyTile + (lane & 31);
+    const f32x4 v = buffer_load4(rkeep, key * L + q0w, 0);
+    return make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                      __float_as_uint(v[3]));
+  };
+  auto mask_of = [&](int kt) -> MaskT {
+    if constexpr (MODE == kMaskRaw) {
+      return raw_of(kt);
+    } else {
+      if (MODE == kMaskBits)
+        return a.bits[((size_t)b * nkt + min(kt, nkt - 1)) * L + min(q, L - 1)];
+      if (vwords) return a.bits[(size_t)b * nkt + min(kt, nkt - 1)];  // uniform
+      return a.valid[(size_t)b * L + min(kt * kKeyTile + (lane & 31), L - 1)];
+    }
   };
 
   // The first tile's loads go out before the Q rotation waits for its rows.
   Stage st;
   st.init(a, xb, tok, tid);
-  uint32_t m0 = 0u;
+  MaskT m0{};
   if (tb < te) {
     m0 = mask_of(tb);
     st.fetch(tb * kKeyTile);
+  }
+  // kMaskRaw: the lowest and highest key any query of the workgroup keeps,
+  // per wave (lane = key; a piece that runs past the last query reads the
+  // next key's bytes, which can only widen the span).
+  __shared__ int s_rspan[MODE == kMaskRaw ? 2 * TEAMS * QW : 1];
+  if constexpr (MODE == kMaskRaw) {
+    const int wg = (int)(threadIdx.x >> 6), nw = (int)(blockDim.x >> 6);
+    for (int k0 = wg * 64; k0 < L; k0 += nw * 64) {  // lo, hi: still empty here
+      const int k = k0 + lane;
+      uint32_t any = 0u;
+#pragma unroll
+      for (int c = 0; c < GQ / 16; ++c) {
+        const f32x4 v = buffer_load4(rkeep, k * L + qg0 + 16 * c, 0);
+        any |= __float_as_uint(v[0]) | __float_as_uint(v[1]) | __float_as_uint(v[2]) |
+               __float_as_uint(v[3]);
+      }
+      span_add(__ballot(k < L && any != 0u), k0);
+    }
+    if (lane == 0) {
+      s_rspan[2 * wg] = lo;
+      s_rspan[2 * wg + 1] = hi;
+    }
   }
 
   if constexpr (VEC) {
@@ -717,9 +770,20 @@ __global__ __launch_bounds__(64 * QW * TEAMS, TEAMS == 1 ? laya_groups_per_cu(HD
     q_valid = qin && x != 0;
   }
 
-  auto keep_word = [&](int kt, uint32_t x) -> uint32_t {
+  auto keep_word = [&](int kt, MaskT x) -> uint32_t {
     uint32_t w = 0u;
-    if (MODE == kMaskBits) {
+    if constexpr (MODE == kMaskRaw) {
+      // Query q0w + c keeps key 32*kt + j when byte c of lane j's piece is
+      // non-zero: one ballot per query, and this lane takes its query's.
+      const uint32_t words[4] = {x.x, x.y, x.z, x.w};
+      const bool kl = lane < kKeyTile;
+#pragma unroll
+      for (int c = 0; c < 16; ++c) {
+        const uint32_t mk = (uint32_t)__ballot(kl && ((words[c / 4] >> (8 * (c % 4))) & 0xffu) != 0u);
+        w = col == c ? mk : w;
+      }
+      w = qin ? w : 0u;
+    } else if (MODE == kMaskBits) {
       w = qin ? x : 0u;
     } else {
       const int k0 = kt * kKeyTile;
@@ -756,12 +820,37 @@ __global__ __launch_bounds__(64 * QW * TEAMS, TEAMS == 1 ? laya_groups_per_cu(HD
   // stops computing (it still stages tiles and meets the barriers), a NaN or
   // inf value reaches O and stays there, and either way the wave redoes its
   // queries with the reference's exact semantics after the walk.
-  uint32_t w = 0u, m_next = 0u;
+  uint32_t w = 0u;
+  MaskT m_next{};
   if (tb < te) {
     st.commit(a, xb, tok, tb * kKeyTile, tid, Ks(0), Vs(0));
     w = keep_word(tb, m0);
   }
   __syncthreads();
+  if constexpr (MODE == kMaskRaw) {
+    // The real span (uniform): a shorter end only trims the walk; a later
+    // start puts other tiles first, which are fetched and committed now.
+    int rlo = 0x7fffffff, rhi = -1;
+    for (int i = 0; i < (int)(blockDim.x >> 6); ++i) {
+      rlo = min(rlo, s_rspan[2 * i]);
+      rhi = max(rhi, s_rspan[2 * i + 1]);
+    }
+    const int nb = rhi >= 0 ? rlo / kKeyTile : 0, ne = rhi >= 0 ? rhi / kKeyTile + 1 : 0;
+    const bool moved = __builtin_amdgcn_readfirstlane(nb) != kt_begin;
+    kt_begin = __builtin_amdgcn_readfirstlane(nb);
+    kt_end = __builtin_amdgcn_readfirstlane(ne);
+    team_span();
+    if (moved) {
+      w = 0u;
+      if (tb < te) {
+        m0 = mask_of(tb);
+        st.fetch(tb * kKeyTile);
+        st.commit(a, xb, tok, tb * kKeyTile, tid, Ks(0), Vs(0));
+        w = keep_word(tb, m0);
+      }
+      __syncthreads();
+    }
+  }
   // Nothing may still be in flight when the walk starts: otherwise the
   // compiler can carry a prologue load's register into the loop's wait
   // bookkeeping and make every tile's first product wait for the prefetch of
@@ -996,6 +1085,14 @@ template <int HDP, bool VEC, bool ROPE, int TEAMS, int QW>
 static hipError_t launch_laya_teams(const LayaArgs &a, dim3 grid, int mode, hipStream_t stream,
                                     const KernelEvents &ev) {
   const dim3 block(64 * QW * TEAMS);
+  if constexpr (TEAMS > 1) {
+    if (mode == kMaskRaw) {
+      hipExtLaunchKernelGGL((laya_attention_kernel<HDP, kMaskRaw, VEC, ROPE, false, TEAMS, QW>),
+                            grid, block, 0, stream, ev.start, ev.stop, 0, a);
+      return hipGetLastError();
+    }
+  }
+  if (mode == kMaskRaw) return hipErrorInvalidValue;  // only the teams variant packs keep bytes
   if (mode == kMaskBits)
     hipExtLaunchKernelGGL((laya_attention_kernel<HDP, kMaskBits, VEC, ROPE, false, TEAMS, QW>),
                           grid, block, 0, stream, ev.start, ev.stop, 0, a);
@@ -1019,12 +1116,14 @@ static hipError_t launch_laya_hd(const LayaArgs &a, int heads, int batch, int mo
   // would suffice, give each workgroup 32 queries (two waves per team), so
   // that every CU gets one.
   const long groups = (long)ng * heads * batch;
+  if (!laya_teams_grid(a.L, heads, batch, a.nkt, a.cus) && mode == kMaskRaw)
+    return hipErrorInvalidValue;
   if (a.cus > 0 && a.nkt > 1 && groups * 2 <= a.cus) {
     const dim3 grid((a.L + 2 * kLayaWaveQueries - 1) / (2 * kLayaWaveQueries), heads, batch);
     return launch_laya_teams<HDP, VEC, ROPE, laya_teams(HDP), 2>(a, grid, mode, stream, ev);
   }
   const dim3 grid(ng, heads, batch);
-  if (a.cus > 0 && a.nkt > 1 && groups <= a.cus)
+  if (laya_teams_grid(a.L, heads, batch, a.nkt, a.cus))
     return launch_laya_teams<HDP, VEC, ROPE, laya_teams(HDP), 4>(a, grid, mode, stream, ev);
   return launch_laya_teams<HDP, VEC, ROPE, 1, 4>(a, grid, mode, stream, ev);
 }

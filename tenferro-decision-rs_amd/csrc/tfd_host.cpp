@@ -439,7 +439,12 @@ int laya_run(tfd_ctx *c, const char *op, const float *qkv, const uint8_t *keep,
             "laya_generic launch");
     return finish(c, flags, out, out_d, sizeof(float) * n);
   }
-  if (keep) {
+  if (keep && tfd::laya_raw_keep(a.L, (int)heads, (int)batch, a.nkt, c->cus)) {
+    // A small grid: the attention kernel packs the keep bytes itself (no
+    // packing pass, no workspace).
+    mode = tfd::kMaskRaw;
+    a.keep = static_cast<const uint8_t *>(mask_d);
+  } else if (keep) {
     mode = tfd::kMaskBits;
     // Workspace: the packed words, then the per-(tile, 64-query group) map.
     size_t words = 0, groups = 0;

@@ -48,6 +48,7 @@ constexpr int kLayaPlanMax = 1024;
 enum LayaMaskMode : int {
   kMaskBits = 0,    // general (L, L, B) keep tensor, pre-packed into 32-key words
   kMaskStruct = 1,  // valid (L, B) + window (build_mask semantics)
+  kMaskRaw = 2,     // the (L, L, B) keep bytes themselves, packed by the attention kernel
 };
 
 struct LayaArgs {
@@ -60,6 +61,7 @@ struct LayaArgs {
   const uint8_t *valid;  // kMaskStruct: (L, B)
   const uint8_t *qneed;  // kMaskStruct, or null: (L, B), a 64-query group with no
                          // non-zero entry is skipped (its output left unwritten)
+  const uint8_t *keep;   // kMaskRaw: byte b*L*L + key*L + query, kept when non-zero
   const float *cos_t;    // (L, half) or nullptr (no RoPE)
   const float *sin_t;
   float *out;            // (d, L, B)
@@ -109,6 +111,18 @@ hipError_t launch_laya_valid_prep(const uint8_t *valid, uint32_t *words, uint8_t
                                   int B, int nkt, int window, hipStream_t stream);
 // Whether a grid of (L, heads, batch) at padded head dim hd_pad gets the
 // placement plan from a tile map (one dispatch round, laya_xcd_layout).
+// Whether a Laya grid takes the teams variant of the attention kernel (at
+// most one 64-query workgroup per CU, more than one key tile), and whether
+// that variant packs the keep bytes itself (kMaskRaw: whole rows of 16-byte
+// pieces, L % 4 == 0) instead of a packing pass.
+inline bool laya_teams_grid(int L, int heads, int batch, int nkt, int cus) {
+  const long groups = (long)((L + kLayaGroupQueries - 1) / kLayaGroupQueries) * heads * batch;
+  return cus > 0 && nkt > 1 && groups <= cus;
+}
+inline bool laya_raw_keep(int L, int heads, int batch, int nkt, int cus) {
+  return laya_teams_grid(L, heads, batch, nkt, cus) && L % 4 == 0 &&
+         (size_t)L * (size_t)L < ((size_t)1 << 31);
+}
 inline bool laya_planned(int L, int heads, int batch, int hd_pad, int cus) {
   const int nqb = (L + kLayaGroupQueries - 1) / kLayaGroupQueries;
   return laya_xcd_layout(nqb, heads, batch, laya_groups_per_cu(hd_pad), cus) &&

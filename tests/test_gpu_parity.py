@@ -115,6 +115,38 @@ def test_laya_sweep_keep_and_structured(gpu_ctx, length, hd):
             assert np.array_equal(np.asarray(st).view(np.uint32), np.asarray(got).view(np.uint32))
 
 
+@pytest.mark.parametrize("L,B,heads,hd,window", [(516, 1, 4, 64, -1), (256, 2, 8, 64, 40),
+                                                 (130, 1, 2, 64, -1), (384, 1, 2, 128, -1),
+                                                 (96, 1, 3, 32, 9), (512, 1, 24, 64, -1)])
+def test_laya_small_grid_teams(gpu_ctx, L, B, heads, hd, window):
+    """Grids of at most one 64-query group per CU take the teams variant (key
+    tiles dealt to teams of waves, merged at the end; 32-query workgroups
+    where half the CUs suffice). With L % 4 == 0 the kernel packs the keep
+    bytes itself (no packing pass): L 516 has a partial last query wave and
+    key tile; L 130 takes the packing pass; L 512 x 24 heads (192 groups)
+    keeps 64-query workgroups. Random keep patterns with queries
+    that keep nothing (NaN rows), against the oracle; the structured entry
+    must give the same bits as the keep entry."""
+    d = heads * hd
+    rng = np.random.default_rng(8800 + L + hd)
+    qkv = rng.standard_normal(3 * d * L * B).astype(np.float32)
+    keep = (rng.random(L * L * B) < 0.6).astype(np.uint8)
+    K = keep.reshape(B, L, L)                  # [b][key][query]
+    K[:, :, 3] = 0                             # query 3 keeps nothing: NaN row
+    K[:, : L // 3, L - 1] = 0                  # the last query keeps only the later keys
+    got = laya_gpu(gpu_ctx, qkv, keep, d, heads, L, B, 160000.0)
+    want = oracle.laya_attention_block(qkv, keep, d, heads, L, B, 160000.0)
+    assert np.isnan(np.asarray(want)).any()
+    assert_close(got, want, F32_TOL)
+    valid = np.ones(L * B, np.uint8)
+    valid[L - 5:L] = 0                          # padded tail of row 0
+    sk = oracle.laya_build_mask(valid, L, B, window)
+    st = te.laya_attention_structured(qkv, valid, d, heads, L, B, window, 10000.0, ctx=gpu_ctx)
+    kp = laya_gpu(gpu_ctx, qkv, sk, d, heads, L, B, 10000.0)
+    assert_close(kp, oracle.laya_attention_block(qkv, sk, d, heads, L, B, 10000.0), F32_TOL)
+    assert np.array_equal(np.asarray(st).view(np.uint32), np.asarray(kp).view(np.uint32))
+
+
 @pytest.mark.parametrize("excluded", [1.0, float("nan"), float("inf"), float("-inf")])
 def test_laya_masked_nonfinite_values_and_empty_rows(gpu_ctx, excluded):
     """cpu-kernels lib.rs:1212-1250 on the GPU."""
