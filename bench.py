@@ -613,6 +613,20 @@ def run_only(args):
         ctx.close()
         return {"only": name, "ms_per_step": round(ms, 5), "attention_kernel_ms": round(kern, 5),
                 "tflops": round((att + gemm) / (ms * 1e-3) / 1e12, 3)}
+    if args.only == "micro":
+        # The reference micro-benchmark's largest shape (L 512, B 1, d 1024,
+        # 16 heads, global keep k % 13 != 7): the small-grid Laya path.
+        L, d, H = 512, 1024, 16
+        qkv, keep = micro_inputs(L, 1, None)
+        flops = 4 * (d // H) * int(keep.astype(np.int64).sum()) * H
+        tq, tk = torch.from_numpy(qkv).to(dev), torch.from_numpy(keep).to(dev)
+        to = torch.empty(d * L, dtype=torch.float32, device=dev)
+        fn = lambda: te.laya_attention_block(tq, tk, d, H, 160000.0, qkv_shape=(3 * d, L, 1),
+                                             ctx=ctx, out=to)
+        ms, kern = time_gpu(fn, args.steps, args.warmup, ctx)
+        ctx.close()
+        return {"only": "micro L512 B1", "ms_per_step": round(ms, 5), "kernel_ms": round(kern, 5),
+                "tflops": round(flops / (ms * 1e-3) / 1e12, 3)}
     if args.only == "c4row":
         # The drop-in op once per C4 row with TFD_KV_HEADS (dropin_rows_line's
         # flag case), for a kernel trace of the per-row path.
@@ -741,7 +755,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="only the C2 headline")
-    ap.add_argument("--only", choices=["c2", "c3", "c4", "c5", "c2s", "c3s", "c2l", "c4l", "c4row", "model", "copy"], default=None,
+    ap.add_argument("--only", choices=["c2", "c3", "c4", "c5", "c2s", "c3s", "c2l", "c4l", "c4row", "micro", "model", "copy"], default=None,
                     help="profiling aid: run one configuration's op (steps + warmup calls), "
                          "print its timing line and skip everything else")
     args = ap.parse_args()
