@@ -1081,6 +1081,28 @@ __device__ __noinline__ void jeff_redo_wave(const JeffArgs *ap, const float *__r
 
 // ------------------------------------------------- f32 attention, split head
 
+// (row, head) of work unit u < rows * heads of the split-head and fused
+// kernels, whose grids are (units, query tiles) and dispatch in the linear
+// order u + units * y, workgroup id % 8 being the XCD: when the counts allow
+// it, the 8 * G consecutive units of one XCD round are the G query heads of
+// eight (row, kv head) pairs, so a pair's K/V tiles are read through one L2.
+// The divisions go through FastDiv (operands below rows * heads, divisors
+// at most heads; the launchers check rows * heads^2 <= 2^32).
+__device__ __forceinline__ void jeff_unit_of(const JeffArgs &a, int rows, int u, int &row,
+                                             int &head) {
+  const int units = rows * a.heads, G = a.groups;
+  if (units % 8 == 0 && (rows * a.kv_heads) % 8 == 0) {
+    const int x = u % 8, i = u / 8;
+    const int ig = (int)a.gdiv.div((uint32_t)i);
+    const int kvu = x + 8 * ig;  // (row, kv head) unit of XCD x
+    row = (int)a.kvdiv.div((uint32_t)kvu);
+    head = (kvu - row * a.kv_heads) * G + (i - ig * G);
+  } else {
+    row = (int)a.hdiv.div((uint32_t)u);
+    head = u - row * a.heads;
+  }
+}
+
 // One workgroup = 4 wavefronts = one (row, head, 16-query tile). Wave w owns
 // features [w*DS, (w+1)*DS) of the head (DS = HDP/4 = 64) in both products:
 //   S^T_w (16 keys x 16 queries) = K[keys, slice w] Q[queries, slice w]^T  (16 MFMA 16x16x4)
@@ -1092,11 +1114,11 @@ __device__ __noinline__ void jeff_redo_wave(const JeffArgs *ap, const float *__r
 // flow is workgroup-uniform.
 //
 // Memory: K comes from the prep workspace in the split layout (each wave's
-// run of a tile is one contiguous 1 KB read), V columns straight from V,
-// into registers at the top of each tile's step: without a second tile of
-// registers the kernel fits 128 VGPRs, and the four workgroups per CU that
-// this allows hide the load latency better than a one-tile prefetch at three
-// (5% on C4). Q, the gate and the output move along tokens
+// run of a tile is one contiguous 1 KB read), V columns straight from V;
+// the next tile's K and V slices go into the wave's LDS with LDS-DMA loads
+// while the current tile is computed, so no second tile of registers is
+// held: the kernel fits 128 VGPRs, four workgroups per CU. Q, the gate and
+// the output move along tokens
 // 16 bytes at a time and are transposed in the wave's own LDS rows, so a
 // wave issues four vector memory instructions per tensor. The row's key span
 // and active-key bits come from the prep (scalar loads).
@@ -1104,7 +1126,7 @@ __device__ __noinline__ void jeff_redo_wave(const JeffArgs *ap, const float *__r
 // Workgroups are numbered from the last query tile down, so the longest
 // causal walks start first; within one query tile, the workgroups of one
 // (row, kv head) share an id residue mod 8 (one XCD, one L2) when the counts
-// allow it.
+// allow it (jeff_unit_of).
 template <int HDP>
 __global__ __launch_bounds__(256, 4) void jeff_split_f32_kernel(const JeffArgs a,
                                                                 const float *__restrict__ kp,
@@ -1137,24 +1159,14 @@ __global__ __launch_bounds__(256, 4) void jeff_split_f32_kernel(const JeffArgs a
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, grp = lane >> 4;
-  const int L = a.L, hd = a.hd, heads = a.heads, G = a.groups;
+  const int L = a.L, hd = a.hd;
 
-  // -------- work item
-  const int nq = (L + 15) / 16;
-  const int units = rows * heads;
-  const int p = blockIdx.x;
-  const int qt = nq - 1 - p / units;
-  int u = p % units, row, head;
-  if (units % 8 == 0 && (rows * a.kv_heads) % 8 == 0) {
-    const int x = u % 8, i = u / 8;
-    const int kvu = x + 8 * (i / G);  // (row, kv head) unit of XCD x
-    row = kvu / a.kv_heads;
-    head = (kvu % a.kv_heads) * G + i % G;
-  } else {
-    row = u / heads;
-    head = u % heads;
-  }
-  const int kvh = min(head / G, a.kv_heads - 1);
+  // -------- work item: query tiles from the last one down (blockIdx.y),
+  // the (row, head) unit in blockIdx.x.
+  const int qt = (int)gridDim.y - 1 - (int)blockIdx.y;
+  int row, head;
+  jeff_unit_of(a, rows, blockIdx.x, row, head);
+  const int kvh = min((int)a.gdiv.div((uint32_t)head), a.kv_heads - 1);
   const int q0 = qt * 16, q = q0 + col;
   const float *Q = static_cast<const float *>(a.q) + row * a.q_row + (size_t)head * hd * L;
   const float *Gt = static_cast<const float *>(a.gate) + row * a.q_row + (size_t)head * hd * L;
@@ -1605,26 +1617,15 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void jeff_fused_f32_kernel(const J
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, grp = lane >> 4;
-  const int L = a.L, heads = a.heads, G = a.groups;
+  const int L = a.L;
   const int L4 = 4 * L;
 
   // -------- work item: query tiles from the last one down; the heads of a
   // (row, kv head) on one XCD.
-  const int nq = (L + 15) / 16;
-  const int units = rows * heads;
-  const int p = blockIdx.x;
-  const int qt = nq - 1 - p / units;
-  int u = p % units, row, head;
-  if (units % 8 == 0 && (rows * a.kv_heads) % 8 == 0) {
-    const int x = u % 8, i = u / 8;
-    const int kvu = x + 8 * (i / G);
-    row = kvu / a.kv_heads;
-    head = (kvu % a.kv_heads) * G + i % G;
-  } else {
-    row = u / heads;
-    head = u % heads;
-  }
-  const int kvh = min(head / G, a.kv_heads - 1);
+  const int qt = (int)gridDim.y - 1 - (int)blockIdx.y;
+  int row, head;
+  jeff_unit_of(a, rows, blockIdx.x, row, head);
+  const int kvh = min((int)a.gdiv.div((uint32_t)head), a.kv_heads - 1);
   const int q0 = qt * 16, q = q0 + col;
   const uint32_t bytes = (uint32_t)((size_t)HDP * L * 4);
   const __amdgpu_buffer_rsrc_t rq = buffer_rsrc(
@@ -2437,9 +2438,11 @@ static hipError_t launch_jeff_f32_hd(const JeffArgs &a, int rows, float *kp, hip
     // 1 KB loads instead of normalizing it again for every query tile.
     const int rb = a.cos_t == nullptr ? 0 : (a.rot_half % 16 == 0 ? a.rot_half / 16 : -1);
     const long items = (long)nq * rows * a.heads;
-    if (vec && a.hd == 256 && rb >= 0 && rb <= 2 && items <= 2L * (a.cus > 0 ? a.cus : 1)) {
+    const bool div_ok = (uint64_t)rows * a.heads * a.heads <= ((uint64_t)1 << 32);
+    if (vec && div_ok && a.hd == 256 && rb >= 0 && rb <= 2 &&
+        items <= 2L * (a.cus > 0 ? a.cus : 1)) {
       constexpr int NW = kJeffFusedWaves;
-      const dim3 fgrid((unsigned)items);
+      const dim3 fgrid((unsigned)(rows * a.heads), (unsigned)nq);
       if (rb == 0)
         hipExtLaunchKernelGGL((jeff_fused_f32_kernel<NW, 0>), fgrid, dim3(NW * 64), 0, stream,
                               ev.start, ev.stop, 0, a, rows);
@@ -2453,7 +2456,7 @@ static hipError_t launch_jeff_f32_hd(const JeffArgs &a, int rows, float *kp, hip
     }
     // Buffer offsets of the split kernel: one head's (hd, L) block and one
     // kv head's padded K blocks within 2 GiB (checked above, L + 15 < 2^21).
-    if (vec) {
+    if (vec && div_ok) {
       int *spans = reinterpret_cast<int *>(reinterpret_cast<char *>(kp) +
                                            jeff_kp_main_bytes(a, rows, HDP, false));
       uint32_t *kbits = reinterpret_cast<uint32_t *>(spans + 2 * rows);
@@ -2462,7 +2465,7 @@ static hipError_t launch_jeff_f32_hd(const JeffArgs &a, int rows, float *kp, hip
                             0, a, kp, spans, kbits);
       hipError_t e = hipGetLastError();
       if (e != hipSuccess) return e;
-      const dim3 sgrid(nq * rows * a.heads);
+      const dim3 sgrid(rows * a.heads, nq);
       hipExtLaunchKernelGGL((jeff_split_f32_kernel<HDP>), sgrid, dim3(256), 0, stream, nullptr,
                             ev.stop, 0, a, kp, spans, kbits, rows);
       return hipGetLastError();

@@ -554,6 +554,9 @@ int jeff_run(tfd_ctx *c, const char *op, bool bf16, size_t rows, size_t length, 
   a.hd = (int)head_dim;
   a.rot_half = (int)(rotary_dim / 2);
   a.groups = (int)(heads / kv_heads);
+  a.gdiv = tfd::FastDiv::make((uint32_t)a.groups);
+  a.kvdiv = tfd::FastDiv::make((uint32_t)kv_heads);
+  a.hdiv = tfd::FastDiv::make((uint32_t)heads);
   a.heads_per_group = (a.groups % 4 == 0) ? 4 : (a.groups % 2 == 0) ? 2 : 1;
   a.trim = (flags & TFD_TRIM_LEADING) ? 1 : 0;
   a.cus = c->cus;

@@ -70,6 +70,26 @@ struct LayaArgs {
   float c1;              // (1/sqrt(hd)) * log2(e)
 };
 
+// Division by a divisor fixed for a launch: floor(n / d) = umulhi(n, m) with
+// m = ceil(2^32 / d), exact whenever n * d <= 2^32 (m * d = 2^32 + e with
+// e < d, so n * m / 2^32 = n / d + n * e / (d * 2^32) stays below the next
+// integer; Granlund and Montgomery, "Division by invariant integers using
+// multiplication", 1994). m = 0 stands for d = 1. A run-time divisor
+// otherwise costs a ~25-instruction sequence, which the kernels' prologues
+// run on the scalar unit that a CU's waves share.
+struct FastDiv {
+  uint32_t d = 1, m = 0;
+  static FastDiv make(uint32_t dv) {
+    FastDiv f;
+    f.d = dv;
+    f.m = dv <= 1 ? 0u : (uint32_t)((((uint64_t)1 << 32) + dv - 1) / dv);
+    return f;
+  }
+  __device__ __forceinline__ uint32_t div(uint32_t n) const {
+    return m == 0 ? n : __umulhi(n, m);
+  }
+};
+
 struct JeffArgs {
   const void *q, *k, *v, *gate;  // f32 or bf16 per kernel
   const float *q_norm, *k_norm;  // (hd)
@@ -86,6 +106,7 @@ struct JeffArgs {
                                  // the copies of an expanded K/V, see kv_head)
   size_t kv_head;                // elements between consecutive kv heads of K/V: L*hd, or
                                  // L*hd*G when each of G expanded copies is skipped
+  FastDiv gdiv, kvdiv, hdiv;     // by groups, kv_heads, heads (exact for n <= rows * heads)
 };
 
 // Timing of an op's attention kernel(s): `start` is recorded when the first
