@@ -46,10 +46,10 @@ namespace tfd {
 // work of a CU changes, never a result. `scratch` holds B*ng + 96 ints of
 // LDS. Returns {row, item head*nqb + qb, kt_begin, kt_end}, uniform.
 __device__ int4 laya_plan_item(const uint8_t *__restrict__ any, int L, int nkt, int B, int H,
-                               int p, int *scratch) {
+                               int p, int *scratch, FastDiv ngdiv, FastDiv mdiv) {
   const int lane = threadIdx.x & 63;
-  const int ng = (L + 63) / 64, G = B * ng;
-  const int M = H * ng / 8, S = B * M / 32;
+  const int ng = (L + 63) >> 6, G = B * ng;
+  const int M = (H * ng) >> 3, S = (B * M) >> 5;  // both exact in this layout
   int *s_span = scratch, *s_cost = scratch + G, *s_rows = s_cost + 32, *s_load = s_rows + 32;
   auto wave_sync = [] {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -76,7 +76,7 @@ __device__ int4 laya_plan_item(const uint8_t *__restrict__ any, int L, int nkt, 
       }
     }
     s_span[g] = lo < 0 ? 0 : lo | ((hi + 1) << 16);
-    if (lo >= 0) atomicMax(&s_cost[g / ng], hi + 1 - lo);
+    if (lo >= 0) atomicMax(&s_cost[ngdiv.div((uint32_t)g)], hi + 1 - lo);
   }
   wave_sync();
   if (lane < B) {  // rows by cost, longest first (ties: lower row first)
@@ -89,20 +89,21 @@ __device__ int4 laya_plan_item(const uint8_t *__restrict__ any, int L, int nkt, 
   auto snake = [](int t, int c) { return 32 * t + ((t & 1) ? 31 - c : c); };
   if (lane < 32) {  // CU `lane`'s load after the snake rounds
     int load = 0;
-    for (int t = 0; t < S - 1; ++t) load += s_cost[s_rows[snake(t, lane) / M]];
+    for (int t = 0; t < S - 1; ++t) load += s_cost[s_rows[mdiv.div((uint32_t)snake(t, lane))]];
     s_load[lane] = load;
   }
   wave_sync();
-  const int x = p % 8, c = (p / 8) % 32, t = p / 256;
+  const int x = p & 7, c = (p >> 3) & 31, t = p >> 8;
   int pos = snake(t, c);
   if (t == S - 1) {  // last round: this CU's place by load, least loaded first
     const int lc = s_load[c];
     const bool before = lane < 32 && (s_load[lane] < lc || (s_load[lane] == lc && lane < c));
     pos = 32 * t + __builtin_popcountll(__ballot(before));
   }
-  const int b = s_rows[pos / M];
-  const int r = x * M + pos % M;
-  const int sp = s_span[b * ng + r % ng];
+  const int pm = (int)mdiv.div((uint32_t)pos);
+  const int b = s_rows[pm];
+  const int r = x * M + (pos - pm * M);
+  const int sp = s_span[b * ng + (r - (int)ngdiv.div((uint32_t)r) * ng)];
   return make_int4(b, r, sp & 0xffff, sp >> 16);
 }
 
@@ -501,33 +502,39 @@ __global__ __launch_bounds__(64 * QW * TEAMS, TEAMS == 1 ? laya_groups_per_cu(HD
   int b = blockIdx.z, head = blockIdx.y, qb = blockIdx.x;
   int kt_begin = 0, kt_end = 0;
   const int nqb = gridDim.x, H = gridDim.y, B = gridDim.z;
-  const bool xcd = TEAMS == 1 && QW == 4 && laya_xcd_layout(nqb, H, B, laya_groups_per_cu(HDP), a.cus);
-  const bool planned = a.any != nullptr && xcd && nqb * B <= kLayaPlanMax;
+  // The launcher decides the layout (laya_xcd_layout, laya_planned) and
+  // supplies the divisions by nqb and by M.
+  const bool xcd = TEAMS == 1 && QW == 4 && a.layout >= 1;
+  const bool planned = TEAMS == 1 && QW == 4 && a.layout == 2;
   {
     const int p = blockIdx.x + nqb * (blockIdx.y + H * blockIdx.z);
     if (planned) {
       __shared__ int4 s_item;
       if (wave == 0) {
-        const int4 e = laya_plan_item(a.any, L, nkt, B, H, p, reinterpret_cast<int *>(smem));
+        const int4 e = laya_plan_item(a.any, L, nkt, B, H, p, reinterpret_cast<int *>(smem),
+                                      a.ngdiv, a.mdiv);
         if (lane == 0) s_item = e;
       }
       __syncthreads();
       const int4 e = s_item;
       b = __builtin_amdgcn_readfirstlane(e.x);
-      head = __builtin_amdgcn_readfirstlane(e.y) / nqb;
-      qb = __builtin_amdgcn_readfirstlane(e.y) % nqb;
+      const int ey = __builtin_amdgcn_readfirstlane(e.y);
+      head = (int)a.ngdiv.div((uint32_t)ey);
+      qb = ey - head * nqb;
       kt_begin = e.z;
       kt_end = e.w;
     } else if (xcd) {
-      const int M = H * nqb / 8;  // items of a batch row per XCD
-      const int x = p % 8, j = p / 8;
-      const int t = j / 32, c = j % 32;  // round, CU of the XCD
-      const int row = (c + 3 * t) % B;
-      const int k = t * (32 / B) + c / B;  // item of that row on this XCD
+      // B divides 32 in this layout (a power of two).
+      const int M = (H * nqb) >> 3;  // items of a batch row per XCD
+      const int lb = __builtin_ctz((unsigned)B);
+      const int x = p & 7, j = p >> 3;
+      const int t = j >> 5, c = j & 31;  // round, CU of the XCD
+      const int row = (c + 3 * t) & (B - 1);
+      const int k = t * (32 >> lb) + (c >> lb);  // item of that row on this XCD
       const int r = x * M + k;
       b = row;
-      head = r / nqb;
-      qb = r % nqb;
+      head = (int)a.ngdiv.div((uint32_t)r);
+      qb = r - head * nqb;
     }
   }
   const int qg0 = qb * GQ;
@@ -1125,7 +1132,13 @@ static hipError_t launch_laya_hd(const LayaArgs &a, int heads, int batch, int mo
   const dim3 grid(ng, heads, batch);
   if (laya_teams_grid(a.L, heads, batch, a.nkt, a.cus))
     return launch_laya_teams<HDP, VEC, ROPE, laya_teams(HDP), 4>(a, grid, mode, stream, ev);
-  return launch_laya_teams<HDP, VEC, ROPE, 1, 4>(a, grid, mode, stream, ev);
+  LayaArgs b = a;
+  b.layout = 0;
+  if (laya_xcd_layout((int)ng, heads, batch, laya_groups_per_cu(HDP), a.cus))
+    b.layout = (a.any != nullptr && (int)ng * batch <= kLayaPlanMax) ? 2 : 1;
+  b.ngdiv = FastDiv::make(ng);
+  b.mdiv = FastDiv::make((uint32_t)(heads * (int)ng / 8 > 0 ? heads * (int)ng / 8 : 1));
+  return launch_laya_teams<HDP, VEC, ROPE, 1, 4>(b, grid, mode, stream, ev);
 }
 
 template <int HDP>

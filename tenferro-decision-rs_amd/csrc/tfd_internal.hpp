@@ -51,25 +51,6 @@ enum LayaMaskMode : int {
   kMaskRaw = 2,     // the (L, L, B) keep bytes themselves, packed by the attention kernel
 };
 
-struct LayaArgs {
-  const float *qkv;      // (3d, L, B)
-  const uint32_t *bits;  // kMaskBits: word (b*nkt + kt)*L + q, bit j = key 32*kt + j kept;
-                         // kMaskStruct (optional): word b*nkt + kt, bit j = key 32*kt + j valid
-  const uint8_t *any;    // byte (b*ceil(L/64) + q/64)*laya_map_row(nkt) + kt: tile kt kept by
-                         // any query of that 64-query group (kMaskBits; optional in
-                         // kMaskStruct, where it only feeds the placement plan)
-  const uint8_t *valid;  // kMaskStruct: (L, B)
-  const uint8_t *qneed;  // kMaskStruct, or null: (L, B), a 64-query group with no
-                         // non-zero entry is skipped (its output left unwritten)
-  const uint8_t *keep;   // kMaskRaw: byte b*L*L + key*L + query, kept when non-zero
-  const float *cos_t;    // (L, half) or nullptr (no RoPE)
-  const float *sin_t;
-  float *out;            // (d, L, B)
-  int d, hd, half, L, nkt, window;
-  int cus;               // compute units of the device (grid shapes)
-  float c1;              // (1/sqrt(hd)) * log2(e)
-};
-
 // Division by a divisor fixed for a launch: floor(n / d) = umulhi(n, m) with
 // m = ceil(2^32 / d), exact whenever n * d <= 2^32 (m * d = 2^32 + e with
 // e < d, so n * m / 2^32 = n / d + n * e / (d * 2^32) stays below the next
@@ -88,6 +69,31 @@ struct FastDiv {
   __device__ __forceinline__ uint32_t div(uint32_t n) const {
     return m == 0 ? n : __umulhi(n, m);
   }
+};
+
+struct LayaArgs {
+  const float *qkv;      // (3d, L, B)
+  const uint32_t *bits;  // kMaskBits: word (b*nkt + kt)*L + q, bit j = key 32*kt + j kept;
+                         // kMaskStruct (optional): word b*nkt + kt, bit j = key 32*kt + j valid
+  const uint8_t *any;    // byte (b*ceil(L/64) + q/64)*laya_map_row(nkt) + kt: tile kt kept by
+                         // any query of that 64-query group (kMaskBits; optional in
+                         // kMaskStruct, where it only feeds the placement plan)
+  const uint8_t *valid;  // kMaskStruct: (L, B)
+  const uint8_t *qneed;  // kMaskStruct, or null: (L, B), a 64-query group with no
+                         // non-zero entry is skipped (its output left unwritten)
+  const uint8_t *keep;   // kMaskRaw: byte b*L*L + key*L + query, kept when non-zero
+  const float *cos_t;    // (L, half) or nullptr (no RoPE)
+  const float *sin_t;
+  float *out;            // (d, L, B)
+  int d, hd, half, L, nkt, window;
+  int cus;               // compute units of the device (grid shapes)
+  float c1;              // (1/sqrt(hd)) * log2(e)
+  // Set by the launcher for the one-round 64-query grid (TEAMS == 1):
+  // layout 0 = grid order, 1 = laya_xcd_layout, 2 = that layout with the
+  // placement plan; division by ceil(L/64) and by the plan's items per
+  // batch row and XCD (heads * ceil(L/64) / 8).
+  int layout;
+  FastDiv ngdiv, mdiv;
 };
 
 struct JeffArgs {
