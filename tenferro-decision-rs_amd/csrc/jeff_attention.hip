@@ -1161,6 +1161,12 @@ __global__ __launch_bounds__(256, 4) void jeff_split_f32_kernel(const JeffArgs a
   const int col = lane & 15, grp = lane >> 4;
   const int L = a.L, hd = a.hd;
 
+  // Issue priority (s_setprio, within this kernel's waves on a SIMD): the
+  // prologue and the epilogue above the walks of the CU's other workgroups,
+  // so that a workgroup reaches its walk, and frees its slot, sooner (f32
+  // MFMAs and vector instructions of a SIMD never run at the same time).
+  __builtin_amdgcn_s_setprio(2);
+
   // -------- work item: query tiles from the last one down (blockIdx.y),
   // the (row, head) unit in blockIdx.x.
   const int qt = (int)gridDim.y - 1 - (int)blockIdx.y;
@@ -1519,8 +1525,10 @@ __global__ __launch_bounds__(256, 4) void jeff_split_f32_kernel(const JeffArgs a
     }
     if (more) w = keep_word(kt - 1, bnext);
   };
+  __builtin_amdgcn_s_setprio(0);
   step(kt_hi, std::true_type{});
   for (int kt = kt_hi - 1; kt >= kt_begin; --kt) step(kt, std::false_type{});
+  __builtin_amdgcn_s_setprio(3);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the gate slice, and no LDS-DMA left in flight
 
   // -------- careful redo (rare): the scores (shared) or this wave's O went
