@@ -596,7 +596,7 @@ __device__ __forceinline__ void jeff_store(const JeffArgs &a, const float *Gt, f
           const float x = ow[(4 * gq + t) * QP + d] * fast_sigmoid(g[u][t]);
           o[t] = qa + t < start ? 0.0f : x;
         }
-        if (qa < L && d < hd) buffer_store4(o, ro, (int)(((size_t)d * L + 4 * gq) * 4), q0 * 4);
+        if (qa < L && d < hd) buffer_store4_nt(o, ro, (int)(((size_t)d * L + 4 * gq) * 4), q0 * 4);
       }
     }
   } else {
@@ -620,7 +620,8 @@ __device__ __forceinline__ void jeff_store(const JeffArgs &a, const float *Gt, f
         const int e = e0 + lane + 64 * u, d = e >> 4, t = e & 15;
         const int qq = q0 + t;
         if (qq < L && d < hd)
-          OUT[qq + (size_t)L * d] = qq < start ? 0.0f : ow[t * QP + d] * fast_sigmoid(g[u]);
+          __builtin_nontemporal_store(qq < start ? 0.0f : ow[t * QP + d] * fast_sigmoid(g[u]),
+                                      &OUT[qq + (size_t)L * d]);
       }
     }
   }
@@ -1245,7 +1246,7 @@ __global__ __launch_bounds__(256, 4) void jeff_split_f32_kernel(const JeffArgs a
     f32x4 r;
 #pragma unroll
     for (int i = 0; i < 4; ++i) r[i] = qa + i < start ? 0.0f : o[i] * fast_sigmoid(gv[t][i]);
-    if (qa < L && d < hd) buffer_store4(r, ro, otask + t * 16 * L * 4, q0 * 4);
+    if (qa < L && d < hd) buffer_store4_nt(r, ro, otask + t * 16 * L * 4, q0 * 4);
   };
   if (kt_begin >= kt_end) {
     // No key at or before these queries: o = 0 (lib.rs:739-743), and
@@ -1258,7 +1259,7 @@ __global__ __launch_bounds__(256, 4) void jeff_split_f32_kernel(const JeffArgs a
       f32x4 r;
 #pragma unroll
       for (int i = 0; i < 4; ++i) r[i] = (qa + i >= start && gv[t][i] != gv[t][i]) ? gv[t][i] : 0.0f;
-      if (qa < L && d < hd) buffer_store4(r, ro, otask + t * 16 * L * 4, q0 * 4);
+      if (qa < L && d < hd) buffer_store4_nt(r, ro, otask + t * 16 * L * 4, q0 * 4);
     }
     return;
   }
@@ -1718,7 +1719,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void jeff_fused_f32_kernel(const J
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float x = q < start ? 0.0f : o[j][r] * fast_sigmoid(g[4 * j + r]);
-          buffer_store1(x, ro, ofs_t, q0 * 4 + (16 * (BPW * wave + j) + r) * L4);
+          buffer_store1_nt(x, ro, ofs_t, q0 * 4 + (16 * (BPW * wave + j) + r) * L4);
         }
     }
   };
@@ -2365,7 +2366,8 @@ __device__ __forceinline__ void jeff_bf16_unit(const JeffArgs &a, const uint16_t
         float o = O[j][r] * inv;
         const uint32_t f = (special[j] >> (8 * r)) & 7u;
         if (f) o = ((f & 1u) || f == 6u) ? __builtin_nanf("") : (f == 2u ? INFINITY : -INFINITY);
-        if (d < hd) OUT[q + (size_t)L * d] = dropped ? 0.0f : o * fast_sigmoid(gv[j][r]);
+        if (d < hd)
+          __builtin_nontemporal_store(dropped ? 0.0f : o * fast_sigmoid(gv[j][r]), &OUT[q + (size_t)L * d]);
       }
   }
 }

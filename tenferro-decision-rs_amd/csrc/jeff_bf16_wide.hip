@@ -564,7 +564,9 @@ __global__ __launch_bounds__(512, 1) void jeff_bf16_wide_kernel(const JeffArgs a
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int f = 32 * j + 8 * (r >> 2) + 4 * half + (r & 3);
-      Oh[(size_t)f * L + qv] = dropped ? 0.0f : O[j][r] * inv * fast_sigmoid(gv[r]);
+      // Non-temporal: the output is not read again in the kernel.
+      __builtin_nontemporal_store(dropped ? 0.0f : O[j][r] * inv * fast_sigmoid(gv[r]),
+                                  &Oh[(size_t)f * L + qv]);
     }
   }
 }

@@ -1022,10 +1022,14 @@ __global__ __launch_bounds__(64 * QW * TEAMS, TEAMS == 1 ? laya_groups_per_cu(HD
   if (qin) {
     float *orow = a.out + ((size_t)b * L + q) * a.d + (size_t)head * hd;
     if constexpr (VEC) {
-      // Block j holds dims 16j + 4*grp + 0..3: one 16-byte store each.
+      // Block j holds dims 16j + 4*grp + 0..3: one 16-byte store each,
+      // non-temporal: nothing in this kernel reads the output again, and
+      // dirty L2 lines would be written back at the kernel's end (C2 kernel
+      // 44.1 -> 42.7 us).
 #pragma unroll
       for (int j = 0; j < NB; ++j)
-        *reinterpret_cast<f32x4 *>(orow + 16 * j + 4 * grp) = O[j] * inv;
+        __builtin_nontemporal_store(O[j] * inv,
+                                    reinterpret_cast<f32x4 *>(orow + 16 * j + 4 * grp));
     } else {
 #pragma unroll
       for (int j = 0; j < NB; ++j)

@@ -160,6 +160,18 @@ __device__ __forceinline__ void buffer_store4(f32x4 v, __amdgpu_buffer_rsrc_t r,
                                               int soff) {
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, v), r, voff, soff, 0);
 }
+// Non-temporal stores (cache policy nt) for outputs nothing in the kernel
+// reads again: they do not leave dirty L2 lines for the end-of-kernel
+// write-back.
+constexpr int kCacheNT = 2;
+__device__ __forceinline__ void buffer_store1_nt(float v, __amdgpu_buffer_rsrc_t r, int voff,
+                                                 int soff) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, voff, soff, kCacheNT);
+}
+__device__ __forceinline__ void buffer_store4_nt(f32x4 v, __amdgpu_buffer_rsrc_t r, int voff,
+                                                 int soff) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, v), r, voff, soff, kCacheNT);
+}
 
 __device__ __forceinline__ float wave_max_f(float v) {
 #pragma unroll
