@@ -97,6 +97,42 @@ def time_gpu(fn, steps, warmup, ctx):
     return start.elapsed_time(end) / steps, total / max(1, launches)
 
 
+def host_call_line(w, ctx, flops, calls=10, warmup=3):
+    """The C2 drop-in called the way the reference's op is: host buffers in,
+    host buffer out (TFD_HOST_PTRS: upload, kernels, download, then the call
+    returns), timed on the host clock. Pageable numpy arrays, as the
+    reference's Vec<f32> tensors are, and pinned host tensors. PCIe-inclusive,
+    so never the headline `value`."""
+    import time
+
+    import numpy as np
+    import torch
+    import tenferro_ext as te
+
+    shape = (3 * w.hidden, w.length, w.batch)
+    n_out = w.hidden * w.length * w.batch
+    h2d = 4 * w.qkv.size + w.keep.size
+    d2h = 4 * n_out
+    res = {"h2d_bytes": int(h2d), "d2h_bytes": int(d2h),
+           "note": "wall time of synchronous host-pointer calls (upload, attention, download)"}
+    pinned = (torch.from_numpy(w.qkv).pin_memory(), torch.from_numpy(w.keep).pin_memory(),
+              torch.empty(n_out, dtype=torch.float32).pin_memory())
+    variants = {"pageable": (w.qkv, w.keep, np.empty(n_out, np.float32)), "pinned": pinned}
+    for name, (q, k, o) in variants.items():
+        for _ in range(warmup):
+            te.laya_attention_block(q, k, w.hidden, w.heads, w.rope_base, qkv_shape=shape,
+                                    ctx=ctx, out=o)
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            te.laya_attention_block(q, k, w.hidden, w.heads, w.rope_base, qkv_shape=shape,
+                                    ctx=ctx, out=o)
+        ms = (time.perf_counter() - t0) * 1e3 / calls
+        res[name] = {"ms_per_call": round(ms, 4), "tflops": round(flops / (ms * 1e-3) / 1e12, 3),
+                     "prefill_tokens_per_s": round(w.valid_tokens() / (ms * 1e-3), 1),
+                     "host_device_gb_per_s": round((h2d + d2h) / (ms * 1e-3) / 1e9, 2)}
+    return res
+
+
 def laya_bytes(w):
     """Algorithmic bytes of one attention-kernel launch: the (3d, L, B) qkv
     read once and the (d, L, B) output written once (f32), plus the packed
@@ -301,6 +337,7 @@ def run(args):
                                  "tflops": round(flops / (ms_s * 1e-3) / 1e12, 3),
                                  "kernel_tflops": round(flops / (k_s * 1e-3) / 1e12, 3)}
         del valid
+        also["C2_host_pointers"] = host_call_line(w, ctx, flops)
 
         w3 = laya_config(3)
         f3 = 4 * w3.head_dim * w3.kept_pairs() * w3.heads
@@ -613,6 +650,11 @@ def run_only(args):
         ctx.close()
         return {"only": name, "ms_per_step": round(ms, 5), "attention_kernel_ms": round(kern, 5),
                 "tflops": round((att + gemm) / (ms * 1e-3) / 1e12, 3)}
+    if args.only == "c2host":
+        w = laya_config(2)
+        res = host_call_line(w, ctx, 4 * w.head_dim * w.kept_pairs() * w.heads)
+        ctx.close()
+        return {"only": "C2_host_pointers", **res}
     if args.only == "micro":
         # The reference micro-benchmark's largest shape (L 512, B 1, d 1024,
         # 16 heads, global keep k % 13 != 7): the small-grid Laya path.
@@ -755,7 +797,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="only the C2 headline")
-    ap.add_argument("--only", choices=["c2", "c3", "c4", "c5", "c2s", "c3s", "c2l", "c4l", "c4row", "micro", "model", "copy"], default=None,
+    ap.add_argument("--only", choices=["c2", "c3", "c4", "c5", "c2s", "c3s", "c2l", "c4l", "c4row", "c2host", "micro", "model",
+                             "copy"], default=None,
                     help="profiling aid: run one configuration's op (steps + warmup calls), "
                          "print its timing line and skip everything else")
     args = ap.parse_args()
