@@ -184,7 +184,16 @@ __global__ __launch_bounds__(256) void jeff_k_prep_kernel(const JeffArgs a, OutT
   const int tid = threadIdx.x, lane = tid & 63;
   const int row = blockIdx.z, kvh = blockIdx.y;
   const int L = a.L, hd = a.hd, rh = a.rot_half;
-  const int k0 = blockIdx.x * kKeyTile;
+  // Key blocks 2m and 2m + 1 go to workgroups i and i + 8 of each 16, which
+  // the dispatcher sends to one XCD: in bf16 the two blocks are the two
+  // halves of every 128-byte run of a feature's keys, so the second half's
+  // loads find the run in that XCD's L2 (C5 prep 16.1 -> 15.1 us).
+  int kb = (int)blockIdx.x;
+  if ((gridDim.x & 15) == 0) {
+    const int g = kb >> 4, r = kb & 15;
+    kb = 16 * g + 2 * (r & 7) + (r >> 3);
+  }
+  const int k0 = kb * kKeyTile;
   const bool bf = sizeof(OutT) == 2;
   const size_t kv_off = row * a.kv_row + (size_t)kvh * a.kv_head;
   const int kk = tid & 31, part = tid >> 5;
@@ -195,7 +204,7 @@ __global__ __launch_bounds__(256) void jeff_k_prep_kernel(const JeffArgs a, OutT
   if (kbits != nullptr && kvh == 0 && tid < 64) {
     const float mv = a.mask[(size_t)row * L + min(k0 + lane, L - 1)];
     const uint64_t bm = __ballot(lane < kKeyTile && k0 + lane < L && mv != 0.0f);
-    if (lane == 0) kbits[(size_t)row * ((L + 31) / 32) + blockIdx.x] = (uint32_t)bm;
+    if (lane == 0) kbits[(size_t)row * ((L + 31) / 32) + kb] = (uint32_t)bm;
   }
   float xs[DP], wn[DP], c[RT], sn[RT];
 #pragma unroll
