@@ -671,6 +671,26 @@ def test_jeff_bf16_hd256_rows_match_oracle(gpu_ctx, length, heads, kv, rot):
         assert_close(got, want, BF16_TOL)
 
 
+@pytest.mark.parametrize("length", [512, 1024])
+def test_jeff_bf16_hd256_paired_prep_blocks(gpu_ctx, length):
+    """Lengths whose K prep grid is a multiple of 16 blocks, where the prep
+    sends the two 32-key halves of each 128-byte run to one XCD (a block
+    permutation): left padding, an interior hole and trimming, against the
+    oracle, and bitwise equal to the same call again."""
+    rows, heads, kv, hd, rot = 2, 8, 2, 256, 64
+    bits, vals, qn, kn, mask = bf16_case(900 + length, rows, length, heads, kv, hd, True)
+    mask[length + 37] = 0.0  # row 1: a hole inside a prep block
+    for trim in (False, True):
+        want = oracle.jeff_rows(*vals, qn, kn, mask, rows, length, heads, kv, hd, rot, 1e7, 1e-6,
+                                trim_leading=trim)
+        got = te.jeff_full_attention_rows(*bits, qn, kn, mask, rows, length, heads, kv, hd, rot,
+                                          1e7, 1e-6, trim_leading=trim, bf16=True, ctx=gpu_ctx)
+        assert_close(got, want, BF16_TOL)
+        again = te.jeff_full_attention_rows(*bits, qn, kn, mask, rows, length, heads, kv, hd, rot,
+                                            1e7, 1e-6, trim_leading=trim, bf16=True, ctx=gpu_ctx)
+        assert np.array_equal(np.asarray(got).view(np.uint32), np.asarray(again).view(np.uint32))
+
+
 @pytest.mark.parametrize("length", [72, 200])
 def test_jeff_bf16_hd256_empty_and_sparse_rows(gpu_ctx, length):
     """Head dim 256, 32x32x16 kernel: a row with no active key (its walk has
