@@ -691,6 +691,30 @@ def test_jeff_bf16_hd256_paired_prep_blocks(gpu_ctx, length):
         assert np.array_equal(np.asarray(got).view(np.uint32), np.asarray(again).view(np.uint32))
 
 
+def test_jeff_f32_general_prep_paired_blocks(gpu_ctx):
+    """The general f32 path (hd 128: K prep + jeff_attention_f32_kernel) at a
+    length whose prep grid takes the paired block mapping, with left padding,
+    a hole and trimming."""
+    rows, length, heads, kv, hd, rot = 2, 512, 4, 2, 128, 32
+    rng = Lcg(512 + hd)
+    W, KW = heads * hd, kv * hd
+    q = rng.normal(rows * length * W).astype(np.float32)
+    g = rng.normal(rows * length * W).astype(np.float32)
+    k = rng.normal(rows * length * KW).astype(np.float32)
+    v = rng.normal(rows * length * KW).astype(np.float32)
+    qn = (rng.normal(hd) * 0.1).astype(np.float32)
+    kn = (rng.normal(hd) * 0.1).astype(np.float32)
+    mask = np.ones(rows * length, np.float32)
+    mask[:100] = 0.0                   # row 0 left-padded
+    mask[length + 333] = 0.0           # row 1 hole
+    for trim in (False, True):
+        want = oracle.jeff_rows(q, k, v, g, qn, kn, mask, rows, length, heads, kv, hd, rot,
+                                1e7, 1e-6, trim_leading=trim)
+        got = te.jeff_full_attention_rows(q, k, v, g, qn, kn, mask, rows, length, heads, kv, hd,
+                                          rot, 1e7, 1e-6, trim_leading=trim, ctx=gpu_ctx)
+        assert_close(got, want, F32_TOL)
+
+
 @pytest.mark.parametrize("length", [72, 200])
 def test_jeff_bf16_hd256_empty_and_sparse_rows(gpu_ctx, length):
     """Head dim 256, 32x32x16 kernel: a row with no active key (its walk has
