@@ -17,7 +17,13 @@ Two independent restatements live here:
   ``full_attention_host`` (crates/jeff-infer/src/model.rs:404-473), used to
   pin the C restatement on small inputs.
 
-Parity status (what pins each part) is tabulated in DESIGN.md.
+What pins each part: the reference's known-answer tests and golden vectors
+(tests/test_golden.py, tests/test_oracle.py; the model forward of
+``laya_model`` against the laya-tiny fixture's outputs and an assembly of
+library modules, tests/test_laya_model.py), float64 brute force at the
+reference tests' shapes, closed forms of the Jeff norm convention
+(tests/test_jeff_closed_forms.py) and planted mistakes that each of these
+checks must catch. No function here is left without such a check.
 """
 from __future__ import annotations
 
