@@ -567,10 +567,12 @@ __device__ __forceinline__ void jeff_q_prep(const JeffArgs &a, const float *Q, i
 // feature-major: the wave writes its 16 x HDP block through its LDS rows ow
 // (16 x (HDP + 4) floats) so that gate loads and output stores run along
 // tokens, 16 bytes at a time, when VEC. Dropped queries (q < start) get 0.
+// Only features d_lo <= d < d_hi are stored (a workgroup that owns part of
+// the head's features).
 template <int HDP, bool VEC>
 __device__ __forceinline__ void jeff_store(const JeffArgs &a, const float *Gt, float *OUT, int q0,
                                            int start, float *ow, const f32x4 (&O)[HDP / 16],
-                                           float inv) {
+                                           float inv, int d_lo = 0, int d_hi = 1 << 30) {
   constexpr int NB = HDP / 16, QP = HDP + 4;
   const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
   const int L = a.L, hd = a.hd;
@@ -605,7 +607,8 @@ __device__ __forceinline__ void jeff_store(const JeffArgs &a, const float *Gt, f
           const float x = ow[(4 * gq + t) * QP + d] * fast_sigmoid(g[u][t]);
           o[t] = qa + t < start ? 0.0f : x;
         }
-        if (qa < L && d < hd) buffer_store4_nt(o, ro, (int)(((size_t)d * L + 4 * gq) * 4), q0 * 4);
+        if (qa < L && d < hd && d >= d_lo && d < d_hi)
+          buffer_store4_nt(o, ro, (int)(((size_t)d * L + 4 * gq) * 4), q0 * 4);
       }
     }
   } else {
@@ -628,7 +631,7 @@ __device__ __forceinline__ void jeff_store(const JeffArgs &a, const float *Gt, f
       for (int u = 0; u < 8; ++u) {
         const int e = e0 + lane + 64 * u, d = e >> 4, t = e & 15;
         const int qq = q0 + t;
-        if (qq < L && d < hd)
+        if (qq < L && d < hd && d >= d_lo && d < d_hi)
           __builtin_nontemporal_store(qq < start ? 0.0f : ow[t * QP + d] * fast_sigmoid(g[u]),
                                       &OUT[qq + (size_t)L * d]);
       }
@@ -714,7 +717,8 @@ struct JeffStage {
 template <int HDP, bool VEC, int TAG = 0>
 __device__ __noinline__ void jeff_redo_wave(const JeffArgs *ap, const float *__restrict__ kp,
                                             int row, int head, int q0, int kt_begin, int kt_end,
-                                            int start, float *ws);
+                                            int start, float *ws, int d_lo = 0,
+                                            int d_hi = 1 << 30);
 
 // The calling kernel's JeffArgs (its first parameter, at offset 0 of the
 // kernel argument segment), for the out-of-line redo: passing the struct by
@@ -950,7 +954,7 @@ __global__ __launch_bounds__(kJeffF32Waves * 64, 1) void jeff_attention_f32_kern
 template <int HDP, bool VEC, int TAG>
 __device__ __noinline__ void jeff_redo_wave(const JeffArgs *ap, const float *__restrict__ kp,
                                             int row, int head, int q0, int kt_begin, int kt_end,
-                                            int start, float *ws) {
+                                            int start, float *ws, int d_lo, int d_hi) {
   const JeffArgs &a = *ap;
   constexpr int KT = kJeffKeyTile, QS = HDP / 4, NB = HDP / 16, PS = KT + 1;
   const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
@@ -1086,7 +1090,7 @@ __device__ __noinline__ void jeff_redo_wave(const JeffArgs *ap, const float *__r
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  jeff_store<HDP, VEC>(a, Gt, OUT, q0, start, ws, O, inv);
+  jeff_store<HDP, VEC>(a, Gt, OUT, q0, start, ws, O, inv, d_lo, d_hi);
 }
 
 // ------------------------------------------------- f32 attention, split head
@@ -1588,6 +1592,7 @@ __global__ __launch_bounds__(256, 4) void jeff_split_f32_kernel(const JeffArgs a
 // ------------------------------------------- f32 attention, fused, hd 256
 
 constexpr int kJeffFusedWaves = 8;  // waves per fused workgroup (the key range's parts)
+constexpr int kJeffHalfMaxL = 4096;  // longest row of the two-workgroup fused kernel
 
 // One kernel for the whole op at hd 256 (no K prep): one workgroup = NW
 // wavefronts = one (row, head, 16-query tile). The RMSNorm scales are
@@ -2000,6 +2005,422 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void jeff_fused_f32_kernel(const J
     for (int v = 1; v < NW; ++v) Of[j] += OM[(v * NB + BPW * wave + j) * 64 + lane] * fac[v];
     Of[j] *= inv;
   }
+  finish(Of);
+}
+
+// ------------------------------------ f32 attention, fused, hd 256, halves
+
+// Grids that fill at most half the CUs (a per-row call is 128 work items):
+// each (row, head, 16-query tile) item runs as two workgroups, blockIdx.z =
+// h, that each compute the item's whole S^T (all 256 features) and its
+// softmax, and P.V and the output for features 128 h .. 128 h + 127 only.
+// The scores are computed twice, but the grid fills twice as many CUs, an
+// item's longest walk on one CU carries 96 instead of 128 MFMAs per key
+// tile, and the two workgroups exchange nothing: each writes its own
+// features, and decides on its own whether its half needs the careful redo.
+// The ring holds one whole tile (six 16-register pieces: K slices 1, 2, 3,
+// 0 and V groups 2h, 2h + 1), and every piece is reloaded with the next
+// tile's as soon as its MFMAs have read it, so each load has a whole tile
+// of the wave's work to land. The eight waves take the key tiles in turn
+// from the diagonal down (wave w: the w-th, (w + 8)-th, ... below it), so a
+// wave's first tile is known from the query tile alone in rows without
+// right padding, and its loads go out with Q's. Layouts, the folded RMSNorm
+// scales, the walk's softmax and the merge are those of
+// jeff_fused_f32_kernel.
+template <int RB, bool TRIM>  // RB: rotated blocks of 16 in the lower half (rot_dim / 32: 0, 1, 2);
+                               // TRIM: a.trim (positions count from the row's first active key)
+__global__ __launch_bounds__(512, 1) void jeff_fused_half_f32_kernel(const JeffArgs a, int rows) {
+  static_assert(RB >= 0 && RB <= 2, "rot_dim 0, 32 or 64");
+  constexpr int NW = 8, HDP = 256, NBH = 8, KT = 16;  // NBH: O^T blocks of the half, one per wave
+  constexpr int OMF = NW * NBH * 64 * 4;  // partial O^T of every wave (the redo's rows too)
+  static_assert(OMF >= 16 * 64 * 4, "the Q operands fit in front of the merge rows");
+  __shared__ __attribute__((aligned(16))) float smem[OMF];
+  __shared__ __attribute__((aligned(16))) float s_wkr[4 * 4 * 4];  // (1 + w_k), rotated blocks
+  __shared__ float s_ssq[4 * 16];
+  __shared__ float s_m[NW * 16], s_l[NW * 16];
+  __shared__ int s_bad;
+  __shared__ uint8_t s_act[kJeffHalfMaxL];  // mask != 0 per key of the row (launcher: L <= this)
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15, grp = lane >> 4;
+  const int L = a.L;
+  const int L4 = 4 * L;
+  const int h = (int)blockIdx.z;  // feature half
+
+  const int qt = (int)gridDim.y - 1 - (int)blockIdx.y;
+  int row, head;
+  jeff_unit_of(a, rows, blockIdx.x, row, head);
+  const int kvh = min((int)a.gdiv.div((uint32_t)head), a.kv_heads - 1);
+  const int q0 = qt * 16, q = q0 + col;
+  const uint32_t bytes = (uint32_t)((size_t)HDP * L * 4);
+  const __amdgpu_buffer_rsrc_t rq = buffer_rsrc(
+      static_cast<const float *>(a.q) + row * a.q_row + (size_t)head * HDP * L, bytes);
+  const __amdgpu_buffer_rsrc_t rg = buffer_rsrc(
+      static_cast<const float *>(a.gate) + row * a.q_row + (size_t)head * HDP * L, bytes);
+  const __amdgpu_buffer_rsrc_t ro =
+      buffer_rsrc(a.out + row * a.q_row + (size_t)head * HDP * L, bytes);
+  const float *Kb = static_cast<const float *>(a.k) + row * a.kv_row + (size_t)kvh * a.kv_head;
+  const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(Kb, bytes);
+  const __amdgpu_buffer_rsrc_t rv = buffer_rsrc(
+      static_cast<const float *>(a.v) + row * a.kv_row + (size_t)kvh * a.kv_head, bytes);
+  const __amdgpu_buffer_rsrc_t rm = buffer_rsrc(a.mask + (size_t)row * L, (uint32_t)L4);
+  // Per-lane byte offsets: feature 4 grp (+ the step's 64s + 16c + e, a
+  // scalar offset) of token col (+ the tile's first token, scalar); past the
+  // buffer's end (read as 0) for a lane with nothing to load.
+  const int ofs_t = (4 * grp * L + col) * 4;
+  const int koob = (int)bytes;
+  const int ofs_q = q < L ? ofs_t : koob;
+
+  // -------- Q slice `wave` (waves 0 .. 3) and its norm weights.
+  const bool prep = wave < 4;
+  const int sw = wave & 3;
+  float xq[16];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      xq[4 * c + e] = buffer_load1(rq, ofs_q, q0 * 4 + (64 * sw + 16 * c + e) * L4);  // waves 4-7: unused
+  const __amdgpu_buffer_rsrc_t rwq = buffer_rsrc(a.q_norm, HDP * 4);
+  const __amdgpu_buffer_rsrc_t rwk = buffer_rsrc(a.k_norm, HDP * 4);
+  f32x4 wq[4], wk[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    wq[c] = buffer_load4(rwq, (64 * sw + 16 * c + 4 * grp) * 4, 0);
+    wk[c] = buffer_load4(rwk, (64 * sw + 16 * c + 4 * grp) * 4, 0);
+  }
+
+  // -------- the ring, the gate, and a first key tile on a guess. Wave w
+  // walks key tiles kt_end - 1 - w, kt_end - 1 - w - NW, ... down to
+  // kt_begin; the span (below) gives kt_end = qt + 1 whenever the row's last
+  // active key is at or past the tile's last query (no right padding), so
+  // the wave's first tile qt - w is loaded with Q, before the span is known,
+  // and loaded again only if the guess was wrong.
+  constexpr int rb = RB, rh = 16 * RB;
+  f32x4 ring[6][4];
+  f32x4 tcs[2], tsn[2];  // the tile's table entries (rotated pairs of key col)
+  auto k_off = [&](int kt) -> int { return kt * KT + col < L ? ofs_t : koob; };
+  auto load_k = [&](int slot, int sl, int kt) {
+    const int vo = k_off(kt);
+    kt = __builtin_amdgcn_readfirstlane(kt);
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        ring[slot][c][e] = buffer_load1(rk, vo, kt * KT * 4 + (64 * sl + 16 * c + e) * L4);
+  };
+  // V: features 16 J + col, keys k0 + 4 grp .. + 3 (L % 4 == 0: all in or out).
+  const int ofs_v = (col * L + 4 * grp) * 4;
+  auto load_v = [&](int slot, int g, int kt) {
+    const int k = kt * KT + 4 * grp;
+    const int vo = k < L ? ofs_v + kt * KT * 4 : koob;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ring[slot][j] = buffer_load4(rv, vo, (4 * g + j) * 16 * L4);
+  };
+  auto load_tile = [&](int kt) {
+    load_k(0, 1, kt);
+    load_k(1, 2, kt);
+    load_k(2, 3, kt);
+    load_k(3, 0, kt);
+    load_v(4, 2 * h, kt);
+    load_v(5, 2 * h + 1, kt);
+  };
+  // o * sigmoid(gate) (lib.rs:755-758) for features 16 (8 h + wave) + 4 grp
+  // + r of query col; 0 for a dropped query (q < start).
+  const int fb = 16 * (NBH * h + wave);
+  float gt[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) gt[r] = buffer_load1(rg, ofs_q, q0 * 4 + (fb + r) * L4);
+  // Q's table entries: at position q, loaded with Q, when nothing is
+  // trimmed; after the span (position q - start) when rows are trimmed.
+  f32x4 qcs[2], qsn[2];
+  auto load_qtab = [&](int pos) {
+#pragma unroll
+    for (int b = 0; b < RB; ++b) {
+      qcs[b] = *reinterpret_cast<const f32x4 *>(a.cos_t + (size_t)pos * rh + 16 * b + 4 * grp);
+      qsn[b] = *reinterpret_cast<const f32x4 *>(a.sin_t + (size_t)pos * rh + 16 * b + 4 * grp);
+    }
+  };
+  if constexpr (!TRIM) load_qtab(min(q, L - 1));
+  // The mask's first 256 keys are loaded before the guessed tile, so that
+  // waiting for them (loads complete in order) does not wait for the tile.
+  const f32x4 mv0 = buffer_load4(rm, 4 * lane * 4, 0);  // past L: 0
+  // Unconditional (tile 0 for a wave past the diagonal), so that the
+  // compiler's waits after it count the same loads on every path.
+  const int guess = max(qt - wave, 0);
+  asm volatile("" ::: "memory");  // keeps the loads above ahead of the tile's
+  load_tile(guess);
+
+  // -------- the row's active span (mask != 0), every wave on its own; wave
+  // 0 also keeps each key's flag in LDS for the walk (read after the Q-prep
+  // barrier), so no load of the walk is waited for out of its order.
+  int first, last;
+  {
+    int lo = 0x7fffffff, hi = -1;
+    for (int k0 = 0; k0 < L; k0 += 256) {
+      const f32x4 mv = k0 == 0 ? mv0 : buffer_load4(rm, (k0 + 4 * lane) * 4, 0);  // past L: 0
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        if (mv[t] != 0.0f) {
+          lo = min(lo, k0 + 4 * lane + t);
+          hi = max(hi, k0 + 4 * lane + t);
+        }
+        if (wave == 0 && k0 + 4 * lane + t < L) s_act[k0 + 4 * lane + t] = mv[t] != 0.0f;
+      }
+    }
+    lo = wave_min(lo);
+    hi = wave_max(hi);
+    first = __builtin_amdgcn_readfirstlane(hi >= 0 ? lo : 0);
+    last = __builtin_amdgcn_readfirstlane(hi);
+  }
+  const int start = (TRIM && last >= 0) ? first : 0;
+  const bool q_live = q < L && q >= start;
+  const int q_last = min(q0 + 15, L - 1);
+  int kt_begin = 0, kt_end = 0;
+  {
+    const int kl = min(last, q_last);
+    if (last >= 0 && first <= kl && q_last >= start) {
+      kt_begin = first / KT;
+      kt_end = kl / KT + 1;
+    }
+  }
+  auto finish = [&](const f32x4 o) {
+    if (q < L) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float x = q < start ? 0.0f : o[r] * fast_sigmoid(gt[r]);
+        buffer_store1_nt(x, ro, ofs_t, q0 * 4 + (fb + r) * L4);
+      }
+    }
+  };
+  if (kt_begin >= kt_end) {  // no key at or before these queries: o = 0 (lib.rs:739-743)
+    finish(f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+    return;
+  }
+  const int kt_first = kt_end - 1 - wave;  // this wave's first tile (none below kt_begin)
+  auto load_tab = [&](int kt) {
+    if (rb > 0) {
+      const int pos = min(max(kt * KT + col - start, 0), L - 1);
+#pragma unroll
+      for (int b = 0; b < rb; ++b) {
+        tcs[b] = *reinterpret_cast<const f32x4 *>(a.cos_t + (size_t)pos * rh + 16 * b + 4 * grp);
+        tsn[b] = *reinterpret_cast<const f32x4 *>(a.sin_t + (size_t)pos * rh + 16 * b + 4 * grp);
+      }
+    }
+  };
+  if (kt_first >= kt_begin) {
+    if (kt_first != guess) load_tile(kt_first);
+    load_tab(kt_first);
+  }
+
+  // -------- Q: x (1 + w_q), RoPE, (1 + w_k) past rot_dim, into LDS; the sum
+  // of squares over the four slices gives scale_q.
+  float ssq = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) ssq += xq[i] * xq[i];
+  ssq += __shfl_xor(ssq, 16);
+  ssq += __shfl_xor(ssq, 32);
+  if (prep && grp == 0) s_ssq[sw * 16 + col] = ssq;
+  float qs[16];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) qs[4 * c + e] = xq[4 * c + e] * (1.0f + wq[c][e]);
+  if constexpr (TRIM) load_qtab(min(max(q - start, 0), L - 1));
+  if (rb > 0 && wave == 0) {  // slice 0 holds the rotated features
+#pragma unroll
+    for (int b = 0; b < rb; ++b) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float x = qs[4 * b + e], y = qs[4 * (b + rb) + e];
+        qs[4 * b + e] = rope_lo(x, y, qcs[b][e], qsn[b][e]);
+        qs[4 * (b + rb) + e] = rope_hi(x, y, qcs[b][e], qsn[b][e]);
+      }
+    }
+  }
+  f32x4 *QL = reinterpret_cast<f32x4 *>(smem);
+  if (prep) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const bool rotated = wave == 0 && c < 2 * rb;
+      f32x4 y;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y[e] = q_live ? qs[4 * c + e] * (rotated ? 1.0f : 1.0f + wk[c][e]) : 0.0f;
+      QL[(sw * 4 + c) * 64 + lane] = y;
+    }
+  }
+  if (wave == 0 && col == 0) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) *reinterpret_cast<f32x4 *>(s_wkr + (c * 4 + grp) * 4) = wk[c] + 1.0f;
+  }
+  __syncthreads();
+  const float c1q =
+      a.c1 * rms_scale(s_ssq[col] + s_ssq[16 + col] + s_ssq[32 + col] + s_ssq[48 + col], HDP, a.eps);
+
+  f32x4 O[4 * 2];  // O^T blocks 8 h .. 8 h + 7 (groups 2h, 2h + 1)
+#pragma unroll
+  for (int j = 0; j < 8; ++j) O[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float m = kNoMax, l = 0.0f;  // l: this lane's share of the row sum
+  bool tainted = false;        // wave-uniform
+
+  // Each piece is reloaded with the next tile's right after its MFMAs; at
+  // the wave's last tile the "next" pieces re-read it (unconditional, so no
+  // ring slot ever holds one of two values).
+  for (int kt = kt_first; kt >= kt_begin; kt -= NW) {
+    const int kn = kt - NW >= kt_begin ? kt - NW : kt;
+    const int k0 = kt * KT;
+    const bool act = k0 + col < L && s_act[k0 + col] != 0;
+    f32x4 s0 = {0.0f, 0.0f, 0.0f, 0.0f}, s1 = {0.0f, 0.0f, 0.0f, 0.0f};
+    float ssk = 0.0f;
+    // S^T over K slices 1, 2, 3 (features past the rotated ones)
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float x = ring[i][c][e];
+          ssk += x * x;
+          const float y = QL[((i + 1) * 4 + c) * 64 + lane][e];
+          if (c & 1)
+            s1 = mfma_16x16x4(x, y, s1);
+          else
+            s0 = mfma_16x16x4(x, y, s0);
+        }
+      load_k(i, i + 1, kn);
+    }
+    // slice 0: sum of squares of the raw key, then x (1 + w_k) and RoPE on
+    // the rotated blocks (0 .. 2 rb - 1)
+    {
+      f32x4(&k)[4] = ring[3];
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ssk += k[c][e] * k[c][e];
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (c < 2 * rb) k[c] *= *reinterpret_cast<const f32x4 *>(s_wkr + (c * 4 + grp) * 4);
+#pragma unroll
+      for (int b = 0; b < rb; ++b) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float x = k[b][e], y = k[b + rb][e];
+          k[b][e] = rope_lo(x, y, tcs[b][e], tsn[b][e]);
+          k[b + rb][e] = rope_hi(x, y, tcs[b][e], tsn[b][e]);
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float y = QL[c * 64 + lane][e];
+          if (c & 1)
+            s1 = mfma_16x16x4(k[c][e], y, s1);
+          else
+            s0 = mfma_16x16x4(k[c][e], y, s0);
+        }
+    }
+    load_k(3, 0, kn);
+    load_tab(kn);
+    // the key's scale (lanes col hold key col), to the S^T rows 4 grp + r
+    ssk += __shfl_xor(ssk, 16);
+    ssk += __shfl_xor(ssk, 32);
+    const float sck = rms_scale(ssk, HDP, a.eps);
+    const uint32_t abits = (uint32_t)__ballot(act && k0 + col >= start) & 0xffffu;
+    const uint32_t w = q_live ? (abits & range_bits(0, q - k0)) : 0u;
+    f32x4 s = s0 + s1;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s[r] *= c1q * __shfl(sck, 4 * grp + r);
+    if (__ballot(q_live && w != 0xffffu) != 0) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s[r] = ((w >> (4 * grp + r)) & 1u) ? s[r] : -INFINITY;
+    }
+    f32x4 ex;
+    float rs = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      ex[r] = fast_exp2(s[r] - m);
+      rs += ex[r];
+    }
+    if (__builtin_expect(__ballot(q_live && !(rs <= kLazyLimit)) != 0, 0)) {
+      const float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+      const float mxs = pair_max(pair16_max(mx));
+      const float mn = mxs > m + kRescaleSlack ? mxs : m;
+      rs = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        ex[r] = fast_exp2(s[r] - mn);
+        rs += ex[r];
+      }
+      if (__ballot(q_live && !__builtin_isfinite(rs)) != 0) {
+        tainted = true;
+      } else {
+        const float alpha = fast_exp2(m - mn);  // exactly 1 where the reference stays
+#pragma unroll
+        for (int j = 0; j < 8; ++j) O[j] *= alpha;
+        l *= alpha;
+        m = mn;
+      }
+    }
+    l += rs;
+    // P.V: the half's V groups in slots 4, 5, each reloaded after its MFMAs.
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          O[4 * g + j] = mfma_16x16x4(ring[4 + g][j][r], ex[r], O[4 * g + j]);
+      load_v(4 + g, 2 * h + g, kn);
+    }
+    if (tainted) break;  // wave-uniform; the half is redone below
+  }
+
+  // -------- careful redo (rare): a wave's scores, or this half's O, went
+  // non-finite; one wave redoes the tile with the reference's exact
+  // semantics and stores this half's features.
+  if (tid == 0) s_bad = 0;
+  __syncthreads();
+  bool bad = tainted;
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) bad |= q_live && !__builtin_isfinite(O[j][r]);
+  if (__ballot(bad) != 0 && lane == 0) s_bad = 1;
+  __syncthreads();
+  if (s_bad != 0) {
+    if (wave == 0)
+      jeff_redo_wave<HDP, true, 2>(kernel_jeff_args(), nullptr, row, head, q0, kt_begin, kt_end,
+                                   start, smem, 128 * h, 128 * h + 128);
+    return;
+  }
+
+  // -------- merge: O = sum_w 2^(m_w - M) O_w / sum_w 2^(m_w - M) l_w; wave w
+  // finishes O^T block 8 h + w. Every wave is past its walk (the barrier
+  // above), so OM may cover the Q rows.
+  f32x4 *OM = reinterpret_cast<f32x4 *>(smem);
+#pragma unroll
+  for (int j = 0; j < NBH; ++j) OM[(wave * NBH + j) * 64 + lane] = O[j];
+  const float lt = pair_sum(pair16_sum(l));
+  if (grp == 0) {
+    s_m[wave * 16 + col] = m;
+    s_l[wave * 16 + col] = lt;
+  }
+  __syncthreads();
+  float M = s_m[col];
+#pragma unroll
+  for (int v = 1; v < NW; ++v) M = fmaxf(M, s_m[v * 16 + col]);
+  float fac[NW], lsum = 0.0f;
+#pragma unroll
+  for (int v = 0; v < NW; ++v) {
+    fac[v] = fast_exp2(s_m[v * 16 + col] - M);  // 0 for a wave without keys (m = kNoMax)
+    lsum += fac[v] * s_l[v * 16 + col];
+  }
+  const float inv = lsum > 0.0f ? fast_rcp(lsum) : 0.0f;
+  f32x4 Of = OM[wave * 64 + lane] * fac[0];
+#pragma unroll
+  for (int v = 1; v < NW; ++v) Of += OM[(v * NBH + wave) * 64 + lane] * fac[v];
+  Of *= inv;
   finish(Of);
 }
 
@@ -2458,6 +2879,19 @@ static hipError_t launch_jeff_f32_hd(const JeffArgs &a, int rows, float *kp, hip
     const int rb = a.cos_t == nullptr ? 0 : (a.rot_half % 16 == 0 ? a.rot_half / 16 : -1);
     const long items = (long)nq * rows * a.heads;
     const bool div_ok = (uint64_t)rows * a.heads * a.heads <= ((uint64_t)1 << 32);
+    // Grids of at most half the CUs (one C4 row per call) run each item as
+    // two workgroups, one per half of the output features.
+    if (vec && div_ok && a.hd == 256 && rb >= 0 && rb <= 2 && a.L <= kJeffHalfMaxL &&
+        2 * items <= (a.cus > 0 ? a.cus : 1)) {
+      const dim3 hgrid((unsigned)(rows * a.heads), (unsigned)nq, 2u);
+      void (*const kern[3][2])(JeffArgs, int) = {
+          {jeff_fused_half_f32_kernel<0, false>, jeff_fused_half_f32_kernel<0, true>},
+          {jeff_fused_half_f32_kernel<1, false>, jeff_fused_half_f32_kernel<1, true>},
+          {jeff_fused_half_f32_kernel<2, false>, jeff_fused_half_f32_kernel<2, true>}};
+      hipExtLaunchKernelGGL(kern[rb][a.trim ? 1 : 0], hgrid, dim3(512), 0, stream, ev.start,
+                            ev.stop, 0, a, rows);
+      return hipGetLastError();
+    }
     if (vec && div_ok && a.hd == 256 && rb >= 0 && rb <= 2 &&
         items <= 2L * (a.cus > 0 ? a.cus : 1)) {
       constexpr int NW = kJeffFusedWaves;
